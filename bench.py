@@ -1,0 +1,277 @@
+"""W4A16 (AutoAWQ GEMM, group 128) linear benchmark on one MI355X.
+
+Headline (`value`): decode-regime aggregate HBM GB/s over the Qwen3-8B projection
+shapes (QKV 4096x6144, O 4096x4096, gate_up 4096x24576, down 12288x4096) at packed
+M in {1, 4, 8, 16}: sum of algorithmic bytes / sum of kernel time.  One "step" is one
+GEMM at each of those 16 points.  Also reported: M = 32 and 64, the chunked-prefill
+TFLOP/s at M = 2048 (1% of input channels x20), and the oracle CPU baseline on the
+host cores.
+
+Method
+  * Inputs are resident in HBM before timing.  Weights are random uniform int32 words
+    (= uniform int4 q), zero words likewise, bf16 scales uniform in [0.002, 0.02],
+    bf16 activations ~N(0, 1); weight copies rotate so that every launch of a point
+    streams a different copy and the copies of one point exceed 2 x 256 MB (the
+    Infinity Cache), i.e. decode bytes come from HBM.
+  * Each point's launches are captured once in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed; HIP events recorded on the replay stream bracket each replay, giving the
+    average kernel duration with host launch overhead removed.
+  * Algorithmic bytes per GEMM = K N / 2 + K N / 256 + K N / 64 + 2 M K + 2 M N
+    (int4 weights, int32 zeros, bf16 scales, bf16 x and y); flops = 2 M N K.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "W4A16 GEMM HBM GB/s (M≤16) and TFLOP/s (M=2048), Qwen3-8B shapes"
+SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+DECODE_M = (1, 4, 8, 16)
+EXTRA_DECODE_M = (32, 64)
+PREFILL_M = 2048
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+CACHE_BYTES = 256 * 2 ** 20
+
+
+def algorithmic_bytes(m: int, k: int, n: int) -> int:
+    return k * n // 2 + k * n // 256 + k * n // 64 + 2 * m * k + 2 * m * n
+
+
+def weight_bytes(k: int, n: int) -> int:
+    return k * n // 2 + k * n // 256 + k * n // 64
+
+
+class Point:
+    """One (shape, M) GEMM with its rotating weight copies, captured as one HIP graph."""
+
+    def __init__(self, lib, name, m, k, n, weights, x):
+        self.name, self.m, self.k, self.n = name, m, k, n
+        dev = x.device
+        self.weights = weights
+        self.x = x
+        self.y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        ws_bytes = lib.workspace_bytes(m, k, n)
+        self.ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        self.ws_len = ws_bytes
+        self.lib = lib
+        self.regime = lib.regime(m, k, n)
+        self.split = lib.split_k(m, k, n)
+        self.graph = None
+
+    def launch_all(self, stream_ptr):
+        dll = self.lib.dll
+        for packed, qzeros, scales in self.weights:
+            rc = dll.w4a16_gemm(self.x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                self.y.data_ptr(), self.m, self.k, self.n, 128,
+                                self.ws.data_ptr() if self.ws_len else None, self.ws_len, stream_ptr)
+            if rc != 0:
+                raise RuntimeError(f"w4a16_gemm failed at {self.name} M={self.m}: {self.lib.last_error()}")
+
+    def capture(self, stream):
+        with torch.cuda.stream(stream):
+            self.launch_all(stream.cuda_stream)  # warm-up outside the graph
+        stream.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=stream):
+            self.launch_all(stream.cuda_stream)
+
+    @property
+    def launches(self) -> int:
+        return len(self.weights)
+
+
+def make_weights(k, n, copies, dev, seed):
+    """`copies` independent AWQ weight sets in the kernel layout (random words = uniform int4)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    out = []
+    for _ in range(copies):
+        packed = torch.randint(-2 ** 31, 2 ** 31 - 1, (k * n // 8,), dtype=torch.int32, device=dev, generator=gen)
+        qzeros = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 128, n // 8), dtype=torch.int32, device=dev,
+                               generator=gen)
+        scales = (torch.rand((k // 128, n), device=dev, generator=gen) * 0.018 + 0.002).to(torch.bfloat16)
+        out.append((packed, qzeros, scales))
+    return out
+
+
+def build_points(lib, ms, dev, seed0=0, min_bytes=2 * CACHE_BYTES):
+    """Decode points; the copies of one shape are shared by its M values and together
+    exceed `min_bytes`, so consecutive launches never find their weights in cache."""
+    points = []
+    for si, (name, (k, n)) in enumerate(SHAPES.items()):
+        copies = max(2, -(-min_bytes // weight_bytes(k, n)))
+        weights = make_weights(k, n, copies, dev, seed0 + 7919 * si)
+        for m in ms:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(seed0 + 1000 * si + m)
+            x = torch.randn((m, k), device=dev, generator=gen).to(torch.bfloat16)
+            points.append(Point(lib, name, m, k, n, weights, x))
+    return points
+
+
+def time_points(points, stream, steps, warmup):
+    """Replay every point's graph `warmup` times untimed, then `steps` times timed.
+    Returns (per-point mean launch ms, total timed ms)."""
+    for p in points:
+        p.capture(stream)
+    for _ in range(warmup):
+        for p in points:
+            p.graph.replay()
+    torch.cuda.synchronize()
+    per_point = {id(p): [] for p in points}
+    events = []
+    start_all = torch.cuda.Event(enable_timing=True)
+    end_all = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start_all.record(stream)
+        for _ in range(steps):
+            for p in points:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                p.graph.replay()
+                e1.record(stream)
+                events.append((p, e0, e1))
+        end_all.record(stream)
+    torch.cuda.synchronize()
+    for p, e0, e1 in events:
+        per_point[id(p)].append(e0.elapsed_time(e1) / p.launches)
+    return {id(p): statistics.mean(v) for p, v in ((p, per_point[id(p)]) for p in points)}, \
+        start_all.elapsed_time(end_all)
+
+
+def cpu_baseline(seconds_budget: float = 20.0) -> dict:
+    """The oracle (numpy restatement of the reference backend: dequant to bf16, then an
+    fp32 BLAS matmul, then bf16) on the host at M=16, K=N=4096 (the O projection)."""
+    from oracle import awq_oracle as ora
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        threads = os.cpu_count() or 1
+    m, k, n = 16, 4096, 4096
+    p = ora.make_problem(seed=0, m=m, k=k, n=n)
+    run = lambda: ora.awq_linear_bf16_bits(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)  # noqa: E731
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < seconds_budget and len(times) < 20):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > seconds_budget and len(times) >= 3:
+            break
+    t = statistics.median(times)
+    return {"value": round(algorithmic_bytes(m, k, n) / t / 1e9, 3), "unit": "GB/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"oracle dequant+fp32 matmul, M={m} K={k} N={n} (O proj), median of {len(times)} runs, "
+                      f"{t * 1e3:.1f} ms/GEMM, host {platform.processor() or platform.machine()}, "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--details", action="store_true", help="print one line per point to stderr")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no multi-GPU "
+              f"component: each GPU runs its own layers' GEMMs)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    pkg = importlib.import_module("llm-serve_amd")
+    lib = pkg.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+
+    decode_points = build_points(lib, DECODE_M + EXTRA_DECODE_M, dev)
+    per_launch, _ = time_points(decode_points, stream, args.steps, args.warmup)
+    head = [p for p in decode_points if p.m in DECODE_M]
+    bytes_head = sum(algorithmic_bytes(p.m, p.k, p.n) for p in head)
+    ms_head = sum(per_launch[id(p)] for p in head)
+    value = bytes_head / (ms_head * 1e-3) / 1e9
+    points_out = []
+    for p in decode_points:
+        ms = per_launch[id(p)]
+        gbs = algorithmic_bytes(p.m, p.k, p.n) / (ms * 1e-3) / 1e9
+        points_out.append({"shape": p.name, "M": p.m, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "split": p.split, "copies": p.launches})
+        if args.details:
+            print(f"decode {p.name:8s} M={p.m:3d} {ms * 1e3:8.2f} us  {gbs:8.1f} GB/s  split={p.split}",
+                  file=sys.stderr)
+    del decode_points
+
+    prefill = None
+    if not args.no_prefill:
+        pts = []
+        for si, (name, (k, n)) in enumerate(SHAPES.items()):
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(99 + si)
+            x = torch.randn((PREFILL_M, k), device=dev, generator=gen)
+            cols = torch.randperm(k, device=dev, generator=gen)[: round(0.01 * k)]
+            x[:, cols] *= 20.0
+            pts.append(Point(lib, name, PREFILL_M, k, n, make_weights(k, n, 2, dev, 500 + si), x.to(torch.bfloat16)))
+        pl, _ = time_points(pts, stream, max(3, args.steps // 4), 1)
+        prefill = {}
+        for p in pts:
+            ms = pl[id(p)]
+            tf = 2 * p.m * p.n * p.k / (ms * 1e-3) / 1e12
+            prefill[p.name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                               "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "split": p.split}
+            if args.details:
+                print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
+        del pts
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    avg_bytes = bytes_head / len(head)
+    avg_ms = ms_head / len(head)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_head, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode sweep: AWQ W4A16 GEMM, group 128, M in {1,4,8,16} x Qwen3-8B "
+                               "QKV 4096x6144, O 4096x4096, gate_up 4096x24576, down 12288x4096",
+                   "group_size": 128, "weights_rotated_bytes_per_point": ">= 512 MiB"},
+        "roofline": {"bound": "hbm", "achieved": round(avg_bytes / (avg_ms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(avg_bytes / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "prefill_m2048": prefill,
+        "points": points_out,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,125 @@
+/*
+ * w4a16.h -- C ABI of the MI355X (gfx950) W4A16 linear library (libw4a16.so).
+ *
+ * Weight format consumed: AutoAWQ "GEMM" version, 4-bit, zero point, group 128:
+ *   qweight int32 [K, N/8]   nibble i of word [k, j] holds column 8j + (0,2,4,6,1,3,5,7)[i]
+ *   qzeros  int32 [K/128, N/8] same nibble order
+ *   scales  bf16  [K/128, N]
+ *   W[k, n] = bf16_rne( (q[k, n] - z[k/128, n]) * s[k/128, n] )
+ * Activations x bf16 [M, K] row-major, output y bf16 [M, N] row-major.
+ *
+ * Conventions
+ *   - Every tensor pointer is a device pointer owned by the caller; the library never
+ *     allocates.  bf16 data is passed as uint16_t bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls only enqueue
+ *     work; nothing synchronises the host.
+ *   - Return 0 on success, otherwise a W4A16_ERR_* code; w4a16_last_error() then gives a
+ *     thread-local message.  No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (HGinkgo/LLM-Serve):
+ *   pybind module of llmserve/layers/quantization/csrc/awq_w4a16.cu:375-379
+ *     (repack_qweight, reorder_qzeros, linear) and its Python wrappers in
+ *     llmserve/layers/quantization/awq_cuda.py:17-185, plus the reference backend
+ *     functions of llmserve/layers/quantization/awq.py:184-276.
+ */
+#ifndef W4A16_H_
+#define W4A16_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_ABI_VERSION 1
+
+enum w4a16_status {
+  W4A16_OK = 0,
+  W4A16_ERR_ARG = 1,       /* null pointer or non-positive size */
+  W4A16_ERR_SHAPE = 2,     /* K / N / group contract violated */
+  W4A16_ERR_ALIGN = 3,     /* a pointer is not aligned as the kernel requires */
+  W4A16_ERR_WORKSPACE = 4, /* workspace missing or smaller than w4a16_workspace_bytes */
+  W4A16_ERR_LAUNCH = 5     /* hipGetLastError() reported a launch failure */
+};
+
+/* Kernel families reported by w4a16_regime(). */
+enum w4a16_regime_id {
+  W4A16_REGIME_NONE = 0,   /* M == 0: nothing to launch */
+  W4A16_REGIME_DECODE = 1, /* M <= 64: split-K, HBM-bound kernel */
+  W4A16_REGIME_TILE = 2    /* M > 64: LDS-tiled bf16 MFMA GEMM */
+};
+
+/* ABI version of the loaded library (W4A16_ABI_VERSION). No reference counterpart. */
+int w4a16_abi_version(void);
+
+/* Thread-local text of the last error on this thread ("" if none).
+ * Replaces the TORCH_CHECK messages of awq_w4a16.cu:249-334. */
+const char* w4a16_last_error(void);
+
+/* Unpack int32 [R, C] AWQ words into int32 [R, 8C] in logical column order.
+ * Replaces unpack_awq_int4 (awq.py:184-200).  Requires R, C > 0. */
+int w4a16_unpack_int4(const int32_t* packed, int32_t* out, int rows, int cols, void* stream);
+
+/* Dequantize the AutoAWQ tensors into bf16 W [K, N], bit-exact with the reference.
+ * Replaces dequantize_awq_gemm (awq.py:235-248).  Any group_size > 0 dividing K; N % 8 == 0. */
+int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                  uint16_t* w_out, int K, int N, int group_size, void* stream);
+
+/* Rewrite qweight [K, N/8] into the gfx950 MFMA fragment layout consumed by w4a16_gemm
+ * (same byte size: K*N/2).  One 1 KiB block per (128-row group g, 16-column tile t):
+ * word [(g*(N/16) + t)*256 + lane*4 + j] holds the 8 values k = 128g + 32j + 8(lane/16) + i,
+ * n = 16t + lane%16, value i at bit 4*(0,4,1,5,2,6,3,7)[i].  K % 128 == 0, N % 16 == 0.
+ * Replaces repack_qweight (awq_w4a16.cu:81-109, 256-272) / repack_awq_qweight_cuda
+ * (awq_cuda.py:129-132).  qzeros need no reorder: the kernels read them as stored, so
+ * reorder_qzeros (awq_w4a16.cu:111-118, 274-286) has no counterpart. */
+int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, void* stream);
+
+/* Dequantize from the repacked layout (same bits as w4a16_dequant).  Uses the dequant
+ * routine of the MFMA tile GEMM; exists to verify both bit-exactly.  No reference
+ * counterpart beyond dequantize_awq_gemm (awq.py:235-248). */
+int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                         uint16_t* w_out, int K, int N, int group_size, void* stream);
+
+/* Bytes of workspace w4a16_gemm needs for this problem (0 = none).  The workspace must be
+ * zero-filled once when first allocated; the kernels leave its counter words at zero.
+ * Two GEMMs in flight at the same time must not share one workspace.
+ * Replaces the workspace sizing of awq.py:168-180 and awq_cuda.py:157-176. */
+size_t w4a16_workspace_bytes(int M, int K, int N, int group_size);
+
+/* y[M, N] = x[M, K] @ W with W given as (packed, qzeros, scales); bf16 in and out, fp32
+ * accumulation.  M >= 0 (M == 0 is a no-op), K % 128 == 0, N % 64 == 0, group_size == 128;
+ * x, packed, y 16-byte aligned.
+ * Replaces linear (awq_w4a16.cu:288-371) / awq_cuda_linear (awq_cuda.py:141-185) and the
+ * reference backend awq_reference_linear (awq.py:251-276). */
+int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+               const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel family w4a16_gemm launches for (M, K, N): a w4a16_regime_id.
+ * Replaces the dispatch rule of select_awq_cuda_split_k (awq_cuda.py:17-26) and
+ * AWQLinearMethod.apply (awq.py:115-154) as the thing a caller can query. */
+int w4a16_regime(int M, int K, int N);
+
+/* Number of K splits w4a16_gemm uses for (M, K, N) (1 = no cross-workgroup reduction).
+ * Counterpart of select_awq_cuda_split_k (awq_cuda.py:17-26). */
+int w4a16_split_k(int M, int K, int N);
+
+/* w4a16_gemm with the kernel configuration forced instead of chosen: regime
+ * W4A16_REGIME_DECODE (p0 = column tiles per workgroup in {1,2,4}, p1 = waves per
+ * workgroup in {4,8,16}, M <= 64) or W4A16_REGIME_TILE (p0 = 16-row tiles per wave in
+ * {8,16}); 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook
+ * (it exercises every split-K reduction path at small sizes). */
+int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                      const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
+                      int regime, int p0, int p1, int split, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Workspace bytes w4a16_gemm_config needs for that configuration.  No reference counterpart. */
+size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_H_ */

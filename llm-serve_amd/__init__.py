@@ -1,0 +1,33 @@
+"""MI355X (gfx950) W4A16 linear layer for AutoAWQ-GEMM checkpoints.
+
+The package directory name contains a hyphen; import it with
+``importlib.import_module("llm-serve_amd")``.  Compute runs only in the HIP library
+``csrc/libw4a16.so`` (C ABI in include/w4a16.h); the Python side validates arguments,
+owns device memory through torch, and mirrors the reference's operator interface.
+"""
+from ._lib import REGIME_DECODE, REGIME_NONE, REGIME_TILE, W4A16Error, W4A16Library, lib
+from .layers.quantization.awq import (
+    AWQLinearMethod,
+    AWQRuntimeConfig,
+    awq_linear,
+    awq_regime,
+    dequantize_awq_gemm,
+    repack_awq_qweight,
+    unpack_awq_int4,
+)
+
+__all__ = (
+    "AWQLinearMethod",
+    "AWQRuntimeConfig",
+    "REGIME_DECODE",
+    "REGIME_NONE",
+    "REGIME_TILE",
+    "W4A16Error",
+    "W4A16Library",
+    "awq_linear",
+    "awq_regime",
+    "dequantize_awq_gemm",
+    "lib",
+    "repack_awq_qweight",
+    "unpack_awq_int4",
+)

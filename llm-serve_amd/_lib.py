@@ -1,0 +1,171 @@
+"""ctypes binding of libw4a16.so, the C ABI declared in include/w4a16.h.
+
+torch is imported first on purpose: libw4a16.so needs ``libamdhip64.so.7`` and must bind to
+the HIP runtime torch already loaded (same soname), so both share one device context and
+torch's streams are valid handles for the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "csrc", "libw4a16.so")
+
+REGIME_NONE = 0
+REGIME_DECODE = 1
+REGIME_TILE = 2
+
+_c_int = ctypes.c_int
+_c_size = ctypes.c_size_t
+_c_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/w4a16.h
+_SIGNATURES = {
+    "w4a16_abi_version": (_c_int, []),
+    "w4a16_last_error": (ctypes.c_char_p, []),
+    "w4a16_unpack_int4": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_dequant": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr]),
+    "w4a16_repack_qweight": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_dequant_packed": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr]),
+    "w4a16_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "w4a16_gemm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+                            _c_ptr, _c_size, _c_ptr]),
+    "w4a16_regime": (_c_int, [_c_int, _c_int, _c_int]),
+    "w4a16_split_k": (_c_int, [_c_int, _c_int, _c_int]),
+    "w4a16_gemm_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+                                   _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+    "w4a16_workspace_bytes_config": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+}
+ABI_VERSION = 1
+
+
+class W4A16Error(RuntimeError):
+    """A nonzero status returned through the C ABI."""
+
+
+class W4A16Library:
+    """Thin typed wrapper over the C ABI.  Tensor-level methods take torch tensors on the
+    GPU, allocate nothing but their outputs, and launch on the current torch stream."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"W4A16 HIP library not built: {path} is missing (run __graft_entry__.build())")
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(self.dll, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = self.dll.w4a16_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libw4a16.so ABI version {version}, expected {ABI_VERSION}")
+
+    # ------------------------------------------------------------------ plumbing
+    def last_error(self) -> str:
+        return (self.dll.w4a16_last_error() or b"").decode()
+
+    def check(self, status: int, what: str) -> None:
+        if status != 0:
+            raise W4A16Error(f"{what} failed (status {status}): {self.last_error()}")
+
+    @staticmethod
+    def _stream(t: torch.Tensor) -> int:
+        return torch.cuda.current_stream(t.device).cuda_stream
+
+    @staticmethod
+    def _require_gpu(*tensors: torch.Tensor) -> None:
+        for t in tensors:
+            if t.device.type != "cuda":
+                raise ValueError("W4A16 HIP kernels require GPU (HIP) tensors")
+
+    # ------------------------------------------------------------ host queries
+    def workspace_bytes(self, m: int, k: int, n: int, group_size: int = 128) -> int:
+        return int(self.dll.w4a16_workspace_bytes(m, k, n, group_size))
+
+    def workspace_bytes_config(self, m: int, n: int, regime: int, p0: int, split: int) -> int:
+        return int(self.dll.w4a16_workspace_bytes_config(m, n, regime, p0, split))
+
+    def regime(self, m: int, k: int, n: int) -> int:
+        return int(self.dll.w4a16_regime(m, k, n))
+
+    def split_k(self, m: int, k: int, n: int) -> int:
+        return int(self.dll.w4a16_split_k(m, k, n))
+
+    # ---------------------------------------------------------- tensor methods
+    def unpack_int4(self, packed: torch.Tensor) -> torch.Tensor:
+        self._require_gpu(packed)
+        rows, cols = packed.shape
+        out = torch.empty((rows, cols * 8), dtype=torch.int32, device=packed.device)
+        with torch.cuda.device(packed.device):
+            self.check(self.dll.w4a16_unpack_int4(packed.data_ptr(), out.data_ptr(), rows, cols,
+                                                  self._stream(packed)), "w4a16_unpack_int4")
+        return out
+
+    def dequant(self, qweight, qzeros, scales, group_size: int) -> torch.Tensor:
+        self._require_gpu(qweight, qzeros, scales)
+        k, n = qweight.shape[0], qweight.shape[1] * 8
+        out = torch.empty((k, n), dtype=torch.bfloat16, device=qweight.device)
+        with torch.cuda.device(qweight.device):
+            self.check(self.dll.w4a16_dequant(qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                              out.data_ptr(), k, n, group_size, self._stream(qweight)),
+                       "w4a16_dequant")
+        return out
+
+    def repack_qweight(self, qweight: torch.Tensor) -> torch.Tensor:
+        self._require_gpu(qweight)
+        k, n = qweight.shape[0], qweight.shape[1] * 8
+        out = torch.empty((k * n // 8,), dtype=torch.int32, device=qweight.device)
+        with torch.cuda.device(qweight.device):
+            self.check(self.dll.w4a16_repack_qweight(qweight.data_ptr(), out.data_ptr(), k, n,
+                                                     self._stream(qweight)), "w4a16_repack_qweight")
+        return out
+
+    def dequant_packed(self, packed, qzeros, scales, k: int, n: int, group_size: int = 128) -> torch.Tensor:
+        self._require_gpu(packed, qzeros, scales)
+        out = torch.empty((k, n), dtype=torch.bfloat16, device=packed.device)
+        with torch.cuda.device(packed.device):
+            self.check(self.dll.w4a16_dequant_packed(packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                                     out.data_ptr(), k, n, group_size, self._stream(packed)),
+                       "w4a16_dequant_packed")
+        return out
+
+    def gemm(self, x, packed, qzeros, scales, y, k: int, n: int, workspace: torch.Tensor | None,
+             group_size: int = 128) -> torch.Tensor:
+        """y[M, N] = x[M, K] @ W; every tensor already on one GPU, contiguous."""
+        m = x.shape[0]
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_gemm(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                           y.data_ptr(), m, k, n, group_size, ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm")
+        return y
+
+    def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,
+                    split: int, workspace: torch.Tensor | None, group_size: int = 128) -> torch.Tensor:
+        m = x.shape[0]
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_gemm_config(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                  scales.data_ptr(), y.data_ptr(), m, k, n, group_size, regime,
+                                                  p0, p1, split, ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm_config")
+        return y
+
+
+_LOCK = threading.Lock()
+_LIB: W4A16Library | None = None
+
+
+def lib() -> W4A16Library:
+    """The process-wide library handle (loaded on first use; raises if it is not built)."""
+    global _LIB
+    with _LOCK:
+        if _LIB is None:
+            _LIB = W4A16Library()
+        return _LIB

@@ -1,0 +1,256 @@
+// extern "C" entry points of libw4a16.so (declared in include/w4a16.h): argument
+// validation, kernel choice, workspace layout and thread-local error text.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/w4a16.h"
+#include "w4a16_common.h"
+#include "w4a16_launch.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return W4A16_OK;
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+constexpr int kDecodeMaxM = 64;
+constexpr size_t kDecodeMaxLds = 64 * 1024;  // LDS of the decode kernel's wave reduction
+
+// LDS the decode kernel's cross-wave reduction needs: one f32x4 per lane per (wave, m-block, tile).
+size_t decode_lds_bytes(int M, int tn, int waves) {
+  return static_cast<size_t>(waves) * ((M + 15) / 16) * tn * 64 * 16;
+}
+
+// Kernel configuration for one GEMM problem.
+struct GemmPlan {
+  int regime;  // w4a16_regime_id
+  int p0;      // decode: column tiles per workgroup; tile: wm (16-row tiles per wave)
+  int p1;      // decode: waves per workgroup; tile: unused
+  int split;   // K splits (1 = none)
+};
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Decode regime: pick the workgroup width and K split so that the grid covers the 256
+// CUs about twice over while keeping the fp32 partial traffic (split * M * N * 8 bytes)
+// small against the weight stream (K * N / 2 bytes).
+GemmPlan plan_decode(int M, int K, int N) {
+  const int G = K / w4a16::kGroup;
+  GemmPlan p{W4A16_REGIME_DECODE, 4, 4, 1};
+  const int target = 512;
+  int tn = 4;
+  if (N / 64 < 256) tn = 2;
+  if (N / 32 < 128) tn = 1;
+  const int blocks = N / (16 * tn);
+  int split = ceil_div(target, blocks);
+  const int waves = 4;  // decode_lds_bytes(64, 4, 4) = 64 KiB: always within kDecodeMaxLds
+  split = split > G / waves ? G / waves : split;
+  if (split < 1) split = 1;
+  p.p0 = tn;
+  p.p1 = waves;
+  p.split = split;
+  (void)M;
+  return p;
+}
+
+GemmPlan plan_tile(int M, int K, int N) {
+  const int G = K / w4a16::kGroup;
+  GemmPlan p{W4A16_REGIME_TILE, 16, 0, 1};
+  const int wm = M <= 128 ? 8 : 16;
+  const int tiles = ceil_div(M, 16 * wm) * ceil_div(N, 256);
+  int split = 1;
+  while (tiles * split < 200 && split * 2 <= G / 4) split *= 2;
+  p.p0 = wm;
+  p.split = split;
+  return p;
+}
+
+GemmPlan plan(int M, int K, int N) {
+  if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 1};
+  return M <= kDecodeMaxM ? plan_decode(M, K, N) : plan_tile(M, K, N);
+}
+
+// Workspace layout: [arrival counters: kCounterBytes][fp32 partials: split * M * N].
+// The counters sit at a fixed offset so that a workspace shared by calls of different
+// shapes always presents zeroed counters (every kernel re-arms the ones it used).
+constexpr size_t kCounterBytes = 64 * 1024;
+constexpr size_t kMaxCounters = kCounterBytes / sizeof(int);
+
+size_t counters_needed(const GemmPlan& p, int M, int N) {
+  if (p.regime == W4A16_REGIME_DECODE) return static_cast<size_t>(N / 16);
+  return static_cast<size_t>(ceil_div(M, 16 * p.p0)) * ceil_div(N, 256);
+}
+
+size_t workspace_for(const GemmPlan& p, int M, int N) {
+  if (p.regime == W4A16_REGIME_NONE || p.split <= 1) return 0;
+  return kCounterBytes + static_cast<size_t>(p.split) * M * N * sizeof(float);
+}
+
+int validate_gemm(const void* x, const void* packed, const void* qzeros, const void* scales, const void* y, int M,
+                  int K, int N, int group_size) {
+  if (M < 0 || K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "M must be >= 0 and K, N positive (got M=%d K=%d N=%d)", M, K, N);
+  if (group_size != w4a16::kGroup)
+    return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
+  if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
+  if (N % 64) return fail(W4A16_ERR_SHAPE, "N must be divisible by 64 (got %d)", N);
+  if (M == 0) return ok();
+  if (!x || !packed || !qzeros || !scales || !y) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(y, 16))
+    return fail(W4A16_ERR_ALIGN, "x, packed qweight and y must be 16-byte aligned");
+  if (!aligned(qzeros, 4) || !aligned(scales, 2)) return fail(W4A16_ERR_ALIGN, "qzeros/scales misaligned");
+  return ok();
+}
+
+int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+             const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
+             hipStream_t stream) {
+  if (p.regime == W4A16_REGIME_NONE) return ok();
+  const size_t need = workspace_for(p, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(W4A16_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if (need > 0 && !aligned(workspace, 256)) return fail(W4A16_ERR_ALIGN, "workspace must be 256-byte aligned");
+  if (need > 0 && counters_needed(p, M, N) > kMaxCounters)
+    return fail(W4A16_ERR_SHAPE, "split-K needs %zu arrival counters (limit %zu)", counters_needed(p, M, N),
+                kMaxCounters);
+  int* counters = need ? static_cast<int*>(workspace) : nullptr;
+  float* partials = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
+  const uint32_t* pk = reinterpret_cast<const uint32_t*>(packed);
+  const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
+  if (p.regime == W4A16_REGIME_DECODE)
+    return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p1,
+                                                 p.split, stream),
+                        "decode");
+  return check_launch(w4a16::launch_tile_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.split, stream),
+                      "tile");
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
+
+const char* w4a16_last_error(void) { return g_error; }
+
+int w4a16_unpack_int4(const int32_t* packed, int32_t* out, int rows, int cols, void* stream) {
+  if (rows <= 0 || cols <= 0) return fail(W4A16_ERR_ARG, "rows and cols must be positive");
+  if (!packed || !out) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(packed, 4) || !aligned(out, 16)) return fail(W4A16_ERR_ALIGN, "out must be 16-byte aligned");
+  return check_launch(w4a16::launch_unpack(reinterpret_cast<const uint32_t*>(packed), out, rows, cols,
+                                           static_cast<hipStream_t>(stream)),
+                      "unpack");
+}
+
+int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales, uint16_t* w_out, int K,
+                  int N, int group_size, void* stream) {
+  if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
+  if (group_size <= 0) return fail(W4A16_ERR_SHAPE, "group_size must be positive");
+  if (K % group_size) return fail(W4A16_ERR_SHAPE, "K must be divisible by group_size");
+  if (N % 8) return fail(W4A16_ERR_SHAPE, "N must be divisible by 8");
+  if (!qweight || !qzeros || !scales || !w_out) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(scales, 16) || !aligned(w_out, 16) || !aligned(qweight, 4) || !aligned(qzeros, 4))
+    return fail(W4A16_ERR_ALIGN, "scales and w_out must be 16-byte aligned");
+  return check_launch(w4a16::launch_dequant(reinterpret_cast<const uint32_t*>(qweight),
+                                            reinterpret_cast<const uint32_t*>(qzeros), scales, w_out, K, N,
+                                            group_size, static_cast<hipStream_t>(stream)),
+                      "dequant");
+}
+
+int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, void* stream) {
+  if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
+  if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
+  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
+  if (!qweight || !packed) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(qweight, 4) || !aligned(packed, 16)) return fail(W4A16_ERR_ALIGN, "packed must be 16-byte aligned");
+  return check_launch(w4a16::launch_repack(reinterpret_cast<const uint32_t*>(qweight),
+                                           reinterpret_cast<uint32_t*>(packed), K, N,
+                                           static_cast<hipStream_t>(stream)),
+                      "repack");
+}
+
+int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uint16_t* scales, uint16_t* w_out,
+                         int K, int N, int group_size, void* stream) {
+  if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
+  if (group_size != w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
+  if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
+  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
+  if (!packed || !qzeros || !scales || !w_out) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(packed, 16) || !aligned(w_out, 2)) return fail(W4A16_ERR_ALIGN, "packed must be 16-byte aligned");
+  return check_launch(w4a16::launch_dequant_packed(reinterpret_cast<const uint32_t*>(packed),
+                                                   reinterpret_cast<const uint32_t*>(qzeros), scales, w_out, K, N,
+                                                   static_cast<hipStream_t>(stream)),
+                      "dequant_packed");
+}
+
+size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
+  if (M <= 0 || K <= 0 || N <= 0 || group_size != w4a16::kGroup || K % w4a16::kGroup || N % 64) return 0;
+  return workspace_for(plan(M, K, N), M, N);
+}
+
+int w4a16_regime(int M, int K, int N) {
+  if (M < 0 || K <= 0 || N <= 0) return W4A16_REGIME_NONE;
+  return plan(M, K, N).regime;
+}
+
+int w4a16_split_k(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0 || K % w4a16::kGroup) return 1;
+  return plan(M, K, N).split;
+}
+
+int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales, uint16_t* y,
+               int M, int K, int N, int group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
+  if (v != W4A16_OK) return v;
+  return run_plan(plan(M, K, N), x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream));
+}
+
+int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                      uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int split,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  const int G = K / w4a16::kGroup;
+  GemmPlan p{regime, p0, p1, split};
+  if (split < 1 || split > G) return fail(W4A16_ERR_ARG, "split must be in [1, K/128] (got %d)", split);
+  if (regime == W4A16_REGIME_DECODE) {
+    if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
+    if (p0 != 1 && p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2 or 4");
+    if (p1 != 4 && p1 != 8 && p1 != 16) return fail(W4A16_ERR_ARG, "decode waves must be 4, 8 or 16");
+    if (decode_lds_bytes(M, p0, p1) > kDecodeMaxLds)
+      return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
+                  decode_lds_bytes(M, p0, p1), kDecodeMaxLds);
+  } else if (regime == W4A16_REGIME_TILE) {
+    if (p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 8 or 16");
+  } else {
+    return fail(W4A16_ERR_ARG, "unknown regime %d", regime);
+  }
+  return run_plan(p, x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream));
+}
+
+size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split) {
+  if (M <= 0 || N <= 0) return 0;
+  return workspace_for(GemmPlan{regime, p0, 0, split}, M, N);
+}
+
+}  // extern "C"

@@ -1,0 +1,258 @@
+// Chunked-prefill / mixed-batch regime (M > 64): LDS-tiled bf16 MFMA GEMM with the int4
+// weights dequantized in registers.
+//
+// Workgroup = 4 waves, output tile BM x 256 (BM = 16 WM).  Wave w owns columns
+// [64 w, 64 w + 64) of the tile and all BM rows: 4 x WM accumulator tiles of
+// v_mfma_f32_16x16x32_bf16.  Because a wave's columns belong to it alone, each weight is
+// dequantized exactly once per workgroup, straight from its 16-byte K8 load into MFMA
+// B fragments -- bf16_rne((q - z) s), the reference's weights (see dequant_k8) -- with no
+// LDS round trip.  The activation tile (BM rows x one 128-deep group) is shared by all four
+// waves through LDS: it is brought in by direct-to-LDS 16-byte loads
+// (global_load_lds_dwordx4), double-buffered one group ahead, in a row-major layout whose
+// 16-byte chunks are XOR-swizzled by (row & 7) so the A-fragment reads are conflict-free.
+//
+// Grid: one workgroup per (m-block, n-block, k-split), enumerated XCD-major so the ~32
+// workgroups resident on one XCD cover a few n-blocks x all m-blocks and share their
+// operands in that XCD's L2.  With split > 1 the workgroups write fp32 partials and the
+// last to arrive at a tile (atomic counter) sums them in split order; the counter is
+// re-armed to zero.
+#include "w4a16_common.h"
+#include "w4a16_launch.h"
+
+namespace w4a16 {
+
+constexpr int kTileWaves = 4;
+constexpr int kTileBN = 256;
+constexpr int kARowBytes = kGroup * 2;  // one activation row of a stage
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Issue the direct-to-LDS loads of activation rows [row0, row0 + BM) x group g into `stage`.
+// Instruction i of wave w fills rows 16 i + 4 w .. +3 (1 KiB); lane -> (row, physical chunk).
+template <int WM>
+__device__ __forceinline__ void issue_a_stage(const uint16_t* __restrict__ x, uint8_t* stage, int row0, int M,
+                                              int K, int g, int wave, int lane) {
+  const int p = lane & 15;
+  const uint16_t* xg = x + kGroup * g;  // wave-uniform
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int r = 16 * i + 4 * wave + (lane >> 4);
+    const int c = p ^ (r & 7);
+    int row = row0 + r;
+    row = row < M ? row : M - 1;  // rows past M load a valid row; their outputs are dropped
+    const uint16_t* src = xg + (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + 8u * c);
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(stage + (16 * i + 4 * wave) * kARowBytes), 16, 0, 0);
+  }
+}
+
+// Raw loads of one group's weights, scales and zero words for a wave's 4 column tiles.
+// Decoding waits until the group is consumed, so the loads stay in flight meanwhile.
+struct BGroup {
+  uint4 w[4];
+  uint32_t s[4];   // bf16 bits
+  uint32_t zw[4];  // AutoAWQ zero word holding this lane's column
+};
+
+// Wave-uniform base pointers plus 32-bit lane offsets (scalar-base addressing).
+__device__ __forceinline__ void load_b_group(BGroup& b, const uint4* __restrict__ packed,
+                                             const uint32_t* __restrict__ qzeros,
+                                             const uint16_t* __restrict__ scales, int g, int NT, int N, int nt0,
+                                             int lane) {
+  const uint4* pw = packed + (static_cast<size_t>(g) * NT + nt0) * 64;
+  const uint16_t* ps = scales + static_cast<size_t>(g) * N + 16 * nt0;
+  const uint32_t* pz = qzeros + static_cast<size_t>(g) * (N >> 3) + 2 * nt0;
+  const int c = lane & 15;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    b.w[tt] = pw[tt * 64 + lane];
+    b.s[tt] = ps[16 * tt + c];
+    b.zw[tt] = pz[2 * tt + (c >> 3)];
+  }
+}
+
+// One 128-deep group: decode scales and zeros, then 4 k-steps of WM x 4 MFMAs.
+template <int WM>
+__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* stage, const BGroup& b, int lane) {
+  const int arow = lane & 15;
+  const int zshift = awq_shift(lane & 7);  // column 16 t + lane % 16 sits at this offset
+  DequantScale d[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) d[tt] = make_dequant_scale(bf16_bits_to_f32(b.s[tt]), (b.zw[tt] >> zshift) & 0xFu);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf16x8_t bf[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint32_t wj = j == 0 ? b.w[tt].x : j == 1 ? b.w[tt].y : j == 2 ? b.w[tt].z : b.w[tt].w;
+      bf[tt] = dequant_k8(wj, d[tt]);
+    }
+    const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 7);
+    const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt) {
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = mfma16(a, bf[tt], acc[mt][tt]);
+    }
+  }
+}
+
+template <int WM>
+__global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict__ x,
+                                                      const uint4* __restrict__ packed,
+                                                      const uint32_t* __restrict__ qzeros,
+                                                      const uint16_t* __restrict__ scales,
+                                                      uint16_t* __restrict__ y, float* __restrict__ partials,
+                                                      int* __restrict__ counters, int M, int K, int N, int split,
+                                                      int m_blocks, int n_blocks) {
+  constexpr int BM = 16 * WM;
+  constexpr int kStage = BM * kARowBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t stage0[kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage1[kStage];
+  __shared__ int is_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int NT = N >> 4;
+  const int G = K / kGroup;
+
+  // XCD-major enumeration: consecutive blockIdx go to different XCDs (round-robin), so
+  // undo that and give each XCD a contiguous run of logical tiles (m fastest).
+  const int total = m_blocks * n_blocks * split;
+  const int b = blockIdx.x;
+  const int per = total >> 3, rem = total & 7, xcd = b & 7, idx = b >> 3;
+  const int L = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  const int mbk = L % m_blocks;
+  const int rest = L / m_blocks;
+  const int nbk = rest % n_blocks;
+  const int sidx = rest / n_blocks;
+  const int g_begin = (G * sidx) / split;
+  const int g_end = (G * (sidx + 1)) / split;
+  const int row0 = mbk * BM;
+  const int col_w = nbk * kTileBN + 64 * wave;  // first column of this wave
+  const int nt0 = col_w >> 4;
+  const bool active = col_w < N;  // wave-uniform: the last n-block may be partly past N
+
+  f32x4_t acc[WM][4];
+#pragma unroll
+  for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  BGroup cur, nxt;
+  if (g_begin < g_end) {
+    issue_a_stage<WM>(x, stage0, row0, M, K, g_begin, wave, lane);
+    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, NT, N, nt0, lane);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // Two groups per trip so each half reads one fixed stage while the other is refilled.
+  for (int g = g_begin; g < g_end; g += 2) {
+    if (g + 1 < g_end) {
+      issue_a_stage<WM>(x, stage1, row0, M, K, g + 1, wave, lane);
+      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, NT, N, nt0, lane);
+    }
+    if (active) mma_group<WM>(acc, stage0, cur, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (g + 1 >= g_end) break;
+    if (g + 2 < g_end) {
+      issue_a_stage<WM>(x, stage0, row0, M, K, g + 2, wave, lane);
+      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, NT, N, nt0, lane);
+    }
+    if (active) mma_group<WM>(acc, stage1, nxt, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  if (split > 1) {
+    if (active) {
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 16 * mt + 4 * (lane >> 4) + i;
+          const int n = col_w + 16 * tt + (lane & 15);
+          if (row < M) partials[(static_cast<size_t>(sidx) * M + row) * N + n] = acc[mt][tt][i];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    const int tile = mbk * n_blocks + nbk;
+    if (threadIdx.x == 0) {
+      const int arrived = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (arrived == split - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    if (active) {
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 16 * mt + 4 * (lane >> 4) + i;
+          const int n = col_w + 16 * tt + (lane & 15);
+          if (row < M) {
+            float v = 0.0f;
+            for (int s = 0; s < split; ++s)
+              v += (s == sidx) ? acc[mt][tt][i] : partials[(static_cast<size_t>(s) * M + row) * N + n];
+            acc[mt][tt][i] = v;
+          }
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  if (!active) return;
+  // Epilogue: bf16 through LDS (row-major BM x 64 per wave, 16-byte chunks swizzled by
+  // row & 7), then 16-byte coalesced stores.  Both stages are free after the last barrier.
+  uint8_t* ep = (wave < 2 ? stage0 : stage1) + (wave & 1) * (BM * 128);
+#pragma unroll
+  for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * mt + 4 * (lane >> 4) + i;
+        const int c = 16 * tt + (lane & 15);
+        const int off = r * 128 + (((c >> 3) ^ (r & 7)) << 4) + ((c & 7) << 1);
+        *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][tt][i]);
+      }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+  for (int round = 0; round < BM / 8; ++round) {
+    const int r = 8 * round + (lane >> 3);
+    const int q = lane & 7;
+    const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 128 + ((q ^ (r & 7)) << 4));
+    const int row = row0 + r;
+    if (row < M) *reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * N + col_w + 8 * q) = v;
+  }
+}
+
+template <int WM>
+static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
+                                const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
+                                int N, int split, hipStream_t stream) {
+  const int m_blocks = (M + 16 * WM - 1) / (16 * WM);
+  const int n_blocks = (N + kTileBN - 1) / kTileBN;
+  const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
+  tile_kernel<WM><<<grid, 64 * kTileWaves, 0, stream>>>(x, reinterpret_cast<const uint4*>(packed), qzeros, scales,
+                                                        y, partials, counters, M, K, N, split, m_blocks, n_blocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
+                           const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
+                           int N, int wm, int split, hipStream_t stream) {
+  if (wm == 8) return launch_tile_t<8>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+  return launch_tile_t<16>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+}
+
+}  // namespace w4a16

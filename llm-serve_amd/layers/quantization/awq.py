@@ -1,0 +1,291 @@
+"""AutoAWQ-GEMM W4A16 linear method on MI355X: the drop-in for the reference's
+``llmserve/layers/quantization/awq.py`` operator interface.
+
+Same names, argument meaning and error behaviour as the reference:
+
+* ``AWQRuntimeConfig`` / ``from_hf_config``        awq.py:11-67
+* ``AWQLinearMethod.create_weights``               awq.py:76-113
+* ``AWQLinearMethod.apply``                        awq.py:115-154
+* ``AWQLinearMethod.process_weights_after_loading`` awq.py:156-181
+* ``unpack_awq_int4``                              awq.py:184-200
+* ``dequantize_awq_gemm``                          awq.py:235-248
+* ``awq_linear`` (the reference's ``awq_cuda_linear`` / ``awq_reference_linear`` role,
+  awq_cuda.py:141-185, awq.py:251-276)
+
+There is one execution backend, the HIP library (libw4a16.so): every tensor operation
+runs there and raises when the library or a GPU is missing -- nothing falls back to a CPU
+path.  ``process_weights_after_loading`` rewrites ``qweight`` once into the gfx950 MFMA
+fragment layout (``awq_qweight``); ``qzeros`` and ``scales`` are consumed as stored.
+"""
+from __future__ import annotations
+
+import threading
+from collections.abc import Mapping
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from ..._lib import REGIME_DECODE, lib
+
+AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
+EXECUTION_BACKEND = "hip"
+DECODE_MAX_M = 64
+
+
+@dataclass(frozen=True)
+class AWQRuntimeConfig:
+    bits: int
+    group_size: int
+    zero_point: bool
+    version: str
+    backend: str
+    activation_dtype: torch.dtype
+    quant_method: str = "awq"
+    execution_backend: str = EXECUTION_BACKEND
+
+    @property
+    def pack_factor(self) -> int:
+        return 32 // self.bits
+
+    @classmethod
+    def from_hf_config(cls, hf_config) -> "AWQRuntimeConfig":
+        raw = getattr(hf_config, "quantization_config", None)
+        if not isinstance(raw, Mapping):
+            raise ValueError("quantization_config must be an AWQ mapping")
+        values = {
+            "quant_method": str(raw.get("quant_method", "")).lower(),
+            "backend": str(raw.get("backend", "")).lower(),
+            "bits": raw.get("bits"),
+            "group_size": raw.get("group_size"),
+            "version": str(raw.get("version", "")).lower(),
+            "zero_point": raw.get("zero_point"),
+        }
+        expected = {
+            "quant_method": "awq",
+            "backend": "autoawq",
+            "bits": 4,
+            "group_size": 128,
+            "version": "gemm",
+            "zero_point": True,
+        }
+        for field, want in expected.items():
+            if values[field] != want:
+                raise ValueError(f"unsupported AWQ {field}: expected {want!r}, got {values[field]!r}")
+        activation_dtype = getattr(hf_config, "dtype", None)
+        if activation_dtype != torch.bfloat16:
+            raise ValueError(f"unsupported AWQ dtype: expected torch.bfloat16, got {activation_dtype!r}")
+        return cls(
+            bits=values["bits"],
+            group_size=values["group_size"],
+            zero_point=values["zero_point"],
+            version=values["version"],
+            backend=values["backend"],
+            activation_dtype=activation_dtype,
+            quant_method=values["quant_method"],
+        )
+
+
+# ------------------------------------------------------------------ workspace
+class _WorkspacePool:
+    """Split-K workspace shared by all layers issuing on one (device, stream).
+
+    Kernels on one stream run in order, so one buffer per stream serves every layer; it
+    is zero-filled when (re)allocated and the kernels re-arm their counters to zero."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes <= 0:
+            return None
+        stream = torch.cuda.current_stream(device).cuda_stream
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._buffers.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._buffers[key] = buf
+            return buf
+
+    def reserve(self, device: torch.device, nbytes: int) -> None:
+        self.get(device, nbytes)
+
+
+WORKSPACE = _WorkspacePool()
+
+
+def decode_workspace_bytes(k: int, n: int, group_size: int = 128) -> int:
+    """Largest workspace any M <= 64 call at this shape needs."""
+    library = lib()
+    return max(library.workspace_bytes(m, k, n, group_size) for m in range(1, DECODE_MAX_M + 1))
+
+
+# ------------------------------------------------------------- linear method
+class AWQLinearMethod:
+
+    def __init__(self, config: AWQRuntimeConfig):
+        if config.execution_backend != EXECUTION_BACKEND:
+            raise ValueError(
+                f"unsupported AWQ execution_backend {config.execution_backend!r}: this build has a single "
+                f"{EXECUTION_BACKEND!r} backend")
+        self.config = config
+
+    def create_weights(self, layer: nn.Module, input_size: int, output_size: int) -> None:
+        if getattr(layer, "tp_size", 1) != 1:
+            raise ValueError("AWQ tensor parallel is not supported")
+        if input_size % self.config.group_size:
+            raise ValueError("AWQ input size must be divisible by group_size")
+        if output_size % self.config.pack_factor:
+            raise ValueError("AWQ output size must be divisible by pack_factor")
+        num_groups = input_size // self.config.group_size
+        packed_output_size = output_size // self.config.pack_factor
+        layer.qweight = nn.Parameter(torch.empty(input_size, packed_output_size, dtype=torch.int32),
+                                     requires_grad=False)
+        layer.qzeros = nn.Parameter(torch.empty(num_groups, packed_output_size, dtype=torch.int32),
+                                    requires_grad=False)
+        layer.scales = nn.Parameter(torch.empty(num_groups, output_size, dtype=self.config.activation_dtype),
+                                    requires_grad=False)
+        for param in (layer.qweight, layer.qzeros):
+            param.output_dim = 1
+            param.input_dim = 0
+            param.packed_dim = 1
+            param.pack_factor = self.config.pack_factor
+        layer.scales.output_dim = 1
+        layer.scales.input_dim = 0
+
+    def apply(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear(inputs, layer.awq_qweight, layer.awq_qzeros, layer.scales,
+                          group_size=self.config.group_size)
+
+    def process_weights_after_loading(self, layer: nn.Module) -> None:
+        qweight = layer.qweight.data
+        if qweight.device.type != "cuda":
+            raise ValueError("AWQ weights must be on a GPU (HIP) device before processing")
+        _validate_awq_tensors(qweight, layer.qzeros.data, layer.scales.data, self.config.group_size)
+        packed = repack_awq_qweight(qweight)
+        qzeros = layer.qzeros.data.contiguous()
+        k, n = qweight.shape[0], qweight.shape[1] * 8
+        delattr(layer, "qweight")
+        delattr(layer, "qzeros")
+        layer.register_buffer("awq_qweight", packed, persistent=False)
+        layer.register_buffer("awq_qzeros", qzeros, persistent=False)
+        layer.awq_shape = (k, n)
+        # decode calls then never allocate (hipGraph capture, tight serving loops)
+        WORKSPACE.reserve(packed.device, decode_workspace_bytes(k, n, self.config.group_size))
+
+
+# ------------------------------------------------------------ tensor functions
+def _validate_awq_tensors(qweight, qzeros, scales, group_size: int) -> None:
+    """Reference contract, awq.py:203-232 (same messages)."""
+    if qweight.ndim != 2 or qweight.dtype != torch.int32:
+        raise ValueError("qweight must be a two-dimensional int32 tensor")
+    if qzeros.ndim != 2 or qzeros.dtype != torch.int32:
+        raise ValueError("qzeros must be a two-dimensional int32 tensor")
+    if scales.ndim != 2 or not scales.is_floating_point():
+        raise ValueError("scales must be a two-dimensional floating tensor")
+    if group_size <= 0:
+        raise ValueError("group_size must be positive")
+    input_size = qweight.shape[0]
+    if input_size % group_size:
+        raise ValueError("qweight input size must be divisible by group_size")
+    num_groups = input_size // group_size
+    output_size = qweight.shape[1] * 8
+    if qzeros.shape != (num_groups, qweight.shape[1]):
+        raise ValueError("qzeros shape must be [input_size / group_size, output_size / 8]")
+    if scales.shape != (num_groups, output_size):
+        raise ValueError("scales shape must be [input_size / group_size, output_size]")
+    if len({qweight.device, qzeros.device, scales.device}) != 1:
+        raise ValueError("qweight, qzeros, and scales must share one device")
+
+
+def unpack_awq_int4(packed: torch.Tensor) -> torch.Tensor:
+    """int32 [R, C] -> int32 [R, 8C] in logical column order (awq.py:184-200)."""
+    if packed.ndim != 2:
+        raise ValueError("packed AWQ tensor must be two-dimensional")
+    if packed.dtype != torch.int32:
+        raise ValueError("packed AWQ tensor must use int32")
+    if packed.numel() == 0:
+        return torch.empty((packed.shape[0], packed.shape[1] * 8), dtype=torch.int32, device=packed.device)
+    return lib().unpack_int4(packed.contiguous())
+
+
+def dequantize_awq_gemm(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, *,
+                        group_size: int) -> torch.Tensor:
+    """bf16 W [K, N] = bf16_rne((q - z) * s), bit-exact with awq.py:235-248 for bf16 scales."""
+    _validate_awq_tensors(qweight, qzeros, scales, group_size)
+    if scales.dtype != torch.bfloat16:
+        raise ValueError("the HIP dequant kernel takes bfloat16 scales")
+    return lib().dequant(qweight.contiguous(), qzeros.contiguous(), scales.contiguous(), group_size)
+
+
+def repack_awq_qweight(qweight: torch.Tensor) -> torch.Tensor:
+    """AutoAWQ qweight [K, N/8] -> gfx950 MFMA fragment layout (flat int32, same bytes)."""
+    if qweight.ndim != 2 or qweight.dtype != torch.int32:
+        raise ValueError("qweight must be a two-dimensional int32 tensor")
+    k, n = qweight.shape[0], qweight.shape[1] * 8
+    if k % 128:
+        raise ValueError("qweight K must be divisible by 128")
+    if n % 16:
+        raise ValueError("qweight N must be divisible by 16")
+    return lib().repack_qweight(qweight.contiguous())
+
+
+def _aligned16(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+               *, group_size: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y[..., N] = inputs[..., K] @ W on the HIP kernels (bf16 in/out, fp32 accumulation).
+
+    ``packed_qweight`` comes from ``repack_awq_qweight``; ``qzeros`` [K/128, N/8] and
+    ``scales`` [K/128, N] are the AutoAWQ tensors.  Leading dimensions of ``inputs`` are
+    flattened into M.  ``workspace`` (uint8, zero-filled when allocated) overrides the
+    per-stream shared one."""
+    if not inputs.is_floating_point():
+        raise ValueError("AWQ activations must use a floating dtype")
+    if inputs.dtype != scales.dtype:
+        raise ValueError("AWQ activation dtype must match checkpoint scales dtype")
+    if inputs.dtype != torch.bfloat16:
+        raise ValueError("AWQ HIP kernels take bfloat16 activations")
+    if inputs.device.type != "cuda":
+        raise ValueError("AWQ HIP inputs must be GPU (HIP) tensors")
+    if group_size != 128:
+        raise ValueError("AWQ HIP kernels require group_size=128")
+    if len({inputs.device, packed_qweight.device, qzeros.device, scales.device}) != 1:
+        raise ValueError("AWQ activations and weights must share one device")
+    if qzeros.dtype != torch.int32 or packed_qweight.dtype != torch.int32:
+        raise ValueError("qweight and qzeros must be int32 tensors")
+    n = scales.shape[1]
+    k = scales.shape[0] * group_size
+    if inputs.shape[-1] != k:
+        raise ValueError("AWQ activation K must match qweight input size")
+    if packed_qweight.numel() * 8 != k * n:
+        raise ValueError("packed qweight does not match the scales shape")
+    if n % 64:
+        raise ValueError("AWQ HIP GEMM requires the output size to be divisible by 64")
+    lead = inputs.shape[:-1]
+    x = inputs.reshape(-1, k)
+    if not x.is_contiguous() or not _aligned16(x):
+        x = x.contiguous()
+        if not _aligned16(x):
+            x = x.clone()
+    m = x.shape[0]
+    y = torch.empty((m, n), dtype=inputs.dtype, device=inputs.device)
+    if m == 0:
+        return y.reshape(*lead, n)
+    library = lib()
+    if workspace is None:
+        workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
+    library.gemm(x, packed_qweight, qzeros, scales.contiguous(), y, k, n, workspace, group_size)
+    return y.reshape(*lead, n)
+
+
+def awq_regime(m: int, k: int, n: int) -> str:
+    """Which kernel family ``awq_linear`` runs for this shape: 'decode' or 'tile'."""
+    return "decode" if lib().regime(m, k, n) == REGIME_DECODE else "tile"

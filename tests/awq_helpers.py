@@ -1,0 +1,96 @@
+"""Shared helpers for the GPU parity tests: numpy oracle data <-> torch GPU tensors."""
+import importlib
+import os
+
+import numpy as np
+import torch
+
+from oracle import awq_oracle as ora
+
+QWEN3_SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+# The bf16 GEMM tolerance: max |y - r| / max(|r|, rms(r)) against an fp64/fp32-accumulated
+# reference over the same bf16 weights.
+GEMM_REL_TOL = 1e-2
+
+
+def pkg():
+    return importlib.import_module("llm-serve_amd")
+
+
+def awq_mod():
+    return importlib.import_module("llm-serve_amd.layers.quantization.awq")
+
+
+def bf16_from_bits(bits: np.ndarray, device="cuda") -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).copy()).view(torch.bfloat16)
+    return t.to(device)
+
+
+def bits_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def to_gpu(problem: dict) -> dict:
+    return {
+        "qweight": torch.from_numpy(problem["qweight"]).cuda(),
+        "qzeros": torch.from_numpy(problem["qzeros"]).cuda(),
+        "scales": bf16_from_bits(problem["scales_bits"]),
+        "x": bf16_from_bits(problem["x_bits"]),
+    }
+
+
+def golden_cases():
+    data = np.load(os.path.join(GOLDEN, "awq_small_seeded.npz"))
+    names = sorted({k.split(".")[0] for k in data.files})
+    return {name: {key.split(".", 1)[1]: data[key] for key in data.files if key.startswith(name + ".")}
+            for name in names}
+
+
+def rel_err(y, r) -> float:
+    """GEMM tolerance metric (oracle.gemm_rel_err); computed on the GPU for GPU tensors."""
+    if isinstance(y, torch.Tensor) and isinstance(r, torch.Tensor) and y.is_cuda and r.is_cuda:
+        y64, r64 = y.detach().double(), r.detach().double()
+        if r64.numel() == 0:
+            return 0.0
+        rms = torch.sqrt(torch.mean(r64 * r64))
+        floor = rms if rms > 0 else torch.ones_like(rms)
+        return float(torch.max((y64 - r64).abs() / torch.maximum(r64.abs(), floor)))
+    y64 = y.detach().double().cpu().numpy() if isinstance(y, torch.Tensor) else np.asarray(y, dtype=np.float64)
+    r64 = r.detach().double().cpu().numpy() if isinstance(r, torch.Tensor) else np.asarray(r, dtype=np.float64)
+    return ora.gemm_rel_err(y64, r64)
+
+
+def same_bits_nan_aware(a: np.ndarray, b: np.ndarray, zero_sign_free: bool = False) -> bool:
+    fa, fb = ora.bf16_bits_to_f32(a), ora.bf16_bits_to_f32(b)
+    nan_a, nan_b = np.isnan(fa), np.isnan(fb)
+    if not np.array_equal(nan_a, nan_b):
+        return False
+    a2, b2 = a[~nan_a], b[~nan_a]
+    if zero_sign_free:
+        a2 = np.where((a2 & 0x7FFF) == 0, 0, a2)
+        b2 = np.where((b2 & 0x7FFF) == 0, 0, b2)
+    return bool(np.array_equal(a2, b2))
+
+
+def random_awq_gpu(k: int, n: int, seed: int, group: int = 128):
+    """Seeded AWQ tensors generated on the GPU: uniform random int32 words are uniform
+    independent nibbles in {0..15}; scales uniform in [0.002, 0.02] (bf16)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    qweight = torch.randint(-2 ** 31, 2 ** 31 - 1, (k, n // 8), dtype=torch.int32, device="cuda", generator=g)
+    qzeros = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // group, n // 8), dtype=torch.int32, device="cuda",
+                           generator=g)
+    scales = (torch.rand((k // group, n), device="cuda", generator=g) * 0.018 + 0.002).to(torch.bfloat16)
+    return qweight, qzeros, scales
+
+
+def random_x_gpu(m: int, k: int, seed: int, outliers: bool = False) -> torch.Tensor:
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    if outliers:
+        cols = torch.randperm(k, device="cuda", generator=g)[: round(0.01 * k)]
+        x[:, cols] *= 20.0
+    return x.to(torch.bfloat16)

@@ -1,0 +1,126 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the header
+declares, and its host-side validation / dispatch queries behave (no kernel launches)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "w4a16.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(w4a16_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    names = declared_functions()
+    for required in ("w4a16_gemm", "w4a16_dequant", "w4a16_repack_qweight", "w4a16_workspace_bytes",
+                     "w4a16_last_error", "w4a16_regime", "w4a16_unpack_int4"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    dll = pkg.lib().dll
+    missing = [name for name in declared_functions() if not hasattr(dll, name)]
+    assert not missing, missing
+
+
+def test_binding_signatures_cover_the_header(pkg):
+    from importlib import import_module
+
+    sigs = import_module("llm-serve_amd._lib")._SIGNATURES
+    assert sorted(sigs) == declared_functions()
+
+
+def test_abi_version_and_empty_error(pkg):
+    L = pkg.lib()
+    assert L.dll.w4a16_abi_version() == 1
+    assert isinstance(L.last_error(), str)
+
+
+@pytest.mark.parametrize("m,k,n,group,code,msg", [
+    (16, 4000, 4096, 128, 2, "K must be divisible by 128"),
+    (16, 4096, 4100, 128, 2, "N must be divisible by 64"),
+    (16, 4096, 4096, 64, 2, "group_size must be 128"),
+    (-1, 4096, 4096, 128, 1, "M must be"),
+    (16, 4096, 4096, 128, 1, "null tensor pointer"),
+])
+def test_gemm_rejects_bad_arguments_without_touching_the_gpu(pkg, m, k, n, group, code, msg):
+    L = pkg.lib()
+    rc = L.dll.w4a16_gemm(None, None, None, None, None, m, k, n, group, None, 0, None)
+    assert rc == code
+    assert msg in L.last_error()
+
+
+def test_gemm_m_zero_is_a_noop(pkg):
+    L = pkg.lib()
+    assert L.dll.w4a16_gemm(None, None, None, None, None, 0, 4096, 4096, 128, None, 0, None) == 0
+
+
+def test_misaligned_pointer_is_rejected(pkg):
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    base = ctypes.addressof(buf)
+    p = base + (16 - base % 16) % 16 + 2  # 2 bytes past a 16-byte boundary
+    rc = L.dll.w4a16_gemm(p, p, p, p, p, 16, 4096, 4096, 128, None, 0, None)
+    assert rc == 3 and "aligned" in L.last_error()
+
+
+def test_format_entry_points_validate_shapes(pkg):
+    L = pkg.lib()
+    assert L.dll.w4a16_repack_qweight(None, None, 100, 64, None) == 2
+    assert L.dll.w4a16_repack_qweight(None, None, 128, 8, None) == 2
+    assert L.dll.w4a16_dequant(None, None, None, None, 4, 12, 2, None) == 2  # N % 8
+    assert L.dll.w4a16_dequant(None, None, None, None, 5, 8, 2, None) == 2   # K % group
+    assert L.dll.w4a16_dequant_packed(None, None, None, None, 128, 64, 64, None) == 2
+    assert L.dll.w4a16_unpack_int4(None, None, 0, 4, None) == 1
+
+
+QWEN3 = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+
+
+def test_regime_boundary_and_split_limits(pkg):
+    L = pkg.lib()
+    for k, n in QWEN3.values():
+        assert L.regime(0, k, n) == 0
+        for m in (1, 4, 8, 16, 32, 64):
+            assert L.regime(m, k, n) == 1
+            assert 1 <= L.split_k(m, k, n) <= k // 128
+        for m in (65, 128, 512, 2048, 4096):
+            assert L.regime(m, k, n) == 2
+            assert 1 <= L.split_k(m, k, n) <= k // 128
+
+
+def test_workspace_covers_partials_and_counters(pkg):
+    L = pkg.lib()
+    for k, n in QWEN3.values():
+        for m in (1, 16, 64, 128, 512, 2048):
+            split = L.split_k(m, k, n)
+            ws = L.workspace_bytes(m, k, n)
+            if split == 1:
+                assert ws == 0
+            else:
+                assert ws >= split * m * n * 4 + 4
+    assert L.workspace_bytes(16, 4096, 4096, 64) == 0  # invalid group -> 0
+
+
+def test_forced_config_validation(pkg):
+    L = pkg.lib()
+    f = L.dll.w4a16_gemm_config
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    assert f(p, p, p, p, p, 128, 4096, 4096, 128, 1, 4, 4, 1, None, 0, None) == 2  # decode needs M <= 64
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 3, 4, 1, None, 0, None) == 1  # bad tiles
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 5, 1, None, 0, None) == 1  # bad waves
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 33, None, 0, None) == 1  # split > K/128
+    assert f(p, p, p, p, p, 64, 4096, 4096, 128, 1, 4, 16, 1, None, 0, None) == 1  # 256 KiB of LDS
+    assert "LDS" in L.last_error()
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 0, 1, None, 0, None) == 1  # bad wm
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 1, None, 0, None) == 1  # bad regime
+    # split > 1 without workspace
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 4, None, 0, None) == 4
+    assert "workspace" in L.last_error()

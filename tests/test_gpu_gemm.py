@@ -1,0 +1,294 @@
+"""GPU parity of the W4A16 GEMM (decode split-K kernel and MFMA tile kernel).
+
+Small sizes compare against the CPU oracle (fp64-accumulated x @ W over the reference's
+bf16 weights).  Full Qwen3-8B sizes compare against torch fp32 matmul on the GPU over the
+bit-exact dequantized weights (checked separately against the oracle in
+test_gpu_format.py).  Tolerance: max |y - r| / max(|r|, rms(r)) <= 1e-2 (GEMM_REL_TOL),
+plus the reference's own assert_close tolerances where its tests state them."""
+import numpy as np
+import pytest
+import torch
+
+from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, golden_cases, pkg,
+                         random_awq_gpu, random_x_gpu, rel_err, to_gpu)
+from oracle import awq_oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+
+def hip_linear(t, packed=None, workspace=None):
+    awq = awq_mod()
+    packed = awq.repack_awq_qweight(t["qweight"]) if packed is None else packed
+    return awq.awq_linear(t["x"], packed, t["qzeros"], t["scales"], group_size=128, workspace=workspace)
+
+
+@pytest.mark.parametrize("case", sorted(golden_cases()))
+def test_gemm_matches_oracle_on_golden_fixtures(gpu_lib, case):
+    c = golden_cases()[case]
+    if case == "special_scales":
+        pytest.skip("special-scale fixture is a dequant fixture (inf/neg scales make y non-finite)")
+    t = to_gpu({"qweight": c["qweight"], "qzeros": c["qzeros"], "scales_bits": c["scales_bits"],
+                "x_bits": c["x_bits"]})
+    y = hip_linear(t)
+    assert y.dtype == torch.bfloat16 and y.shape == c["y_f64"].shape
+    assert rel_err(y, c["y_f64"]) <= GEMM_REL_TOL
+
+
+def test_decode_token_counts_reference_recipe(gpu_lib):
+    """tests/test_awq_cuda.py:110-155: seed 17, K=128, N=64, M in {1,4,8,16,32,65,128},
+    assert_close(rtol=0.02, atol=0.05) against the reference backend."""
+    rng = np.random.default_rng(17)
+    k, n = 128, 64
+    q = rng.integers(0, 16, size=(k, n))
+    z = rng.integers(0, 16, size=(1, n))
+    s = ora.f32_to_bf16_bits(rng.random((1, n)).astype(np.float32) * 0.05)
+    base = {"qweight": ora.pack_awq_int4(q), "qzeros": ora.pack_awq_int4(z), "scales_bits": s}
+    for m in (1, 4, 8, 16, 32, 65, 128):
+        x = ora.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+        t = to_gpu(dict(base, x_bits=x))
+        y = hip_linear(t)
+        want = ora.bf16_bits_to_f32(ora.awq_linear_bf16_bits(x, base["qweight"], base["qzeros"], s, 128))
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.02, atol=0.05)
+        assert rel_err(y, ora.awq_linear_ref(x, base["qweight"], base["qzeros"], s, 128)) <= GEMM_REL_TOL
+
+
+def test_single_token_wide_gemv_reference_recipe(gpu_lib):
+    """tests/test_awq_triton.py:83-113: M=1, K=128, N=16384, rtol=0.01, atol=0.02."""
+    p = ora.make_problem(seed=11, m=1, k=128, n=16384, scale_lo=0.0, scale_hi=0.05)
+    t = to_gpu(p)
+    y = hip_linear(t)
+    want = ora.bf16_bits_to_f32(ora.awq_linear_bf16_bits(p["x_bits"], p["qweight"], p["qzeros"],
+                                                         p["scales_bits"], 128))
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.01, atol=0.02)
+
+
+DECODE_CONFIGS = [(tn, w, s) for tn in (1, 2, 4) for w in (4, 8, 16) for s in (1, 3, 8)]
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 33, 64])
+def test_every_decode_configuration(gpu_lib, m):
+    """All column-tile / wave / split combinations of the decode kernel, incl. uneven splits."""
+    k, n = 1024, 512
+    p = ora.make_problem(seed=100 + m, m=m, k=k, n=n)
+    t = to_gpu(p)
+    packed = awq_mod().repack_awq_qweight(t["qweight"])
+    want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    for tn, waves, split in DECODE_CONFIGS:
+        if waves * ((m + 15) // 16) * tn * 1024 > 64 * 1024:
+            continue  # rejected by the library (LDS limit), see test_capi
+        ws_bytes = gpu_lib.workspace_bytes_config(m, n, 1, tn, split)
+        ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 1, tn, waves, split, ws)
+        err = rel_err(y, want)
+        assert err <= GEMM_REL_TOL, (tn, waves, split, err)
+        if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
+            assert int(torch.count_nonzero(ws[:65536])) == 0
+
+
+@pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256)])
+def test_every_tile_configuration(gpu_lib, m, n):
+    k = 1024
+    p = ora.make_problem(seed=200 + m, m=m, k=k, n=n)
+    t = to_gpu(p)
+    packed = awq_mod().repack_awq_qweight(t["qweight"])
+    want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    for wm in (8, 16):
+        for split in (1, 2, 3):
+            ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
+            ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+            gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, 0, split, ws)
+            err = rel_err(y, want)
+            assert err <= GEMM_REL_TOL, (wm, split, err)
+
+
+def test_shared_workspace_across_shapes_and_m(gpu_lib):
+    """One workspace reused by calls of different M and N (as the per-stream pool does):
+    the counters must always be found re-armed."""
+    k = 4096
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    for n in (4096, 6144):
+        qw, qz, s = random_awq_gpu(k, n, seed=n)
+        packed = awq_mod().repack_awq_qweight(qw)
+        for m in (1, 4, 16, 64, 200, 16, 1):
+            x = random_x_gpu(m, k, seed=m)
+            y = awq_mod().awq_linear(x, packed, qz, s, group_size=128, workspace=ws)
+            assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL, (n, m)
+    assert int(torch.count_nonzero(ws[:65536])) == 0
+
+
+def test_split_k_results_are_deterministic(gpu_lib):
+    k, n = 4096, 4096
+    qw, qz, s = random_awq_gpu(k, n, seed=3)
+    packed = awq_mod().repack_awq_qweight(qw)
+    for m in (16, 300):
+        x = random_x_gpu(m, k, seed=m)
+        a = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+        b = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def full_reference(x, qw, qz, s):
+    w = awq_mod().dequantize_awq_gemm(qw, qz, s, group_size=128)
+    return x.float() @ w.float()
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
+def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=11)
+    packed = awq_mod().repack_awq_qweight(qw)
+    for m in (1, 4, 8, 16, 32, 64):
+        assert pkg().awq_regime(m, k, n) == "decode"
+        x = random_x_gpu(m, k, seed=m)
+        y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+        err = rel_err(y, full_reference(x, qw, qz, s))
+        assert err <= GEMM_REL_TOL, (m, err)
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
+def test_full_qwen3_shapes_prefill_chunk_with_outliers(gpu_lib, shape):
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=12)
+    packed = awq_mod().repack_awq_qweight(qw)
+    x = random_x_gpu(2048, k, seed=7, outliers=True)
+    assert pkg().awq_regime(2048, k, n) == "tile"
+    y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+    err = rel_err(y, full_reference(x, qw, qz, s))
+    assert err <= GEMM_REL_TOL, err
+
+
+@pytest.mark.parametrize("shape", ["gate_up", "down"])
+def test_mixed_ragged_batch_m512(gpu_lib, shape):
+    """48 decode rows + 8 x 4 verify rows + a 432-row prefill chunk packed into M = 512."""
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=13)
+    x = torch.cat([random_x_gpu(48, k, 1), random_x_gpu(32, k, 2), random_x_gpu(432, k, 3, outliers=True)])
+    y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
+    assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+    # rows are independent: the 48 decode rows alone give the same values within rounding
+    y48 = awq_mod().awq_linear(x[:48].contiguous(), awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
+    assert rel_err(y48, y[:48].float()) <= GEMM_REL_TOL
+
+
+@pytest.mark.parametrize("m", [0, 17, 63, 65, 100, 255, 257])
+def test_ragged_m(gpu_lib, m):
+    k, n = 512, 256
+    qw, qz, s = random_awq_gpu(k, n, seed=m + 1)
+    x = random_x_gpu(m, k, seed=m) if m else torch.empty((0, k), dtype=torch.bfloat16, device="cuda")
+    y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
+    assert y.shape == (m, n)
+    if m:
+        assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+
+
+def test_leading_dims_are_flattened(gpu_lib):
+    k, n = 256, 128
+    qw, qz, s = random_awq_gpu(k, n, seed=4)
+    x = random_x_gpu(6, k, seed=4).view(2, 3, k)
+    y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
+    assert y.shape == (2, 3, n)
+    assert rel_err(y.reshape(6, n), full_reference(x.reshape(6, k), qw, qz, s)) <= GEMM_REL_TOL
+
+
+def test_too_small_workspace_is_an_error(gpu_lib):
+    k, n, m = 4096, 4096, 16
+    qw, qz, s = random_awq_gpu(k, n, seed=5)
+    need = gpu_lib.workspace_bytes(m, k, n)
+    assert need > 0
+    ws = torch.zeros(need - 256, dtype=torch.uint8, device="cuda")
+    with pytest.raises(pkg().W4A16Error, match="workspace"):
+        awq_mod().awq_linear(random_x_gpu(m, k, 1), awq_mod().repack_awq_qweight(qw), qz, s, group_size=128,
+                             workspace=ws)
+
+
+def test_zero_scales_and_q_equal_z_give_zero(gpu_lib):
+    k, n = 256, 128
+    qw, qz, s = random_awq_gpu(k, n, seed=6)
+    packed = awq_mod().repack_awq_qweight(qw)
+    for m in (8, 128):
+        x = random_x_gpu(m, k, seed=1)
+        y = awq_mod().awq_linear(x, packed, qz, torch.zeros_like(s), group_size=128)
+        assert torch.count_nonzero(y.float()) == 0
+    # q == z everywhere (every row takes its group's zero words): W == 0 exactly, so both
+    # kernels multiply exact zero weights and y is exactly 0.
+    q_equal_z = qz.repeat_interleave(128, dim=0).contiguous()
+    packed = awq_mod().repack_awq_qweight(q_equal_z)
+    for m in (8, 128):
+        y = awq_mod().awq_linear(random_x_gpu(m, k, seed=2), packed, qz, s, group_size=128)
+        assert torch.count_nonzero(y.float()) == 0
+
+
+def test_layer_forward_matches_oracle(gpu_lib):
+    """tests/test_awq_linear_backend.py:125-148 pattern (q = arange % 16, z = 8, linspace scales)
+    through ColumnParallelLinear -> AWQLinearMethod.apply on the GPU."""
+    import importlib
+
+    linear = importlib.import_module("llm-serve_amd.layers.linear")
+    awq = awq_mod()
+    cfg = awq.AWQRuntimeConfig(bits=4, group_size=128, zero_point=True, version="gemm", backend="autoawq",
+                               activation_dtype=torch.bfloat16)
+    k, n = 128, 64
+    with torch.device("cuda"):
+        layer = linear.ColumnParallelLinear(k, n, quant_config=cfg)
+    q = np.arange(k * n).reshape(k, n) % 16
+    z = np.full((1, n), 8)
+    s_bits = ora.f32_to_bf16_bits(np.linspace(0.01, 0.64, n, dtype=np.float32).reshape(1, n))
+    qweight, qzeros = ora.pack_awq_int4(q), ora.pack_awq_int4(z)
+    layer.qweight.weight_loader(layer.qweight, torch.from_numpy(qweight).cuda())
+    layer.qzeros.weight_loader(layer.qzeros, torch.from_numpy(qzeros).cuda())
+    layer.scales.weight_loader(layer.scales, bf16_from_bits(s_bits))
+    layer.quant_method.process_weights_after_loading(layer)
+    assert not hasattr(layer, "qweight") and not hasattr(layer, "qzeros")
+    for m in (4, 100):
+        x_bits = ora.f32_to_bf16_bits(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))
+        y = layer(bf16_from_bits(x_bits))
+        want = ora.awq_linear_ref(x_bits, qweight, qzeros, s_bits, 128)
+        assert rel_err(y, want) <= GEMM_REL_TOL
+
+
+def test_row_parallel_layer_forward(gpu_lib):
+    import importlib
+
+    linear = importlib.import_module("llm-serve_amd.layers.linear")
+    awq = awq_mod()
+    cfg = awq.AWQRuntimeConfig(bits=4, group_size=128, zero_point=True, version="gemm", backend="autoawq",
+                               activation_dtype=torch.bfloat16)
+    k, n = 1024, 256
+    qw, qz, s = random_awq_gpu(k, n, seed=9)
+    with torch.device("cuda"):
+        layer = linear.RowParallelLinear(k, n, quant_config=cfg)
+    layer.qweight.weight_loader(layer.qweight, qw)
+    layer.qzeros.weight_loader(layer.qzeros, qz)
+    layer.scales.weight_loader(layer.scales, s)
+    layer.quant_method.process_weights_after_loading(layer)
+    x = random_x_gpu(16, k, seed=3)
+    assert rel_err(layer(x), full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+
+
+def test_hip_graph_capture_replays_match_eager(gpu_lib):
+    """A captured decode GEMM with a split-K reduction (counters live in the workspace)
+    replayed several times, with eager work in between, matches the eager result."""
+    k, n, m = 4096, 4096, 16
+    qw, qz, s = random_awq_gpu(k, n, seed=21)
+    awq = awq_mod()
+    packed = awq.repack_awq_qweight(qw)
+    assert gpu_lib.split_k(m, k, n) > 1
+    x = random_x_gpu(m, k, seed=1)
+    eager = awq.awq_linear(x, packed, qz, s, group_size=128).clone()
+    static_x = x.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        awq.awq_linear(static_x, packed, qz, s, group_size=128)  # warm the per-stream workspace
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        static_y = awq.awq_linear(static_x, packed, qz, s, group_size=128)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_y.view(torch.int16), eager.view(torch.int16)), i
+        _ = awq.awq_linear(random_x_gpu(m, k, seed=50 + i), packed, qz, s, group_size=128)
+        torch.cuda.synchronize()

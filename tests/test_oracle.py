@@ -1,0 +1,301 @@
+"""Pins the CPU oracle before any GPU result is compared against it.
+
+Each check is independent of the oracle's own formula: hand-derived constants, the
+reference's known-answer tests (tests/golden/reference_kats.json, with file:line),
+torch's bf16 arithmetic (the library the reference computes with), exact rational
+arithmetic on small inputs, and algebraic invariants.
+"""
+import json
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as ora
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def kats():
+    with open(os.path.join(GOLDEN, "reference_kats.json")) as f:
+        return json.load(f)
+
+
+def hex_u32_to_i32(h):
+    return np.array([int(h, 16)], dtype=np.uint64).astype(np.uint32).view(np.int32)[0]
+
+
+# --------------------------------------------------------------------- format
+def test_pack_order_constants_are_inverse_permutations():
+    for c in range(8):
+        assert ora.AWQ_PACK_ORDER[ora.AWQ_REVERSE_ORDER[c]] == c
+
+
+@pytest.mark.parametrize("name", ["pack_word_0_to_7", "pack_word_8_to_15"])
+def test_pack_matches_hand_derived_word(name):
+    kat = kats()[name]
+    packed = ora.pack_awq_int4(np.array(kat["values"]))
+    assert packed.dtype == np.int32
+    assert packed[0, 0] == hex_u32_to_i32(kat["packed_hex"][0])
+    # unpack must restore the values, including for a word with the sign bit set
+    np.testing.assert_array_equal(ora.unpack_awq_int4(packed), np.array(kat["values"]))
+
+
+def test_unpack_restores_autoawq_channel_order_kat():
+    kat = kats()["unpack_channel_order"]
+    values = np.array(kat["values"], dtype=np.int32)
+    np.testing.assert_array_equal(ora.unpack_awq_int4(ora.pack_awq_int4(values)), values)
+
+
+def test_pack_nibble_positions_brute_force():
+    rng = np.random.default_rng(5)
+    values = rng.integers(0, 16, size=(3, 32))
+    packed = ora.pack_awq_int4(values).view(np.uint32)
+    for r in range(3):
+        for c in range(32):
+            word = int(packed[r, c // 8])
+            nib = ora.AWQ_PACK_ORDER.index(c % 8)  # nibble slot that holds column c
+            assert (word >> (4 * nib)) & 0xF == values[r, c]
+
+
+def test_pack_rejects_out_of_range_and_shapes():
+    with pytest.raises(ValueError, match="divisible by 8"):
+        ora.pack_awq_int4(np.zeros((2, 7), dtype=np.int64))
+    with pytest.raises(ValueError, match=r"\[0, 15\]"):
+        ora.pack_awq_int4(np.full((1, 8), 16))
+    with pytest.raises(TypeError):
+        ora.pack_awq_int4(np.zeros((1, 8), dtype=np.float32))
+
+
+# ----------------------------------------------------------------------- bf16
+def test_bf16_rne_table():
+    kat = kats()["bf16_rne_table"]
+    f = np.array([int(h, 16) for h in kat["f32_hex"]], dtype=np.uint64).astype(np.uint32).view(np.float32)
+    want = np.array([int(h, 16) for h in kat["bf16_hex"]], dtype=np.uint16)
+    np.testing.assert_array_equal(ora.f32_to_bf16_bits(f), want)
+
+
+def test_bf16_rne_matches_torch_on_random_bits():
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 2 ** 32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    # force many exact ties and near-ties
+    bits[:50_000] = (bits[:50_000] & 0xFFFF0000) | 0x8000
+    bits[50_000:60_000] = (bits[50_000:60_000] & 0xFFFF0000) | 0x7FFF
+    f = bits.view(np.float32)
+    ours = ora.f32_to_bf16_bits(f)
+    theirs = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    finite = ~np.isnan(f)
+    np.testing.assert_array_equal(ours[finite], theirs[finite])
+    # NaN stays NaN (payload is not part of the contract)
+    assert np.all(np.isnan(ora.bf16_bits_to_f32(ours[~finite])))
+
+
+# -------------------------------------------------------------------- dequant
+def test_dequant_kat_group2_fp32():
+    kat = kats()["dequant_group2_fp32"]
+    qw = ora.pack_awq_int4(np.array(kat["qvalues"]))
+    qz = ora.pack_awq_int4(np.array(kat["zeros"]))
+    s = np.array(kat["scales"], dtype=np.float32)
+    got = ora.dequantize_awq_gemm_fp(qw, qz, s, kat["group_size"])
+    assert got.dtype == np.float32
+    np.testing.assert_array_equal(got, np.array(kat["expected"], dtype=np.float32))
+    # the bf16 path gives the same numbers (all are exact in bf16)
+    bits = ora.dequantize_awq_gemm_bits(qw, qz, ora.f32_to_bf16_bits(s), kat["group_size"])
+    np.testing.assert_array_equal(ora.bf16_bits_to_f32(bits), np.array(kat["expected"], dtype=np.float32))
+
+
+def torch_reference_dequant_bits(qweight, qzeros, scales_bits, group_size):
+    """The reference backend's arithmetic (awq.py:243-248) evaluated with torch bf16 ops."""
+    q = torch.from_numpy(ora.unpack_awq_int4(qweight))
+    z = torch.from_numpy(ora.unpack_awq_int4(qzeros)).repeat_interleave(group_size, dim=0)
+    s = torch.from_numpy(scales_bits.view(np.int16).copy()).view(torch.bfloat16)
+    s = s.repeat_interleave(group_size, dim=0)
+    w = (q.to(torch.bfloat16) - z.to(torch.bfloat16)) * s
+    return w.view(torch.int16).numpy().view(np.uint16)
+
+
+def test_dequant_matches_torch_bf16_arithmetic_including_special_scales():
+    rng = np.random.default_rng(3)
+    k, n, g = 512, 64, 128
+    q = rng.integers(0, 16, size=(k, n))
+    z = rng.integers(0, 16, size=(k // g, n))
+    q[:g, :8] = z[0, :8]  # q == z
+    s = rng.uniform(0.002, 0.02, size=(k // g, n)).astype(np.float32)
+    s[0, 8:16] = 0.0
+    s[0, 16:24] = -0.0
+    s[0, 24:32] = -0.013
+    s[1, :8] = np.float32(2.0 ** -131)
+    s[1, 8:16] = np.float32(2.0 ** -126)
+    s[1, 16:24] = np.float32(1.0e38)
+    s[1, 24:32] = np.inf
+    s[2, :8] = -np.inf
+    s[2, 8:16] = np.nan
+    s[2, 16:24] = np.float32(3.389e38)  # near bf16 max: products overflow to inf
+    qw, qz, sb = ora.pack_awq_int4(q), ora.pack_awq_int4(z), ora.f32_to_bf16_bits(s)
+    ours = ora.dequantize_awq_gemm_bits(qw, qz, sb, g)
+    theirs = torch_reference_dequant_bits(qw, qz, sb, g)
+    nan_ours = np.isnan(ora.bf16_bits_to_f32(ours))
+    nan_theirs = np.isnan(ora.bf16_bits_to_f32(theirs))
+    np.testing.assert_array_equal(nan_ours, nan_theirs)
+    np.testing.assert_array_equal(ours[~nan_ours], theirs[~nan_ours])
+    assert nan_ours.any() and (ours == 0x8000).any() and (ours == 0x7F80).any()
+
+
+def test_dequant_matches_torch_on_seeded_qwen_like_tile():
+    p = ora.make_problem(seed=9, m=1, k=1024, n=512)
+    ours = ora.dequantize_awq_gemm_bits(p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    theirs = torch_reference_dequant_bits(p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    np.testing.assert_array_equal(ours, theirs)
+
+
+def test_dequant_invariants():
+    rng = np.random.default_rng(4)
+    k, n, g = 256, 32, 128
+    z = rng.integers(0, 16, size=(k // g, n))
+    s = ora.f32_to_bf16_bits(rng.uniform(0.002, 0.02, size=(k // g, n)))
+    # q == z everywhere -> +0 exactly
+    q = np.repeat(z, g, axis=0)
+    w = ora.dequantize_awq_gemm_bits(ora.pack_awq_int4(q), ora.pack_awq_int4(z), s, g)
+    assert np.all(w == 0)
+    # power-of-two scales are exact: W == (q - z) * 2^-e
+    q = rng.integers(0, 16, size=(k, n))
+    s2 = ora.f32_to_bf16_bits(np.full((k // g, n), 2.0 ** -7, dtype=np.float32))
+    w = ora.bf16_bits_to_f32(ora.dequantize_awq_gemm_bits(ora.pack_awq_int4(q), ora.pack_awq_int4(z), s2, g))
+    np.testing.assert_array_equal(w, (q - np.repeat(z, g, axis=0)) * 2.0 ** -7)
+    # changing group 1's zero point changes rows [g, 2g) only
+    z2 = z.copy()
+    z2[1] = (z2[1] + 3) % 16
+    a = ora.dequantize_awq_gemm_bits(ora.pack_awq_int4(q), ora.pack_awq_int4(z), s, g)
+    b = ora.dequantize_awq_gemm_bits(ora.pack_awq_int4(q), ora.pack_awq_int4(z2), s, g)
+    assert np.array_equal(a[:g], b[:g]) and not np.array_equal(a[g:], b[g:])
+
+
+def test_validation_messages_match_reference_contract():
+    qw = np.zeros((4, 1), dtype=np.int32)
+    qz = np.zeros((2, 1), dtype=np.int32)
+    s = np.ones((2, 8), dtype=np.float32)
+    with pytest.raises(ValueError, match="qweight.*int32"):
+        ora.dequantize_awq_gemm_f32(qw.astype(np.int64), qz, s, 2)
+    with pytest.raises(ValueError, match="qzeros.*int32"):
+        ora.dequantize_awq_gemm_f32(qw, qz.astype(np.int64), s, 2)
+    with pytest.raises(ValueError, match="scales"):
+        ora.dequantize_awq_gemm_f32(qw, qz, np.ones((2, 7), dtype=np.float32), 2)
+    with pytest.raises(ValueError, match="divisible"):
+        ora.dequantize_awq_gemm_f32(np.zeros((5, 1), dtype=np.int32), qz, s, 2)
+
+
+# --------------------------------------------------------------------- linear
+def test_linear_kat_group2_fp32():
+    kat = kats()
+    d = kat["dequant_group2_fp32"]
+    qw = ora.pack_awq_int4(np.array(d["qvalues"]))
+    qz = ora.pack_awq_int4(np.array(d["zeros"]))
+    sb = ora.f32_to_bf16_bits(np.array(d["scales"], dtype=np.float32))
+    x = np.array(kat["linear_group2_fp32"]["inputs"], dtype=np.float32)
+    y = ora.awq_linear_ref(ora.f32_to_bf16_bits(x), qw, qz, sb, d["group_size"], accum="f32")
+    assert y.shape == (1, 2, 8)
+    np.testing.assert_array_equal(y, np.array(kat["linear_group2_fp32"]["expected"], dtype=np.float32))
+
+
+def exact_linear(x_bits, qweight, qzeros, scales_bits, g):
+    """Brute force with Python Fractions and explicit nibble extraction."""
+    qwu = np.asarray(qweight).view(np.uint32)
+    qzu = np.asarray(qzeros).view(np.uint32)
+    xf = ora.bf16_bits_to_f32(x_bits)
+    sf = ora.bf16_bits_to_f32(scales_bits)
+    m, k = xf.shape
+    n = qwu.shape[1] * 8
+    out = [[Fraction(0)] * n for _ in range(m)]
+    for kk in range(k):
+        for nn in range(n):
+            slot = ora.AWQ_PACK_ORDER.index(nn % 8)
+            q = (int(qwu[kk, nn // 8]) >> (4 * slot)) & 0xF
+            z = (int(qzu[kk // g, nn // 8]) >> (4 * slot)) & 0xF
+            wf = np.array([np.float32(q - z) * sf[kk // g, nn]], dtype=np.float32)
+            w = Fraction(float(ora.bf16_bits_to_f32(ora.f32_to_bf16_bits(wf))[0]))
+            for mm in range(m):
+                out[mm][nn] += Fraction(float(xf[mm, kk])) * w
+    return np.array([[float(v) for v in row] for row in out])
+
+
+def test_linear_matches_exact_rational_brute_force():
+    p = ora.make_problem(seed=21, m=3, k=256, n=16)
+    want = exact_linear(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    got64 = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128, accum="f64")
+    got32 = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128, accum="f32")
+    np.testing.assert_allclose(got64, want, rtol=1e-12, atol=1e-12)
+    assert ora.gemm_rel_err(got32, want) < 1e-5
+
+
+def test_linear_is_linear_in_x_and_zero_for_zero_scales():
+    p = ora.make_problem(seed=22, m=4, k=256, n=64)
+    x = ora.bf16_bits_to_f32(p["x_bits"])
+    xa = ora.f32_to_bf16_bits(x * 2.0)  # exact scaling by 2
+    ya = ora.awq_linear_ref(xa, p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    y = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+    np.testing.assert_array_equal(ya, 2.0 * y)
+    zero_s = np.zeros_like(p["scales_bits"])
+    assert np.all(ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], zero_s, 128) == 0)
+
+
+def test_linear_rejects_k_mismatch():
+    p = ora.make_problem(seed=1, m=1, k=256, n=16)
+    with pytest.raises(ValueError, match="K must match"):
+        ora.awq_linear_ref(p["x_bits"][:, :128], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+
+
+# ------------------------------------------------------------------- producer
+def test_quantizer_exact_roundtrip_kat():
+    kat = kats()["quantize_exact_roundtrip"]
+    w = np.array(kat["weight"], dtype=np.float32)
+    qw, qz, sb = ora.quantize_awq_weight(w, group_size=kat["group_size"])
+    assert qw.shape == (4, 1) and qz.shape == (2, 1) and sb.shape == (2, 8)
+    np.testing.assert_array_equal(ora.bf16_bits_to_f32(sb), np.array(kat["expected_scales"], dtype=np.float32))
+    np.testing.assert_array_equal(ora.unpack_awq_int4(qw), np.array(kat["expected_qweight_values"]))
+    np.testing.assert_array_equal(ora.unpack_awq_int4(qz), np.array(kat["expected_zero_values"]))
+    restored = ora.bf16_bits_to_f32(ora.dequantize_awq_gemm_bits(qw, qz, sb, kat["group_size"])).T
+    np.testing.assert_array_equal(restored, w)
+
+
+def test_quantizer_matches_explicit_asymmetric_reference():
+    # tests/test_awq_quantizer.py:43-72, with a numpy generator
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((16, 128)).astype(np.float32)
+    mn, mx = w.min(axis=1, keepdims=True), w.max(axis=1, keepdims=True)
+    s = np.maximum(mx - mn, 1e-5) / 15
+    z = np.clip(-np.round(mn / s), 0, 15)
+    expected = (np.clip(np.round(w / s) + z, 0, 15) - z) * s
+    qw, qz, sb = ora.quantize_awq_weight(w, group_size=128)
+    got = ora.bf16_bits_to_f32(ora.dequantize_awq_gemm_bits(qw, qz, sb, 128)).T
+    np.testing.assert_allclose(got, expected, rtol=0.01, atol=0.01)
+
+
+def test_quantizer_rejects_unsupported_shapes():
+    with pytest.raises(ValueError, match="two-dimensional"):
+        ora.quantize_awq_weight(np.zeros(8, dtype=np.float32), group_size=2)
+    with pytest.raises(ValueError, match="floating"):
+        ora.quantize_awq_weight(np.zeros((8, 4), dtype=np.int32), group_size=2)
+    with pytest.raises(ValueError, match="input size"):
+        ora.quantize_awq_weight(np.zeros((8, 5), dtype=np.float32), group_size=2)
+    with pytest.raises(ValueError, match="output size"):
+        ora.quantize_awq_weight(np.zeros((7, 4), dtype=np.float32), group_size=2)
+
+
+# -------------------------------------------------------------- golden fixture
+def test_oracle_reproduces_committed_golden_fixture():
+    data = np.load(os.path.join(GOLDEN, "awq_small_seeded.npz"))
+    names = sorted({k.split(".")[0] for k in data.files})
+    assert {"m1", "m16", "m64", "outlier_m32", "special_scales"} <= set(names)
+    for name in names:
+        qw, qz, sb, xb = (data[f"{name}.{t}"] for t in ("qweight", "qzeros", "scales_bits", "x_bits"))
+        np.testing.assert_array_equal(ora.dequantize_awq_gemm_bits(qw, qz, sb, 128), data[f"{name}.w_bits"])
+        np.testing.assert_array_equal(ora.awq_linear_ref(xb, qw, qz, sb, 128), data[f"{name}.y_f64"])
+
+
+def test_metric_floor_behaviour():
+    r = np.array([1.0, -1.0, 1e-6, 0.0])
+    assert ora.gemm_rel_err(r, r) == 0.0
+    # rms(r) = sqrt(0.5): the two small entries are judged against that floor
+    assert ora.gemm_rel_err(r + 0.01, r) == pytest.approx(0.01 / np.sqrt(0.5), rel=1e-9)
