@@ -66,17 +66,19 @@ int w4a16_unpack_int4(const int32_t* packed, int32_t* out, int rows, int cols, v
 int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
                   uint16_t* w_out, int K, int N, int group_size, void* stream);
 
-/* Rewrite qweight [K, N/8] into the gfx950 MFMA fragment layout consumed by w4a16_gemm
- * (same byte size: K*N/2).  One 1 KiB block per (128-row group g, 16-column tile t):
- * word [(g*(N/16) + t)*256 + lane*4 + j] holds the 8 values k = 128g + 32j + 8(lane/16) + i,
- * n = 16t + lane%16, value i at bit 4*(0,4,1,5,2,6,3,7)[i].  K % 128 == 0, N % 16 == 0.
+/* Reorder qweight [K, N/8] into the group-block layout consumed by w4a16_gemm (same
+ * words, same byte size K*N/2; each word keeps its 8 columns in AutoAWQ nibble order).
+ * One 2 KiB block per (128-row group g, 32-column block b); word
+ * [((g*(N/32) + b)*64 + lane)*8 + 2*js + h] is qweight[k][4b + lane/16] with
+ * k = 128g + 32js + 8*((lane%16)/4) + 4h + lane%4.  K % 128 == 0, N % 32 == 0.
  * Replaces repack_qweight (awq_w4a16.cu:81-109, 256-272) / repack_awq_qweight_cuda
  * (awq_cuda.py:129-132).  qzeros need no reorder: the kernels read them as stored, so
  * reorder_qzeros (awq_w4a16.cu:111-118, 274-286) has no counterpart. */
 int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, void* stream);
 
-/* Dequantize from the repacked layout (same bits as w4a16_dequant).  Uses the dequant
- * routine of the MFMA tile GEMM; exists to verify both bit-exactly.  No reference
+/* Dequantize from the repacked layout through the GEMM kernels' matrix-core dequant
+ * (same bits as w4a16_dequant for every finite scale with |s| < 2^123, zero signs aside);
+ * exists to verify that path bit-exactly.  K % 128 == 0, N % 32 == 0.  No reference
  * counterpart beyond dequantize_awq_gemm (awq.py:235-248). */
 int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
                          uint16_t* w_out, int K, int N, int group_size, void* stream);
@@ -88,8 +90,9 @@ int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uin
 size_t w4a16_workspace_bytes(int M, int K, int N, int group_size);
 
 /* y[M, N] = x[M, K] @ W with W given as (packed, qzeros, scales); bf16 in and out, fp32
- * accumulation.  M >= 0 (M == 0 is a no-op), K % 128 == 0, N % 64 == 0, group_size == 128;
- * x, packed, y 16-byte aligned.
+ * accumulation.  M >= 0 (M == 0 is a no-op), K % 128 == 0, N % 64 == 0, group_size == 128,
+ * K * N / 2 < 2^31 bytes of packed weights; x, packed, y 16-byte and qzeros, scales 4-byte
+ * aligned.
  * Replaces linear (awq_w4a16.cu:288-371) / awq_cuda_linear (awq_cuda.py:141-185) and the
  * reference backend awq_reference_linear (awq.py:251-276). */
 int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
@@ -106,13 +109,14 @@ int w4a16_regime(int M, int K, int N);
 int w4a16_split_k(int M, int K, int N);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
- * W4A16_REGIME_DECODE (p0 = column tiles per workgroup in {1,2,4}, p1 = waves per
- * workgroup in {4,8,16}, M <= 64) or W4A16_REGIME_TILE (p0 = 16-row tiles per wave in
- * {8,16}); 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook
- * (it exercises every split-K reduction path at small sizes). */
+ * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {2,4}, p1 = waves per
+ * workgroup in {4,8,16}, p2 = 128-row groups in flight per wave in {1,2,4}, M <= 64) or
+ * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {8,16}; p1, p2 ignored);
+ * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises
+ * every split-K reduction path at small sizes). */
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
                       const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
-                      int regime, int p0, int p1, int split, void* workspace,
+                      int regime, int p0, int p1, int p2, int split, void* workspace,
                       size_t workspace_bytes, void* stream);
 
 /* Workspace bytes w4a16_gemm_config needs for that configuration.  No reference counterpart. */

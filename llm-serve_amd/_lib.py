@@ -36,7 +36,7 @@ _SIGNATURES = {
     "w4a16_regime": (_c_int, [_c_int, _c_int, _c_int]),
     "w4a16_split_k": (_c_int, [_c_int, _c_int, _c_int]),
     "w4a16_gemm_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
-                                   _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
     "w4a16_workspace_bytes_config": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
 }
 ABI_VERSION = 1
@@ -146,14 +146,15 @@ class W4A16Library:
         return y
 
     def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,
-                    split: int, workspace: torch.Tensor | None, group_size: int = 128) -> torch.Tensor:
+                    split: int, workspace: torch.Tensor | None, group_size: int = 128,
+                    p2: int = 0) -> torch.Tensor:
         m = x.shape[0]
         ws_ptr = workspace.data_ptr() if workspace is not None else None
         ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
         with torch.cuda.device(x.device):
             self.check(self.dll.w4a16_gemm_config(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
                                                   scales.data_ptr(), y.data_ptr(), m, k, n, group_size, regime,
-                                                  p0, p1, split, ws_ptr, ws_len, self._stream(x)),
+                                                  p0, p1, p2, split, ws_ptr, ws_len, self._stream(x)),
                        "w4a16_gemm_config")
         return y
 

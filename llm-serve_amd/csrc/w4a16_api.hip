@@ -32,6 +32,9 @@ int check_launch(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr int kDecodeMaxM = 64;
+// The decode kernel addresses each input through a buffer descriptor with 32-bit byte
+// offsets and uses offsets >= 2^31 as "fetch nothing".
+constexpr size_t kMaxTensorBytes = size_t(1) << 31;
 constexpr size_t kDecodeMaxLds = 64 * 1024;  // LDS of the decode kernel's wave reduction
 
 // LDS the decode kernel's cross-wave reduction needs: one f32x4 per lane per (wave, m-block, tile).
@@ -44,6 +47,7 @@ struct GemmPlan {
   int regime;  // w4a16_regime_id
   int p0;      // decode: column tiles per workgroup; tile: wm (16-row tiles per wave)
   int p1;      // decode: waves per workgroup; tile: unused
+  int p2;      // decode: groups in flight per wave; tile: unused
   int split;   // K splits (1 = none)
 };
 
@@ -54,11 +58,10 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // small against the weight stream (K * N / 2 bytes).
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  GemmPlan p{W4A16_REGIME_DECODE, 4, 4, 1};
+  GemmPlan p{W4A16_REGIME_DECODE, 4, 4, 2, 1};
   const int target = 512;
   int tn = 4;
   if (N / 64 < 256) tn = 2;
-  if (N / 32 < 128) tn = 1;
   const int blocks = N / (16 * tn);
   int split = ceil_div(target, blocks);
   const int waves = 4;  // decode_lds_bytes(64, 4, 4) = 64 KiB: always within kDecodeMaxLds
@@ -73,7 +76,7 @@ GemmPlan plan_decode(int M, int K, int N) {
 
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  GemmPlan p{W4A16_REGIME_TILE, 16, 0, 1};
+  GemmPlan p{W4A16_REGIME_TILE, 16, 0, 0, 1};
   const int wm = M <= 128 ? 8 : 16;
   const int tiles = ceil_div(M, 16 * wm) * ceil_div(N, 256);
   int split = 1;
@@ -84,7 +87,7 @@ GemmPlan plan_tile(int M, int K, int N) {
 }
 
 GemmPlan plan(int M, int K, int N) {
-  if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 1};
+  if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
   return M <= kDecodeMaxM ? plan_decode(M, K, N) : plan_tile(M, K, N);
 }
 
@@ -111,11 +114,16 @@ int validate_gemm(const void* x, const void* packed, const void* qzeros, const v
     return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
   if (N % 64) return fail(W4A16_ERR_SHAPE, "N must be divisible by 64 (got %d)", N);
+  if (static_cast<size_t>(K) * N / 2 >= kMaxTensorBytes)
+    return fail(W4A16_ERR_SHAPE, "packed weights of K=%d N=%d exceed 2 GiB", K, N);
+  if (static_cast<size_t>(M) * K * 2 >= kMaxTensorBytes && M <= kDecodeMaxM)
+    return fail(W4A16_ERR_SHAPE, "activations of M=%d K=%d exceed 2 GiB", M, K);
   if (M == 0) return ok();
   if (!x || !packed || !qzeros || !scales || !y) return fail(W4A16_ERR_ARG, "null tensor pointer");
   if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(y, 16))
     return fail(W4A16_ERR_ALIGN, "x, packed qweight and y must be 16-byte aligned");
-  if (!aligned(qzeros, 4) || !aligned(scales, 2)) return fail(W4A16_ERR_ALIGN, "qzeros/scales misaligned");
+  if (!aligned(qzeros, 4) || !aligned(scales, 4))
+    return fail(W4A16_ERR_ALIGN, "qzeros and scales must be 4-byte aligned");
   return ok();
 }
 
@@ -135,8 +143,8 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const uint32_t* pk = reinterpret_cast<const uint32_t*>(packed);
   const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
   if (p.regime == W4A16_REGIME_DECODE)
-    return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p1,
-                                                 p.split, stream),
+    return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p2,
+                                                 p.p1, p.split, stream),
                         "decode");
   return check_launch(w4a16::launch_tile_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.split, stream),
                       "tile");
@@ -177,7 +185,7 @@ int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
 int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, void* stream) {
   if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
-  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
+  if (N % 32) return fail(W4A16_ERR_SHAPE, "N must be divisible by 32 (got %d)", N);
   if (!qweight || !packed) return fail(W4A16_ERR_ARG, "null tensor pointer");
   if (!aligned(qweight, 4) || !aligned(packed, 16)) return fail(W4A16_ERR_ALIGN, "packed must be 16-byte aligned");
   return check_launch(w4a16::launch_repack(reinterpret_cast<const uint32_t*>(qweight),
@@ -191,9 +199,10 @@ int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uin
   if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
   if (group_size != w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
-  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
+  if (N % 32) return fail(W4A16_ERR_SHAPE, "N must be divisible by 32 (got %d)", N);
   if (!packed || !qzeros || !scales || !w_out) return fail(W4A16_ERR_ARG, "null tensor pointer");
-  if (!aligned(packed, 16) || !aligned(w_out, 2)) return fail(W4A16_ERR_ALIGN, "packed must be 16-byte aligned");
+  if (!aligned(packed, 16) || !aligned(w_out, 2) || !aligned(scales, 4) || !aligned(qzeros, 4))
+    return fail(W4A16_ERR_ALIGN, "packed must be 16-byte and scales, qzeros 4-byte aligned");
   return check_launch(w4a16::launch_dequant_packed(reinterpret_cast<const uint32_t*>(packed),
                                                    reinterpret_cast<const uint32_t*>(qzeros), scales, w_out, K, N,
                                                    static_cast<hipStream_t>(stream)),
@@ -224,18 +233,19 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, 
 }
 
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
-                      uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int split,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+                      uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int p2,
+                      int split, void* workspace, size_t workspace_bytes, void* stream) {
   const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
   const int G = K / w4a16::kGroup;
-  GemmPlan p{regime, p0, p1, split};
+  GemmPlan p{regime, p0, p1, p2, split};
   if (split < 1 || split > G) return fail(W4A16_ERR_ARG, "split must be in [1, K/128] (got %d)", split);
   if (regime == W4A16_REGIME_DECODE) {
     if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
-    if (p0 != 1 && p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2 or 4");
+    if (p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 2 or 4");
     if (p1 != 4 && p1 != 8 && p1 != 16) return fail(W4A16_ERR_ARG, "decode waves must be 4, 8 or 16");
+    if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
     if (decode_lds_bytes(M, p0, p1) > kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
                   decode_lds_bytes(M, p0, p1), kDecodeMaxLds);
@@ -250,7 +260,7 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
 
 size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split) {
   if (M <= 0 || N <= 0) return 0;
-  return workspace_for(GemmPlan{regime, p0, 0, split}, M, N);
+  return workspace_for(GemmPlan{regime, p0, 0, 0, split}, M, N);
 }
 
 }  // extern "C"

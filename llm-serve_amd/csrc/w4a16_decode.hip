@@ -1,116 +1,180 @@
 // Decode / speculative-verify regime (M <= 64): HBM-bound split-K kernel.
 //
-// Each lane dequantizes its weights in registers exactly as the reference does --
-// bf16_rne((q - z) s), see dequant_k8 -- and feeds them to v_mfma_f32_16x16x32_bf16
-// against up to four 16-row activation fragments, accumulating in fp32.  The output is
-// therefore the reference's matmul over the reference's bf16 weights, up to fp32
-// summation order.
+// Each wave streams (128-row group, 32-column block) weight blocks (2 KiB, two 16-byte
+// loads per lane), dequantizes them on the matrix cores (dequant_block: the reference's
+// bf16_rne((q - z) s) weights) and multiplies them with up to four 16-row activation
+// fragments by v_mfma_f32_16x16x32_bf16, accumulating in fp32.  The output is the
+// reference's matmul over the reference's bf16 weights up to fp32 summation order.
 //
-// Work split.  A workgroup owns TN 16-column tiles (16 TN columns) and one K range
-// (blockIdx.y of `split`); its W waves take interleaved 128-row groups of that range and
-// are reduced through LDS in a fixed order.  With split > 1 the workgroups write fp32
-// partials; the last one to finish a column block (atomic arrival counter) sums them in
-// split order and writes bf16, then re-arms the counter to zero.  Results are therefore
-// deterministic run to run.
+// Work split.  A workgroup owns TB 32-column blocks and one K range (blockIdx.y of
+// `split`); its W waves take interleaved 128-row groups of that range, are reduced
+// through LDS in a fixed order, and with split > 1 the workgroups exchange fp32 partials
+// (store_partial / arrive / load_partial): the last one to finish a column block sums
+// them in split order, writes bf16 and re-arms the counter.  Results are deterministic.
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
 
 namespace w4a16 {
 
-template <int MB, int TN, int WAVES>
+struct DecodeArgs {
+  const uint16_t* x;
+  const uint32_t* packed;
+  const uint32_t* qzeros;
+  const uint16_t* scales;
+  uint16_t* y;
+  float* partials;
+  int* counters;
+  int M, K, N, split;
+};
+
+// Everything one wave needs for one 128-row group: two 16-byte weight loads per block,
+// the raw scale-pair and zero words of its 2 TB output columns, and the MB x 4 activation
+// fragments.  Loaded DEPTH groups ahead of use; decoded only when consumed.
+template <int MB, int TB>
+struct DecodeStage {
+  u32x4_t w[TB][2];
+  uint32_t s[TB][2];
+  uint32_t zw[TB][2];
+  u32x4_t a[MB][4];
+};
+
+// Buffer descriptors of the four inputs.  Every load of the decode kernel is an
+// unconditional buffer load: a lane or a group with nothing to fetch (activation row >= M,
+// group past the workgroup's K range) uses kOutOfRange, which the hardware answers with
+// zeros and no memory access.  With no branch around any load the compiler's wait counts
+// are exact, so the DEPTH groups in flight really overlap.
+struct DecodeSources {
+  __amdgpu_buffer_rsrc_t x, w, s, z;
+};
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // >= every num_records (checked on the host)
+constexpr int kRawBufferWord3 = 0x00020000;    // raw (untyped) buffer, 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           kRawBufferWord3);
+}
+
+// Byte offsets that do not depend on the group: per activation fragment row (or
+// kOutOfRange for rows >= M), and per block of the lane's weight words.
+template <int MB>
+struct DecodeOffsets {
+  uint32_t x_row[MB];  // (row K + 8 (lane / 16)) * 2, or kOutOfRange
+};
+
+template <int MB, int TB>
+__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TB>& st, const DecodeSources& src,
+                                                  const DecodeOffsets<MB>& off, int g, bool valid, int N, int cb,
+                                                  int lane) {
+  const int NB = N / kBlockCols;
+  const int c = lane & 15;
+  const uint32_t oob = valid ? 0u : kOutOfRange;
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb) {
+    const int b = cb * TB + tb;
+    const uint32_t wo = (valid ? static_cast<uint32_t>(block_word(g, b, NB, lane)) * 4u : 0u) | oob;
+    st.w[tb][0] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
+    st.w[tb][1] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo + 16u, 0, 0);
+    const uint32_t so = oob | (static_cast<uint32_t>(g * N + kBlockCols * b + (c & ~1)) * 2u);
+    const uint32_t zo = oob | (static_cast<uint32_t>(g * (N >> 3) + 4 * b + (c >> 3)) * 4u);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      st.s[tb][u] = __builtin_amdgcn_raw_buffer_load_b32(src.s, so + 32u * u, 0, 0);
+      st.zw[tb][u] = __builtin_amdgcn_raw_buffer_load_b32(src.z, zo + 8u * u, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const uint32_t xo = (off.x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 2u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st.a[mb][j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 64u * j, 0, 0);
+  }
+}
+
+template <int MB, int TB>
+__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][2 * TB], const DecodeStage<MB, TB>& st,
+                                                     const NibbleConsts& nib, int lane) {
+  const int zshift = awq_shift(lane & 7);
+  TileScale ts[TB][2];
+#pragma unroll
+  for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ts[tb][u] = make_tile_scale(st.s[tb][u], (st.zw[tb][u] >> zshift) & 0xFu, u, lane);
+#pragma unroll
+  for (int js = 0; js < 4; ++js) {
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const u32x4_t& v = st.w[tb][js >> 1];
+      const uint32_t w0 = (js & 1) ? v[2] : v[0];
+      const uint32_t w1 = (js & 1) ? v[3] : v[1];
+      bf16x8_t frag[2];
+      dequant_block(frag, w0, w1, ts[tb], nib);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[mb][2 * tb + u] = mfma16(__builtin_bit_cast(bf16x8_t, st.a[mb][js]), frag[u], acc[mb][2 * tb + u]);
+    }
+  }
+}
+
+template <int MB, int TB, int DEPTH, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
-                                                      const uint4* __restrict__ packed,
-                                                      const uint32_t* __restrict__ qzeros,
-                                                      const uint16_t* __restrict__ scales,
-                                                      uint16_t* __restrict__ y, float* __restrict__ partials,
-                                                      int* __restrict__ counters, int M, int K, int N,
-                                                      int split) {
+                                                            const uint32_t* __restrict__ packed,
+                                                            const uint32_t* __restrict__ qzeros,
+                                                            const uint16_t* __restrict__ scales,
+                                                            uint16_t* __restrict__ y, float* __restrict__ partials,
+                                                            int* __restrict__ counters, int M, int K, int N,
+                                                            int split) {
+  constexpr int TN = 2 * TB;  // 16-column tiles per workgroup
   extern __shared__ f32x4_t red[];  // [W][MB][TN][64]
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   constexpr int W = WAVES;
-  const int NT = N >> 4;
   const int G = K / kGroup;
   const int cb = blockIdx.x;
   const int sidx = blockIdx.y;
   const int g_begin = (G * sidx) / split;
   const int g_end = (G * (sidx + 1)) / split;
   const int col0 = cb * (16 * TN) + (lane & 15);  // this lane's column in tile 0
-  const f32x4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-  const u32x4_t zero_u = {0u, 0u, 0u, 0u};
-  const bf16x8_t zero_a = __builtin_bit_cast(bf16x8_t, zero_u);
+
+  DecodeSources src;
+  src.x = make_rsrc(x, static_cast<uint32_t>(M) * K * 2u);
+  src.w = make_rsrc(packed, static_cast<uint32_t>(K) * (N / 2));
+  src.s = make_rsrc(scales, static_cast<uint32_t>(G) * N * 2u);
+  src.z = make_rsrc(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u);
+  DecodeOffsets<MB> off;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int row = 16 * mb + (lane & 15);
+    off.x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * 2u : kOutOfRange;
+  }
 
   f32x4_t acc[MB][TN];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int tt = 0; tt < TN; ++tt) acc[mb][tt] = zero4;
+    for (int tt = 0; tt < TN; ++tt) acc[mb][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // One-group-ahead prefetch of the HBM stream (weights, scales, zeros).
-  uint4 bw[TN];
-  float sc[TN];
-  uint32_t zz[TN];
-  int g = g_begin + wave;
-  if (g < g_end) {
+  // Depth-DEPTH ring over the wave's groups g0 + i W (g0 = g_begin + wave): group i is
+  // loaded while group i - DEPTH is being consumed.  The first trip only loads (its
+  // compute guards are all false), so the loop is the only place loads are issued and
+  // each stage's wait is "all but the DEPTH - 1 younger stages".  Loads are issued
+  // whether or not the group exists (out-of-range ones fetch nothing): no branch encloses
+  // a load, and the scheduling barriers keep each stage's loads together and in order.
+  DecodeStage<MB, TB> ring[DEPTH];
+  const int g0 = g_begin + wave;
+  const NibbleConsts nib = nibble_consts();
+  for (int base = g0 - DEPTH * W; base < g_end; base += DEPTH * W) {
 #pragma unroll
-    for (int tt = 0; tt < TN; ++tt) {
-      const int n = col0 + 16 * tt;
-      bw[tt] = packed[(static_cast<size_t>(g) * NT + cb * TN + tt) * 64 + lane];
-      sc[tt] = bf16_bits_to_f32(scales[static_cast<size_t>(g) * N + n]);
-      zz[tt] = load_zero(qzeros, g, N, n);
-    }
-  }
-  for (; g < g_end; g += W) {
-    const int gn = g + W;
-    uint4 bw_n[TN];
-    float sc_n[TN];
-    uint32_t zz_n[TN];
-    if (gn < g_end) {
-#pragma unroll
-      for (int tt = 0; tt < TN; ++tt) {
-        const int n = col0 + 16 * tt;
-        bw_n[tt] = packed[(static_cast<size_t>(gn) * NT + cb * TN + tt) * 64 + lane];
-        sc_n[tt] = bf16_bits_to_f32(scales[static_cast<size_t>(gn) * N + n]);
-        zz_n[tt] = load_zero(qzeros, gn, N, n);
-      }
-    }
-    // Activation fragments: row 16 mb + lane % 16, k = 128 g + 32 j + 8 (lane / 16) .. +7.
-    bf16x8_t a[MB][4];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int row = 16 * mb + (lane & 15);
-      const bf16x8_t* src = reinterpret_cast<const bf16x8_t*>(
-          x + static_cast<size_t>(row) * K + kGroup * g + 8 * (lane >> 4));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (row < M) {
-          a[mb][j] = src[4 * j];
-        } else {
-          a[mb][j] = zero_a;
-        }
-      }
-    }
-    DequantScale d[TN];
-#pragma unroll
-    for (int tt = 0; tt < TN; ++tt) d[tt] = make_dequant_scale(sc[tt], zz[tt]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int tt = 0; tt < TN; ++tt) {
-        const uint32_t wj = j == 0 ? bw[tt].x : j == 1 ? bw[tt].y : j == 2 ? bw[tt].z : bw[tt].w;
-        const bf16x8_t b = dequant_k8(wj, d[tt]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb][tt] = mfma16(a[mb][j], b, acc[mb][tt]);
-      }
-    }
-    if (gn < g_end) {
-#pragma unroll
-      for (int tt = 0; tt < TN; ++tt) {
-        bw[tt] = bw_n[tt];
-        sc[tt] = sc_n[tt];
-        zz[tt] = zz_n[tt];
-      }
+    for (int d = 0; d < DEPTH; ++d) {
+      const int g = base + d * W;
+      if (g >= g0 && g < g_end) compute_decode_stage<MB, TB>(acc, ring[d], nib, lane);
+      const int gn = g + DEPTH * W;
+      __builtin_amdgcn_sched_barrier(0);
+      load_decode_stage<MB, TB>(ring[d], src, off, gn, gn < g_end, N, cb, lane);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -155,18 +219,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * (p / TN) + 4 * (lane >> 4) + i;
-      if (row < M) partials[(static_cast<size_t>(sidx) * M + row) * N + n] = out[p][i];
+      if (row < M) store_partial(partials + (static_cast<size_t>(sidx) * M + row) * N + n, out[p][i]);
     }
   }
-  __threadfence();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int arrived = __hip_atomic_fetch_add(&counters[cb], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (arrived == split - 1);
-  }
+  if (threadIdx.x == 0) is_last = (arrive(&counters[cb]) == split - 1);
   __syncthreads();
   if (!is_last) return;
-  __threadfence();
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
     if (p % W != wave) continue;
@@ -177,56 +236,56 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
       if (row < M) {
         float v = 0.0f;
         for (int s = 0; s < split; ++s)
-          v += (s == sidx) ? out[p][i] : partials[(static_cast<size_t>(s) * M + row) * N + n];
+          v += (s == sidx) ? out[p][i] : load_partial(partials + (static_cast<size_t>(s) * M + row) * N + n);
         y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(v);
       }
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) rearm(&counters[cb]);
 }
 
-template <int MB, int TN, int WAVES>
-static hipError_t launch_decode_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                                  const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M,
-                                  int K, int N, int split, hipStream_t stream) {
-  const dim3 grid(N / (16 * TN), split);
-  const size_t lds = static_cast<size_t>(WAVES) * MB * TN * 64 * sizeof(f32x4_t);
-  decode_kernel<MB, TN, WAVES><<<grid, 64 * WAVES, lds, stream>>>(
-      x, reinterpret_cast<const uint4*>(packed), qzeros, scales, y, partials, counters, M, K, N, split);
+template <int MB, int TB, int DEPTH, int WAVES>
+static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid(a.N / (kBlockCols * TB), a.split);
+  const size_t lds = static_cast<size_t>(WAVES) * MB * 2 * TB * 64 * sizeof(f32x4_t);
+  decode_kernel<MB, TB, DEPTH, WAVES><<<grid, 64 * WAVES, lds, stream>>>(
+      a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split);
   return hipGetLastError();
 }
 
-template <int MB, int TN>
-static hipError_t launch_decode_w(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                                  const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M,
-                                  int K, int N, int waves, int split, hipStream_t stream) {
+template <int MB, int TB, int DEPTH>
+static hipError_t launch_decode_w(const DecodeArgs& a, int waves, hipStream_t stream) {
   switch (waves) {
-    case 4: return launch_decode_t<MB, TN, 4>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
-    case 8: return launch_decode_t<MB, TN, 8>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
-    default: return launch_decode_t<MB, TN, 16>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+    case 4: return launch_decode_t<MB, TB, DEPTH, 4>(a, stream);
+    case 8: return launch_decode_t<MB, TB, DEPTH, 8>(a, stream);
+    default: return launch_decode_t<MB, TB, DEPTH, 16>(a, stream);
+  }
+}
+
+template <int MB, int TB>
+static hipError_t launch_decode_d(const DecodeArgs& a, int depth, int waves, hipStream_t stream) {
+  switch (depth) {
+    case 1: return launch_decode_w<MB, TB, 1>(a, waves, stream);
+    case 2: return launch_decode_w<MB, TB, 2>(a, waves, stream);
+    default: return launch_decode_w<MB, TB, 4>(a, waves, stream);
   }
 }
 
 template <int MB>
-static hipError_t launch_decode_m(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                                  const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M,
-                                  int K, int N, int tn, int waves, int split, hipStream_t stream) {
-  switch (tn) {
-    case 1: return launch_decode_w<MB, 1>(x, packed, qzeros, scales, y, partials, counters, M, K, N, waves, split, stream);
-    case 2: return launch_decode_w<MB, 2>(x, packed, qzeros, scales, y, partials, counters, M, K, N, waves, split, stream);
-    default: return launch_decode_w<MB, 4>(x, packed, qzeros, scales, y, partials, counters, M, K, N, waves, split, stream);
-  }
+static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int waves, hipStream_t stream) {
+  if (tn == 2) return launch_decode_d<MB, 1>(a, depth, waves, stream);
+  return launch_decode_d<MB, 2>(a, depth, waves, stream);
 }
 
-// tn in {1, 2, 4} column tiles per workgroup, waves in {4, 8, 16}, 1 <= split <= K / 128.
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                             int N, int tn, int waves, int split, hipStream_t stream) {
+                             int N, int tn, int depth, int waves, int split, hipStream_t stream) {
+  const DecodeArgs a{x, packed, qzeros, scales, y, partials, counters, M, K, N, split};
   switch ((M + 15) / 16) {
-    case 1: return launch_decode_m<1>(x, packed, qzeros, scales, y, partials, counters, M, K, N, tn, waves, split, stream);
-    case 2: return launch_decode_m<2>(x, packed, qzeros, scales, y, partials, counters, M, K, N, tn, waves, split, stream);
-    case 3: return launch_decode_m<3>(x, packed, qzeros, scales, y, partials, counters, M, K, N, tn, waves, split, stream);
-    default: return launch_decode_m<4>(x, packed, qzeros, scales, y, partials, counters, M, K, N, tn, waves, split, stream);
+    case 1: return launch_decode_m<1>(a, tn, depth, waves, stream);
+    case 2: return launch_decode_m<2>(a, tn, depth, waves, stream);
+    case 3: return launch_decode_m<3>(a, tn, depth, waves, stream);
+    default: return launch_decode_m<4>(a, tn, depth, waves, stream);
   }
 }
 

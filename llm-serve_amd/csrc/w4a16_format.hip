@@ -1,4 +1,4 @@
-// Format kernels: AutoAWQ unpack, bit-exact dequant, and the repack into the K8 fragment
+// Format kernels: AutoAWQ unpack, bit-exact dequant, and the repack into the group-block
 // layout described in w4a16_common.h.  All are HBM-bound byte/integer work.
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
@@ -57,60 +57,63 @@ __global__ __launch_bounds__(256) void dequant_awq_kernel(const uint32_t* __rest
   *reinterpret_cast<uint4*>(w_out + idx * 8) = make_uint4(outw[0], outw[1], outw[2], outw[3]);
 }
 
-// One thread per (8-row block kb, word column c8): reads the 8 words qweight[8kb .. 8kb+7][c8]
-// (coalesced across threads) and writes the 8 K8 words of columns 8 c8 .. 8 c8 + 7.
+// One thread per output word of the group-block layout (see w4a16_common.h): gathers the
+// AutoAWQ word it holds.  Writes are coalesced; this runs once per weight at load time.
 __global__ __launch_bounds__(256) void repack_kernel(const uint32_t* __restrict__ qweight,
                                                      uint32_t* __restrict__ packed, int K, int N) {
-  const int C8 = N >> 3;
   const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= static_cast<size_t>(K >> 3) * C8) return;
-  const int kb = static_cast<int>(idx / C8);
-  const int c8 = static_cast<int>(idx - static_cast<size_t>(kb) * C8);
-  uint32_t in[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) in[i] = qweight[static_cast<size_t>(8 * kb + i) * C8 + c8];
-  const int NT = N >> 4;
-  const int g = kb >> 4;               // 16 eight-row blocks per group
-  const int j = (kb >> 2) & 3;         // 32-row step inside the group
-  const int lane_hi = kb & 3;          // which 8 rows of the 32-row step
-#pragma unroll
-  for (int col = 0; col < 8; ++col) {
-    const int n = 8 * c8 + col;
-    const int src_sh = awq_shift(col);
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) word |= ((in[i] >> src_sh) & 0xFu) << awq_shift(i);
-    const int t = n >> 4;
-    const int lane = lane_hi * 16 + (n & 15);
-    packed[((static_cast<size_t>(g) * NT + t) * 64 + lane) * 4 + j] = word;
-  }
+  const size_t total = static_cast<size_t>(K) * (N >> 3);
+  if (idx >= total) return;
+  const int NB = N / kBlockCols;
+  const int slot = static_cast<int>(idx & 7);
+  const int lane = static_cast<int>((idx >> 3) & 63);
+  const size_t blk = idx >> 9;
+  const int g = static_cast<int>(blk / NB);
+  const int b = static_cast<int>(blk - static_cast<size_t>(g) * NB);
+  const int js = slot >> 1, h = slot & 1;
+  const int row = kGroup * g + 32 * js + 8 * ((lane & 15) >> 2) + 4 * h + (lane & 3);
+  const int cw = 4 * b + (lane >> 4);
+  packed[idx] = qweight[static_cast<size_t>(row) * (N >> 3) + cw];
 }
 
-// One wave per (group, column tile) block; lane reads its 16-byte slice (4 K8 words) and
-// writes 32 bf16 values of its column.  Uses dequant_k8, the MFMA tile GEMM's routine.
+// One wave per (group, 32-column block): the MFMA GEMMs' dequant (dequant_block) run on
+// the block, with every lane writing the 8 rows x 2 columns it produces.  Exists to check
+// that path bit for bit against the reference.
 __global__ __launch_bounds__(256) void dequant_packed_kernel(const uint4* __restrict__ packed,
                                                              const uint32_t* __restrict__ qzeros,
                                                              const uint16_t* __restrict__ scales,
                                                              uint16_t* __restrict__ w_out, int K, int N) {
-  const int NT = N >> 4;
+  const int NB = N / kBlockCols;
   const int lane = threadIdx.x & 63;
-  const size_t block = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const size_t nblocks = static_cast<size_t>(K / kGroup) * NT;
+  const size_t block = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + wave_id();
+  const size_t nblocks = static_cast<size_t>(K / kGroup) * NB;
   if (block >= nblocks) return;  // whole wave exits together
-  const int g = static_cast<int>(block / NT);
-  const int t = static_cast<int>(block - static_cast<size_t>(g) * NT);
-  const int n = 16 * t + (lane & 15);
-  const uint4 v = packed[block * 64 + lane];
-  const float s = bf16_bits_to_f32(scales[static_cast<size_t>(g) * N + n]);
-  const DequantScale d = make_dequant_scale(s, load_zero(qzeros, g, N, n));
-  const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+  const int g = static_cast<int>(block / NB);
+  const int b = static_cast<int>(block - static_cast<size_t>(g) * NB);
+  const uint4* src = packed + block * 128 + lane * 2;
+  const uint4 v0 = src[0], v1 = src[1];
+  const uint32_t words[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  TileScale ts[2];
+  int cols[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const u32x4_t f = __builtin_bit_cast(u32x4_t, dequant_k8(words[j], d));
-    const int k0 = kGroup * g + 32 * j + 8 * (lane >> 4);
+  for (int u = 0; u < 2; ++u) {
+    cols[u] = kBlockCols * b + 16 * u + (lane & 15);
+    const uint32_t s_pair = reinterpret_cast<const uint32_t*>(scales)[(static_cast<size_t>(g) * N + cols[u]) >> 1];
+    ts[u] = make_tile_scale(s_pair, load_zero(qzeros, g, N, cols[u]), u, lane);
+  }
+  const NibbleConsts nib = nibble_consts();
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      w_out[static_cast<size_t>(k0 + i) * N + n] = static_cast<uint16_t>(f[i >> 1] >> (16 * (i & 1)));
+  for (int js = 0; js < 4; ++js) {
+    bf16x8_t frag[2];
+    dequant_block(frag, words[2 * js], words[2 * js + 1], ts, nib);
+    const int k0 = kGroup * g + 32 * js + 8 * (lane >> 4);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const u32x4_t f = __builtin_bit_cast(u32x4_t, frag[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        w_out[static_cast<size_t>(k0 + e) * N + cols[u]] = static_cast<uint16_t>(f[e >> 1] >> (16 * (e & 1)));
+    }
   }
 }
 
@@ -132,14 +135,14 @@ hipError_t launch_dequant(const uint32_t* qweight, const uint32_t* qzeros, const
 }
 
 hipError_t launch_repack(const uint32_t* qweight, uint32_t* packed, int K, int N, hipStream_t stream) {
-  const size_t n = static_cast<size_t>(K >> 3) * (N >> 3);
+  const size_t n = static_cast<size_t>(K) * (N >> 3);
   repack_kernel<<<blocks_for(n, 256), 256, 0, stream>>>(qweight, packed, K, N);
   return hipGetLastError();
 }
 
 hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros, const uint16_t* scales,
                                  uint16_t* w_out, int K, int N, hipStream_t stream) {
-  const size_t waves = static_cast<size_t>(K / kGroup) * (N >> 4);
+  const size_t waves = static_cast<size_t>(K / kGroup) * (N / kBlockCols);
   dequant_packed_kernel<<<blocks_for(waves, 4), 256, 0, stream>>>(
       reinterpret_cast<const uint4*>(packed), qzeros, scales, w_out, K, N);
   return hipGetLastError();

@@ -4,9 +4,9 @@
 // Workgroup = 4 waves, output tile BM x 256 (BM = 16 WM).  Wave w owns columns
 // [64 w, 64 w + 64) of the tile and all BM rows: 4 x WM accumulator tiles of
 // v_mfma_f32_16x16x32_bf16.  Because a wave's columns belong to it alone, each weight is
-// dequantized exactly once per workgroup, straight from its 16-byte K8 load into MFMA
-// B fragments -- bf16_rne((q - z) s), the reference's weights (see dequant_k8) -- with no
-// LDS round trip.  The activation tile (BM rows x one 128-deep group) is shared by all four
+// dequantized exactly once per workgroup, on the matrix cores straight from its 16-byte
+// loads into MFMA B fragments -- bf16_rne((q - z) s), the reference's weights, see
+// dequant_block -- with no LDS round trip.  The activation tile (BM rows x one 128-deep group) is shared by all four
 // waves through LDS: it is brought in by direct-to-LDS 16-byte loads
 // (global_load_lds_dwordx4), double-buffered one group ahead, in a row-major layout whose
 // 16-byte chunks are XOR-swizzled by (row & 7) so the A-fragment reads are conflict-free.
@@ -45,46 +45,57 @@ __device__ __forceinline__ void issue_a_stage(const uint16_t* __restrict__ x, ui
   }
 }
 
-// Raw loads of one group's weights, scales and zero words for a wave's 4 column tiles.
-// Decoding waits until the group is consumed, so the loads stay in flight meanwhile.
+// Raw loads of one group for a wave's 64 columns (two 32-column layout blocks): two
+// 16-byte weight loads per block, and the scale and zero words of the lane's column in
+// each of the 4 tiles.  Decoding waits until the group is consumed.
 struct BGroup {
-  uint4 w[4];
-  uint32_t s[4];   // bf16 bits
-  uint32_t zw[4];  // AutoAWQ zero word holding this lane's column
+  uint4 w[2][2];
+  uint32_t s[2][2];   // bf16 scale pair holding the lane's column
+  uint32_t zw[2][2];  // AutoAWQ zero word holding the lane's column
 };
 
-// Wave-uniform base pointers plus 32-bit lane offsets (scalar-base addressing).
+// Wave-uniform base pointers plus lane offsets (scalar-base addressing).
 __device__ __forceinline__ void load_b_group(BGroup& b, const uint4* __restrict__ packed,
                                              const uint32_t* __restrict__ qzeros,
-                                             const uint16_t* __restrict__ scales, int g, int NT, int N, int nt0,
+                                             const uint16_t* __restrict__ scales, int g, int N, int blk0,
                                              int lane) {
-  const uint4* pw = packed + (static_cast<size_t>(g) * NT + nt0) * 64;
-  const uint16_t* ps = scales + static_cast<size_t>(g) * N + 16 * nt0;
-  const uint32_t* pz = qzeros + static_cast<size_t>(g) * (N >> 3) + 2 * nt0;
+  const int NB = N / kBlockCols;
   const int c = lane & 15;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    b.w[tt] = pw[tt * 64 + lane];
-    b.s[tt] = ps[16 * tt + c];
-    b.zw[tt] = pz[2 * tt + (c >> 3)];
+  for (int tb = 0; tb < 2; ++tb) {
+    const uint4* pw = packed + block_word(g, blk0 + tb, NB, 0) / 4;
+    b.w[tb][0] = pw[2 * lane];
+    b.w[tb][1] = pw[2 * lane + 1];
+    const uint32_t* ps = reinterpret_cast<const uint32_t*>(scales + static_cast<size_t>(g) * N +
+                                                           kBlockCols * (blk0 + tb));
+    const uint32_t* pz = qzeros + static_cast<size_t>(g) * (N >> 3) + 4 * (blk0 + tb);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      b.s[tb][u] = ps[8 * u + (c >> 1)];
+      b.zw[tb][u] = pz[2 * u + (c >> 3)];
+    }
   }
 }
 
-// One 128-deep group: decode scales and zeros, then 4 k-steps of WM x 4 MFMAs.
+// One 128-deep group: per 32-row step, the matrix-core dequant of the wave's 4 weight
+// tiles (8 scaling MFMAs), then WM x 4 main MFMAs against the LDS activation tile.
 template <int WM>
-__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* stage, const BGroup& b, int lane) {
+__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* stage, const BGroup& b,
+                                          const NibbleConsts& nib, int lane) {
   const int arow = lane & 15;
-  const int zshift = awq_shift(lane & 7);  // column 16 t + lane % 16 sits at this offset
-  DequantScale d[4];
+  const int zshift = awq_shift(lane & 7);
+  TileScale ts[2][2];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) d[tt] = make_dequant_scale(bf16_bits_to_f32(b.s[tt]), (b.zw[tt] >> zshift) & 0xFu);
+  for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ts[tb][u] = make_tile_scale(b.s[tb][u], (b.zw[tb][u] >> zshift) & 0xFu, u, lane);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    bf16x8_t bf[4];
+    bf16x8_t bf[2][2];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint32_t wj = j == 0 ? b.w[tt].x : j == 1 ? b.w[tt].y : j == 2 ? b.w[tt].z : b.w[tt].w;
-      bf[tt] = dequant_k8(wj, d[tt]);
+    for (int tb = 0; tb < 2; ++tb) {
+      const uint4& v = b.w[tb][j >> 1];
+      dequant_block(bf[tb], (j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y, ts[tb], nib);
     }
     const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 7);
     const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
@@ -92,7 +103,7 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
     for (int mt = 0; mt < WM; ++mt) {
       const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = mfma16(a, bf[tt], acc[mt][tt]);
+      for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = mfma16(a, bf[tt >> 1][tt & 1], acc[mt][tt]);
     }
   }
 }
@@ -113,7 +124,6 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
 
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
-  const int NT = N >> 4;
   const int G = K / kGroup;
 
   // XCD-major enumeration: consecutive blockIdx go to different XCDs (round-robin), so
@@ -130,7 +140,7 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   const int g_end = (G * (sidx + 1)) / split;
   const int row0 = mbk * BM;
   const int col_w = nbk * kTileBN + 64 * wave;  // first column of this wave
-  const int nt0 = col_w >> 4;
+  const int blk0 = col_w / kBlockCols;
   const bool active = col_w < N;  // wave-uniform: the last n-block may be partly past N
 
   f32x4_t acc[WM][4];
@@ -139,10 +149,11 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  const NibbleConsts nib = nibble_consts();
   BGroup cur, nxt;
   if (g_begin < g_end) {
     issue_a_stage<WM>(x, stage0, row0, M, K, g_begin, wave, lane);
-    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, NT, N, nt0, lane);
+    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, N, blk0, lane);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -151,17 +162,17 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   for (int g = g_begin; g < g_end; g += 2) {
     if (g + 1 < g_end) {
       issue_a_stage<WM>(x, stage1, row0, M, K, g + 1, wave, lane);
-      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, NT, N, nt0, lane);
+      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, N, blk0, lane);
     }
-    if (active) mma_group<WM>(acc, stage0, cur, lane);
+    if (active) mma_group<WM>(acc, stage0, cur, nib, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (g + 1 >= g_end) break;
     if (g + 2 < g_end) {
       issue_a_stage<WM>(x, stage0, row0, M, K, g + 2, wave, lane);
-      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, NT, N, nt0, lane);
+      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, N, blk0, lane);
     }
-    if (active) mma_group<WM>(acc, stage1, nxt, lane);
+    if (active) mma_group<WM>(acc, stage1, nxt, nib, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -176,19 +187,14 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
         for (int i = 0; i < 4; ++i) {
           const int row = row0 + 16 * mt + 4 * (lane >> 4) + i;
           const int n = col_w + 16 * tt + (lane & 15);
-          if (row < M) partials[(static_cast<size_t>(sidx) * M + row) * N + n] = acc[mt][tt][i];
+          if (row < M) store_partial(partials + (static_cast<size_t>(sidx) * M + row) * N + n, acc[mt][tt][i]);
         }
     }
-    __threadfence();
     __syncthreads();
     const int tile = mbk * n_blocks + nbk;
-    if (threadIdx.x == 0) {
-      const int arrived = __hip_atomic_fetch_add(&counters[tile], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      is_last = (arrived == split - 1);
-    }
+    if (threadIdx.x == 0) is_last = (arrive(&counters[tile]) == split - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     if (active) {
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
@@ -201,12 +207,12 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
           if (row < M) {
             float v = 0.0f;
             for (int s = 0; s < split; ++s)
-              v += (s == sidx) ? acc[mt][tt][i] : partials[(static_cast<size_t>(s) * M + row) * N + n];
+              v += (s == sidx) ? acc[mt][tt][i] : load_partial(partials + (static_cast<size_t>(s) * M + row) * N + n);
             acc[mt][tt][i] = v;
           }
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(&counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) rearm(&counters[tile]);
   }
 
   if (!active) return;

@@ -113,14 +113,16 @@ def test_forced_config_validation(pkg):
     f = L.dll.w4a16_gemm_config
     buf = (ctypes.c_uint8 * 64)()
     p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
-    assert f(p, p, p, p, p, 128, 4096, 4096, 128, 1, 4, 4, 1, None, 0, None) == 2  # decode needs M <= 64
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 3, 4, 1, None, 0, None) == 1  # bad tiles
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 5, 1, None, 0, None) == 1  # bad waves
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 33, None, 0, None) == 1  # split > K/128
-    assert f(p, p, p, p, p, 64, 4096, 4096, 128, 1, 4, 16, 1, None, 0, None) == 1  # 256 KiB of LDS
+    assert f(p, p, p, p, p, 128, 4096, 4096, 128, 1, 4, 4, 2, 1, None, 0, None) == 2  # decode needs M <= 64
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 3, 4, 2, 1, None, 0, None) == 1  # bad tiles
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 5, 2, 1, None, 0, None) == 1  # bad waves
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 33, None, 0, None) == 1  # split > K/128
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 3, 1, None, 0, None) == 1  # bad depth
+    assert "depth" in L.last_error()
+    assert f(p, p, p, p, p, 64, 4096, 4096, 128, 1, 4, 16, 2, 1, None, 0, None) == 1  # 256 KiB of LDS
     assert "LDS" in L.last_error()
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 0, 1, None, 0, None) == 1  # bad wm
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 1, None, 0, None) == 1  # bad regime
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 0, 2, 1, None, 0, None) == 1  # bad wm
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 2, 1, None, 0, None) == 1  # bad regime
     # split > 1 without workspace
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 4, None, 0, None) == 4
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 4, None, 0, None) == 4
     assert "workspace" in L.last_error()

@@ -60,36 +60,41 @@ def test_dequant_bit_exact_full_qwen3_shapes(gpu_lib, shape):
     np.testing.assert_array_equal(bits_of(w), want)
 
 
-def k8_layout_numpy(qweight: np.ndarray) -> np.ndarray:
-    """The repacked layout restated from its definition (values along K, 1 KiB blocks)."""
-    q = ora.unpack_awq_int4(qweight)  # [K, N]
-    k, n = q.shape
-    out = np.zeros(k * n // 8, dtype=np.uint32)
-    shifts = [((i & 1) << 4) | ((i >> 1) << 2) for i in range(8)]
+def group_block_layout_numpy(qweight: np.ndarray) -> np.ndarray:
+    """The repacked word order restated from its definition: per (128-row group g,
+    32-column block b), lane l and slot 2 js + h hold qweight[k][4 b + l // 16] with
+    k = 128 g + 32 js + 8 ((l % 16) // 4) + 4 h + l % 4."""
+    k, c8 = qweight.shape
+    n = c8 * 8
+    out = np.zeros(k * c8, dtype=np.int32)
     for g in range(k // 128):
-        for t in range(n // 16):
+        for b in range(n // 32):
             for lane in range(64):
-                col = 16 * t + lane % 16
-                for j in range(4):
-                    k0 = 128 * g + 32 * j + 8 * (lane // 16)
-                    word = 0
-                    for i in range(8):
-                        word |= int(q[k0 + i, col]) << shifts[i]
-                    out[((g * (n // 16) + t) * 64 + lane) * 4 + j] = word
-    return out.view(np.int32)
+                for js in range(4):
+                    for h in range(2):
+                        row = 128 * g + 32 * js + 8 * ((lane % 16) // 4) + 4 * h + lane % 4
+                        out[((g * (n // 32) + b) * 64 + lane) * 8 + 2 * js + h] = qweight[row, 4 * b + lane // 16]
+    return out
 
 
 def test_repack_matches_layout_definition(gpu_lib):
     awq = awq_mod()
     rng = np.random.default_rng(8)
-    qw = rng.integers(-2 ** 31, 2 ** 31, size=(256, 4), dtype=np.int64).astype(np.int32)  # K=256, N=32
+    qw = rng.integers(-2 ** 31, 2 ** 31, size=(256, 8), dtype=np.int64).astype(np.int32)  # K=256, N=64
     got = awq.repack_awq_qweight(torch.from_numpy(qw).cuda()).cpu().numpy()
-    np.testing.assert_array_equal(got, k8_layout_numpy(qw))
+    np.testing.assert_array_equal(got, group_block_layout_numpy(qw))
+
+
+def test_repack_is_a_permutation_of_the_words(gpu_lib):
+    awq = awq_mod()
+    qw = torch.arange(512 * 96, dtype=torch.int32, device="cuda").view(512, 96)  # K=512, N=768
+    got = awq.repack_awq_qweight(qw)
+    assert torch.equal(torch.sort(got).values, qw.flatten())
 
 
 @pytest.mark.parametrize("case", sorted(golden_cases()))
 def test_tile_dequant_matches_reference_on_golden(gpu_lib, case):
-    """The MFMA tile GEMM's dequant routine, read back through w4a16_dequant_packed: the
+    """The GEMM kernels' matrix-core dequant, read back through w4a16_dequant_packed: the
     reference's weights bit for bit (zero signs aside for non-positive scales)."""
     awq = awq_mod()
     L = gpu_lib

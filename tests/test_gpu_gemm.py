@@ -62,26 +62,27 @@ def test_single_token_wide_gemv_reference_recipe(gpu_lib):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.01, atol=0.02)
 
 
-DECODE_CONFIGS = [(tn, w, s) for tn in (1, 2, 4) for w in (4, 8, 16) for s in (1, 3, 8)]
+DECODE_CONFIGS = [(tn, w, d, s) for tn in (2, 4) for w in (4, 8, 16) for d in (1, 2, 4) for s in (1, 3, 8)]
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 33, 64])
 def test_every_decode_configuration(gpu_lib, m):
-    """All column-tile / wave / split combinations of the decode kernel, incl. uneven splits."""
-    k, n = 1024, 512
+    """All column-tile / wave / depth / split combinations of the decode kernel, incl. uneven
+    splits, waves with no group and prefetch rings that wrap (K = 2048: 16 groups)."""
+    k, n = 2048, 512
     p = ora.make_problem(seed=100 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
-    for tn, waves, split in DECODE_CONFIGS:
+    for tn, waves, depth, split in DECODE_CONFIGS:
         if waves * ((m + 15) // 16) * tn * 1024 > 64 * 1024:
             continue  # rejected by the library (LDS limit), see test_capi
         ws_bytes = gpu_lib.workspace_bytes_config(m, n, 1, tn, split)
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 1, tn, waves, split, ws)
+        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 1, tn, waves, split, ws, p2=depth)
         err = rel_err(y, want)
-        assert err <= GEMM_REL_TOL, (tn, waves, split, err)
+        assert err <= GEMM_REL_TOL, (tn, waves, depth, split, err)
         if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
