@@ -18,6 +18,16 @@ Method
     average kernel duration with host launch overhead removed.
   * Algorithmic bytes per GEMM = K N / 2 + K N / 256 + K N / 64 + 2 M K + 2 M N
     (int4 weights, int32 zeros, bf16 scales, bf16 x and y); flops = 2 M N K.
+  * `roofline` describes the dominant launch (the decode point with the longest
+    kernel time, gate_up at M = 16): its algorithmic bytes over its event-timed
+    duration, against the 8 TB/s HBM peak.  `traffic` is that launch's HBM bytes as
+    measured by rocprofv3 counters (FETCH_SIZE + WRITE_SIZE, each scaled by the factor
+    that makes a plain 256 MiB copy read and write 256 MiB), taken from the committed
+    summary profiles/decode_gate_up_m16_traffic.txt when present.
+
+Profiling mode: `--profile-point SHAPE:M` runs one point without graphs (a 256 MiB copy
+for counter calibration, then --steps launches over rotating weights) so that
+rocprofv3 --kernel-trace / --pmc see exactly that launch.
 """
 from __future__ import annotations
 
@@ -44,6 +54,9 @@ PREFILL_M = 2048
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 CACHE_BYTES = 256 * 2 ** 20
+DOMINANT = ("gate_up", 16)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_gate_up_m16_traffic.txt")
+CALIBRATION_BYTES = 256 * 2 ** 20
 
 
 def algorithmic_bytes(m: int, k: int, n: int) -> int:
@@ -183,6 +196,57 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
                       f"os.cpu_count()={os.cpu_count()}"}
 
 
+def read_traffic(path: str = TRAFFIC_FILE):
+    """HBM bytes per launch recorded in the committed counter summary, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
+
+
+def profile_point(lib, spec: str, steps: int, dev) -> int:
+    """Counter/trace workload: one 256 MiB bf16 copy (3x) for calibration, then `steps`
+    direct launches of one decode or prefill point over rotating weights."""
+    name, m = spec.split(":")
+    m = int(m)
+    k, n = SHAPES[name]
+    src = torch.ones(CALIBRATION_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    copies = max(2, -(-2 * CACHE_BYTES // weight_bytes(k, n)))
+    weights = make_weights(k, n, copies, dev, 7919 * list(SHAPES).index(name))
+    x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+    p = Point(lib, name, m, k, n, weights, x)
+    stream = torch.cuda.current_stream(dev)
+    p.launch_all(stream.cuda_stream)  # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    done = 0
+    while done < steps:
+        for packed, qzeros, scales in weights[: steps - done]:
+            rc = lib.dll.w4a16_gemm(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                    p.y.data_ptr(), m, k, n, 128, p.ws.data_ptr() if p.ws_len else None,
+                                    p.ws_len, stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(lib.last_error())
+            done += 1
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"profile_point": spec, "launches": steps, "us_per_launch_incl_gaps": round(ms * 1e3, 3),
+                      "algorithmic_bytes": algorithmic_bytes(m, k, n), "regime": p.regime, "split": p.split,
+                      "calibration_copy_bytes": CALIBRATION_BYTES}))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +255,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--details", action="store_true", help="print one line per point to stderr")
+    ap.add_argument("--profile-point", metavar="SHAPE:M", help="profiling workload for one point (see doc)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no multi-GPU "
@@ -203,6 +268,8 @@ def main(argv=None):
     lib = pkg.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.profile_point:
+        return profile_point(lib, args.profile_point, args.steps, dev)
     stream = torch.cuda.Stream(dev)
 
     decode_points = build_points(lib, DECODE_M + EXTRA_DECODE_M, dev)
@@ -211,6 +278,9 @@ def main(argv=None):
     bytes_head = sum(algorithmic_bytes(p.m, p.k, p.n) for p in head)
     ms_head = sum(per_launch[id(p)] for p in head)
     value = bytes_head / (ms_head * 1e-3) / 1e9
+    dom = next(p for p in head if (p.name, p.m) == DOMINANT)
+    dom_ms = per_launch[id(dom)]
+    dom_gbs = algorithmic_bytes(dom.m, dom.k, dom.n) / (dom_ms * 1e-3) / 1e9
     points_out = []
     for p in decode_points:
         ms = per_launch[id(p)]
@@ -244,8 +314,6 @@ def main(argv=None):
         del pts
 
     cpu = None if args.no_cpu else cpu_baseline()
-    avg_bytes = bytes_head / len(head)
-    avg_ms = ms_head / len(head)
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -262,9 +330,11 @@ def main(argv=None):
         "config": {"workload": "decode sweep: AWQ W4A16 GEMM, group 128, M in {1,4,8,16} x Qwen3-8B "
                                "QKV 4096x6144, O 4096x4096, gate_up 4096x24576, down 12288x4096",
                    "group_size": 128, "weights_rotated_bytes_per_point": ">= 512 MiB"},
-        "roofline": {"bound": "hbm", "achieved": round(avg_bytes / (avg_ms * 1e-3) / 1e9, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(avg_bytes / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": {"kernel": f"decode {DOMINANT[0]} {dom.k}x{dom.n} M={DOMINANT[1]}", "bound": "hbm",
+                     "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "algorithmic_bytes": algorithmic_bytes(dom.m, dom.k, dom.n),
+                     "launch_us": round(dom_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "prefill_m2048": prefill,
         "points": points_out,

@@ -53,37 +53,33 @@ struct GemmPlan {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Decode regime: pick the workgroup width and K split so that the grid covers the 256
-// CUs about twice over while keeping the fp32 partial traffic (split * M * N * 8 bytes)
-// small against the weight stream (K * N / 2 bytes).
+// Decode regime.  One 32-column block per workgroup (tn = 2) keeps the per-wave register
+// ring small; wide layers at M > 48 use two blocks (tn = 4) with 4 waves so that the
+// activation fragments are shared by twice the weights.  Two groups in flight per wave
+// up to M = 32 (depth 1 above that, where the activation fragments dominate the ring).
+// K is split in two only where the column blocks alone leave the CUs short of work
+// (long K, or M > 32 on narrow layers); every extra split costs a round of fp32 partials.
+// Chosen from measured sweeps over the Qwen3-8B projection shapes.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  GemmPlan p{W4A16_REGIME_DECODE, 4, 4, 2, 1};
-  const int target = 512;
-  int tn = 4;
-  if (N / 64 < 256) tn = 2;
+  const int MB = (M + 15) / 16;
+  const int tn = (MB >= 4 && N >= 16384) ? 4 : 2;
+  const int waves = tn == 4 ? 4 : 8;   // decode_lds_bytes(64, tn, waves) <= 64 KiB
+  const int depth = MB <= 2 ? 2 : 1;
   const int blocks = N / (16 * tn);
-  int split = ceil_div(target, blocks);
-  const int waves = 4;  // decode_lds_bytes(64, 4, 4) = 64 KiB: always within kDecodeMaxLds
-  split = split > G / waves ? G / waves : split;
-  if (split < 1) split = 1;
-  p.p0 = tn;
-  p.p1 = waves;
-  p.split = split;
-  (void)M;
-  return p;
+  int split = (G >= 64 || (MB >= 3 && blocks <= 128)) ? 2 : 1;
+  if (split > G) split = G;
+  return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
+// Tile regime: 128-row tiles (wm = 8) everywhere; split K in two when the tiles alone
+// cannot cover the CUs and K is long enough that each split keeps >= 32 groups.
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  GemmPlan p{W4A16_REGIME_TILE, 16, 0, 0, 1};
-  const int wm = M <= 128 ? 8 : 16;
+  const int wm = 8;
   const int tiles = ceil_div(M, 16 * wm) * ceil_div(N, 256);
-  int split = 1;
-  while (tiles * split < 200 && split * 2 <= G / 4) split *= 2;
-  p.p0 = wm;
-  p.split = split;
-  return p;
+  const int split = (tiles < 128 && G >= 64) ? 2 : 1;
+  return GemmPlan{W4A16_REGIME_TILE, wm, 0, 0, split};
 }
 
 GemmPlan plan(int M, int K, int N) {

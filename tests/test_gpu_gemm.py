@@ -194,7 +194,7 @@ def test_leading_dims_are_flattened(gpu_lib):
 
 
 def test_too_small_workspace_is_an_error(gpu_lib):
-    k, n, m = 4096, 4096, 16
+    k, n, m = 12288, 4096, 16  # the down projection: split-K, so a workspace is needed
     qw, qz, s = random_awq_gpu(k, n, seed=5)
     need = gpu_lib.workspace_bytes(m, k, n)
     assert need > 0
@@ -271,7 +271,7 @@ def test_row_parallel_layer_forward(gpu_lib):
 def test_hip_graph_capture_replays_match_eager(gpu_lib):
     """A captured decode GEMM with a split-K reduction (counters live in the workspace)
     replayed several times, with eager work in between, matches the eager result."""
-    k, n, m = 4096, 4096, 16
+    k, n, m = 12288, 4096, 16  # the down projection
     qw, qz, s = random_awq_gpu(k, n, seed=21)
     awq = awq_mod()
     packed = awq.repack_awq_qweight(qw)
