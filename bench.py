@@ -25,6 +25,15 @@ Method
     that makes a plain 256 MiB copy read and write 256 MiB), taken from the committed
     summary profiles/decode_gate_up_m16_traffic.txt when present.
 
+Also reported (not part of `value`):
+  * mixed_m512: the ragged continuous batch (48 decode rows + 8 x 4 verify rows + a
+    432-row prefill chunk = M 512) at gate_up and down, TFLOP/s and GB/s;
+  * stack36: a 36-layer Qwen3-8B-shaped stack (independent weights, 3.6 GB) stepped at
+    M in {1, 8, 64, 128}: 144 GEMMs per step captured in one graph; aggregate weight
+    GB/s and linear-layer time per decoded token;
+  * measured_ceilings: a 1 GiB device copy (read + write GB/s) and torch.matmul
+    (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks.
+
 Profiling mode: `--profile-point SHAPE:M` runs one point without graphs (a 256 MiB copy
 for counter calibration, then --steps launches over rotating weights) so that
 rocprofv3 --kernel-trace / --pmc see exactly that launch.
@@ -196,6 +205,100 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
                       f"os.cpu_count()={os.cpu_count()}"}
 
 
+MIXED_M = 48 * 1 + 8 * 4 + 432
+STACK_LAYERS = 36
+STACK_M = (1, 8, 64, 128)
+
+
+def time_graph(fn, stream, reps: int) -> float:
+    """Capture fn() in a HIP graph on `stream`, replay it `reps` times between HIP events
+    on that stream; returns ms per replay."""
+    with torch.cuda.stream(stream):
+        fn()
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    with torch.cuda.stream(stream):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def mixed_batch(lib, dev, stream, reps: int) -> dict:
+    """48 decode rows + 8 verify sequences x 4 rows + one 432-row prefill chunk, packed into
+    one [512, K] GEMM, at the gate_up and down shapes."""
+    out = {}
+    for si, name in enumerate(("gate_up", "down")):
+        k, n = SHAPES[name]
+        copies = max(2, -(-2 * CACHE_BYTES // weight_bytes(k, n)))
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(300 + si)
+        x = torch.randn((MIXED_M, k), device=dev, generator=gen).to(torch.bfloat16)
+        p = Point(lib, name, MIXED_M, k, n, make_weights(k, n, copies, dev, 400 + si), x)
+        ms = time_graph(lambda: p.launch_all(torch.cuda.current_stream(dev).cuda_stream), stream, reps) / p.launches
+        out[name] = {"M": MIXED_M, "us": round(ms * 1e3, 2),
+                     "TFLOP/s": round(2 * MIXED_M * n * k / (ms * 1e-3) / 1e12, 1),
+                     "GB/s": round(algorithmic_bytes(MIXED_M, k, n) / (ms * 1e-3) / 1e9, 1),
+                     "regime": "decode" if p.regime == 1 else "tile", "split": p.split}
+        del p
+    return out
+
+
+def layer_stack(lib, dev, stream, reps: int) -> dict:
+    """36 layers x (QKV, O, gate_up, down) with independent weights; one step = the 144
+    GEMMs back to back on one stream at packed M."""
+    layers = [{name: make_weights(k, n, 1, dev, 1000 + 4 * li + si)[0]
+               for si, (name, (k, n)) in enumerate(SHAPES.items())} for li in range(STACK_LAYERS)]
+    out = {}
+    for m in STACK_M:
+        xs = {name: torch.randn((m, k), device=dev).to(torch.bfloat16) for name, (k, n) in SHAPES.items()}
+        ys = {name: torch.empty((m, n), dtype=torch.bfloat16, device=dev) for name, (k, n) in SHAPES.items()}
+        ws_len = max(lib.workspace_bytes(m, k, n) for k, n in SHAPES.values())
+        ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
+
+        def step():
+            sp = torch.cuda.current_stream(dev).cuda_stream
+            for layer in layers:
+                for name, (k, n) in SHAPES.items():
+                    packed, qzeros, scales = layer[name]
+                    rc = lib.dll.w4a16_gemm(xs[name].data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                            scales.data_ptr(), ys[name].data_ptr(), m, k, n, 128,
+                                            ws.data_ptr() if ws_len else None, ws_len, sp)
+                    if rc != 0:
+                        raise RuntimeError(lib.last_error())
+
+        ms = time_graph(step, stream, reps)
+        total = sum(algorithmic_bytes(m, k, n) for k, n in SHAPES.values()) * STACK_LAYERS
+        out[f"M={m}"] = {"step_us": round(ms * 1e3, 1), "weight_GB/s": round(total / (ms * 1e-3) / 1e9, 1),
+                         "us_per_token": round(ms * 1e3 / m, 2),
+                         "regimes": sorted({"decode" if lib.regime(m, k, n) == 1 else "tile"
+                                            for k, n in SHAPES.values()})}
+    del layers
+    return out
+
+
+def measured_ceilings(dev, stream) -> dict:
+    """A 1 GiB device-to-device copy and a hipBLASLt bf16 GEMM at the prefill gate_up shape."""
+    src = torch.empty(2 ** 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    ms = time_graph(lambda: dst.copy_(src), stream, 10)
+    copy_gbs = 2 * src.numel() * 2 / (ms * 1e-3) / 1e9
+    del src, dst
+    k, n = SHAPES["gate_up"]
+    a = torch.randn((PREFILL_M, k), device=dev).to(torch.bfloat16)
+    b = torch.randn((k, n), device=dev).to(torch.bfloat16)
+    c = torch.empty((PREFILL_M, n), dtype=torch.bfloat16, device=dev)
+    ms = time_graph(lambda: torch.matmul(a, b, out=c), stream, 10)
+    return {"copy_1GiB_read+write_GB/s": round(copy_gbs, 1),
+            "hipblaslt_bf16_gate_up_m2048_TFLOP/s": round(2 * PREFILL_M * n * k / (ms * 1e-3) / 1e12, 1)}
+
+
 def read_traffic(path: str = TRAFFIC_FILE):
     """HBM bytes per launch recorded in the committed counter summary, or None."""
     try:
@@ -254,6 +357,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the mixed-batch, layer-stack and ceiling legs")
     ap.add_argument("--details", action="store_true", help="print one line per point to stderr")
     ap.add_argument("--profile-point", metavar="SHAPE:M", help="profiling workload for one point (see doc)")
     args = ap.parse_args(argv)
@@ -313,6 +417,16 @@ def main(argv=None):
                 print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
         del pts
 
+    mixed = stack = ceilings = None
+    if not args.no_extra:
+        mixed = mixed_batch(lib, dev, stream, max(3, args.steps // 4))
+        stack = layer_stack(lib, dev, stream, max(2, args.steps // 10))
+        ceilings = measured_ceilings(dev, stream)
+        if args.details:
+            print(f"mixed M={MIXED_M}: {json.dumps(mixed)}", file=sys.stderr)
+            print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
+            print(f"ceilings: {json.dumps(ceilings)}", file=sys.stderr)
+
     cpu = None if args.no_cpu else cpu_baseline()
     result = {
         "metric": METRIC,
@@ -337,6 +451,9 @@ def main(argv=None):
                      "launch_us": round(dom_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "prefill_m2048": prefill,
+        "mixed_m512": mixed,
+        "stack36": stack,
+        "measured_ceilings": ceilings,
         "points": points_out,
     }
     print(json.dumps(result))

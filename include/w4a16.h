@@ -66,11 +66,11 @@ int w4a16_unpack_int4(const int32_t* packed, int32_t* out, int rows, int cols, v
 int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
                   uint16_t* w_out, int K, int N, int group_size, void* stream);
 
-/* Reorder qweight [K, N/8] into the group-block layout consumed by w4a16_gemm (same
- * words, same byte size K*N/2; each word keeps its 8 columns in AutoAWQ nibble order).
- * One 2 KiB block per (128-row group g, 32-column block b); word
- * [((g*(N/32) + b)*64 + lane)*8 + 2*js + h] is qweight[k][4b + lane/16] with
- * k = 128g + 32js + 8*((lane%16)/4) + 4h + lane%4.  K % 128 == 0, N % 32 == 0.
+/* Rearrange qweight [K, N/8] into the group-tile layout consumed by w4a16_gemm (same
+ * 4-bit values, same byte size K*N/2).  One 1 KiB tile per (128-row group g, 16-column
+ * tile t); word [((g*(N/16) + t)*64 + lane)*4 + js] holds, at bit 8h + 4(k/2) + 16(k%2),
+ * the value of row 128g + 32js + 8(lane/16) + 4h + lane%4 and column
+ * 16t + 4((lane/4)%4) + k, for h = 0..1 and k = 0..3.  K % 128 == 0, N % 16 == 0.
  * Replaces repack_qweight (awq_w4a16.cu:81-109, 256-272) / repack_awq_qweight_cuda
  * (awq_cuda.py:129-132).  qzeros need no reorder: the kernels read them as stored, so
  * reorder_qzeros (awq_w4a16.cu:111-118, 274-286) has no counterpart. */
@@ -78,7 +78,7 @@ int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, 
 
 /* Dequantize from the repacked layout through the GEMM kernels' matrix-core dequant
  * (same bits as w4a16_dequant for every finite scale with |s| < 2^123, zero signs aside);
- * exists to verify that path bit-exactly.  K % 128 == 0, N % 32 == 0.  No reference
+ * exists to verify that path bit-exactly.  K % 128 == 0, N % 16 == 0.  No reference
  * counterpart beyond dequantize_awq_gemm (awq.py:235-248). */
 int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
                          uint16_t* w_out, int K, int N, int group_size, void* stream);
@@ -109,7 +109,7 @@ int w4a16_regime(int M, int K, int N);
 int w4a16_split_k(int M, int K, int N);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
- * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {2,4}, p1 = waves per
+ * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,4}, p1 = waves per
  * workgroup in {4,8,16}, p2 = 128-row groups in flight per wave in {1,2,4}, M <= 64) or
  * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {8,16}; p1, p2 ignored);
  * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises

@@ -53,21 +53,35 @@ struct GemmPlan {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Decode regime.  One 32-column block per workgroup (tn = 2) keeps the per-wave register
-// ring small; wide layers at M > 48 use two blocks (tn = 4) with 4 waves so that the
-// activation fragments are shared by twice the weights.  Two groups in flight per wave
-// up to M = 32 (depth 1 above that, where the activation fragments dominate the ring).
-// K is split in two only where the column blocks alone leave the CUs short of work
-// (long K, or M > 32 on narrow layers); every extra split costs a round of fp32 partials.
-// Chosen from measured sweeps over the Qwen3-8B projection shapes.
+// Decode regime, chosen from measured sweeps over the Qwen3-8B projection shapes.
+//  * Narrow layers (N <= 4096) at M <= 16 use one 16-column tile per workgroup, so that
+//    every CU gets work; long K (>= 8192) at M > 4 instead splits K in two with 32-column
+//    workgroups, which keeps the activation traffic per weight down.
+//  * Wider layers use 32-column workgroups (tn = 2), and at M > 48 on N >= 16384 64-column
+//    workgroups (tn = 4) that share each activation fragment among four tiles.
+//  * 8 waves with one group in flight per wave, or 4 waves with two; K is split only where
+//    the column tiles alone cannot cover the CUs (every split costs a round of fp32
+//    partials).
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
-  const int tn = (MB >= 4 && N >= 16384) ? 4 : 2;
-  const int waves = tn == 4 ? 4 : 8;   // decode_lds_bytes(64, tn, waves) <= 64 KiB
-  const int depth = MB <= 2 ? 2 : 1;
-  const int blocks = N / (16 * tn);
-  int split = (G >= 64 || (MB >= 3 && blocks <= 128)) ? 2 : 1;
+  int tn = 2, waves = 8, depth = 1, split = 1;
+  if (MB == 1) {
+    if (N <= 4096 && !(K >= 8192 && M > 4)) {
+      tn = 1;
+      waves = M <= 4 ? 8 : 4;
+      depth = 2;
+    } else if (N <= 4096) {
+      split = 2;
+    }
+  } else if (MB == 2) {
+    split = N <= 4096 ? 2 : 1;
+  } else {
+    tn = N >= 16384 ? 4 : 2;
+    waves = (tn == 4 || N > 4096) ? 4 : 8;  // decode_lds_bytes(64, tn, waves) <= 64 KiB
+    depth = 2;
+    split = N <= 4096 ? 2 : 1;
+  }
   if (split > G) split = G;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
@@ -181,7 +195,7 @@ int w4a16_dequant(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
 int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, void* stream) {
   if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
-  if (N % 32) return fail(W4A16_ERR_SHAPE, "N must be divisible by 32 (got %d)", N);
+  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
   if (!qweight || !packed) return fail(W4A16_ERR_ARG, "null tensor pointer");
   if (!aligned(qweight, 4) || !aligned(packed, 16)) return fail(W4A16_ERR_ALIGN, "packed must be 16-byte aligned");
   return check_launch(w4a16::launch_repack(reinterpret_cast<const uint32_t*>(qweight),
@@ -195,7 +209,7 @@ int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uin
   if (K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "K and N must be positive");
   if (group_size != w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
-  if (N % 32) return fail(W4A16_ERR_SHAPE, "N must be divisible by 32 (got %d)", N);
+  if (N % 16) return fail(W4A16_ERR_SHAPE, "N must be divisible by 16 (got %d)", N);
   if (!packed || !qzeros || !scales || !w_out) return fail(W4A16_ERR_ARG, "null tensor pointer");
   if (!aligned(packed, 16) || !aligned(w_out, 2) || !aligned(scales, 4) || !aligned(qzeros, 4))
     return fail(W4A16_ERR_ALIGN, "packed must be 16-byte and scales, qzeros 4-byte aligned");
@@ -239,7 +253,7 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
   if (split < 1 || split > G) return fail(W4A16_ERR_ARG, "split must be in [1, K/128] (got %d)", split);
   if (regime == W4A16_REGIME_DECODE) {
     if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
-    if (p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 2 or 4");
+    if (p0 != 1 && p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2 or 4");
     if (p1 != 4 && p1 != 8 && p1 != 16) return fail(W4A16_ERR_ARG, "decode waves must be 4, 8 or 16");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
     if (decode_lds_bytes(M, p0, p1) > kDecodeMaxLds)

@@ -1,24 +1,28 @@
 // Device helpers shared by the W4A16 kernels (gfx950 / CDNA4, wave64).
 //
-// Weight layout ("group blocks").  The kernels read the AutoAWQ words unchanged -- each
-// holds 8 consecutive columns of one row, column c at bit 4 * (0,4,1,5,2,6,3,7)[c] --
-// but in an order that lets a wavefront fetch one (128-row group g, 32-column block b)
-// block of 2 KiB as two 16-byte loads per lane:
-//   word index  ((g * (N / 32) + b) * 64 + lane) * 8 + 2 js + h,  js = 0..3, h = 0..1
-//   row         k = 128 g + 32 js + 8 ((lane % 16) / 4) + 4 h + lane % 4
-//   column word 4 b + lane / 16          (columns 32 b + 8 (lane / 16) .. +7)
+// Weight layout ("group tiles").  One 1 KiB tile per (128-row group g, 16-column tile
+// t): 64 lanes x 4 words, one 32-bit word per lane per 32-row step js, so a wavefront
+// fetches a tile with one 16-byte load per lane:
+//   word index   ((g * (N / 16) + t) * 64 + lane) * 4 + js
+//   word bits    nibble of (row, column) at bit 8 h + 4 (k / 2) + 16 (k % 2), h = 0..1,
+//                k = 0..3, with
+//   row          128 g + 32 js + 8 (lane / 16) + 4 h + lane % 4
+//   column       16 t + 4 ((lane / 4) % 4) + k
+// The nibbles are AutoAWQ's unchanged 4-bit values; only their placement differs.
 //
-// Dequant on the matrix cores.  For a 32-row step js, lane l's word h unpacks -- one
-// v_and_or_b32 per two values -- into the exact bf16 values (128 + q) of its 8 columns,
-// which is the A operand of v_mfma_f32_16x16x32_bf16 (16 rows x 32 columns).  With B the
-// 32 x 16 diagonal carrying s for the 16 columns of output tile u and the accumulator
-// input C = -(128 + z) s, the MFMA returns (128 + q) s - (128 + z) s = (q - z) s, exact in
-// fp32 (every product has <= 16 significant bits and the result is representable), and
-// v_cvt_pk_bf16_f32 rounds it like the reference.  Output row i of the MFMA fed by half h
-// is weight row 8 (i / 4) + 4 h + i % 4, so a lane's results for h = 0 and 1 are the 8
-// consecutive rows k = 8 (lane / 16) .. +7 of its column lane % 16: exactly the B fragment
-// of the main v_mfma_f32_16x16x32_bf16, whose A fragment is then the plain 16-byte
-// activation load x[row][8 (lane / 16) .. +7].
+// Dequant on the matrix cores.  For step js, lane l's word unpacks -- one v_and_or_b32 per
+// two values -- into the exact bf16 values (128 + q): words r_s = ((w >> 4 s) & 0x000F000F)
+// | 0x43004300, s = 0..3, so {r_0, r_1} holds k = 0..3 of half h = 0 and {r_2, r_3} those of
+// h = 1.  That is the A operand of v_mfma_f32_4x4x4bf16_1k, whose 16 blocks b = l / 4 each
+// multiply a 4 x 4 A (lane 4 b + i holds row i) by a 4 x 4 B (lane 4 b + j holds column j).
+// With B the diagonal of the block's 4 column scales and the accumulator input
+// C = -(128 + z) s, block b returns (128 + q) s - (128 + z) s = (q - z) s, exact in fp32
+// (every product has <= 16 significant bits and the result is representable), and
+// v_cvt_pk_bf16_f32 rounds it like the reference.  Output register i of lane l (column
+// j = l % 4 of block b) is weight row 8 (l / 16) + 4 h + i of column 4 (b % 4) + j = l % 16,
+// so the two half-steps give the 8 consecutive rows 8 (l / 16) .. +7 of column l % 16:
+// exactly the B fragment of the main v_mfma_f32_16x16x32_bf16, whose A fragment is then the
+// plain 16-byte activation load x[row][8 (lane / 16) .. +7].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,17 +31,18 @@
 namespace w4a16 {
 
 constexpr int kGroup = 128;      // quantization group (rows of K per scale / zero)
-constexpr int kBlockCols = 32;   // columns of one layout block
-constexpr int kBlockWords = 512; // words of one (group, 32-column) block = 2 KiB
+constexpr int kTileCols = 16;    // columns of one layout tile
+constexpr int kTileWords = 256;  // words of one (group, 16-column) tile = 1 KiB
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 // Bit offset of logical column c (0..7) inside an AutoAWQ word: 4 * (0,4,1,5,2,6,3,7)[c].
-// The same offsets place value i of a K8 word.
 __device__ __forceinline__ int awq_shift(int c) { return ((c & 1) << 4) | ((c >> 1) << 2); }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
@@ -75,16 +80,17 @@ __device__ __forceinline__ NibbleConsts nibble_consts() {
   return NibbleConsts{mask, bias};
 }
 
-// AutoAWQ word -> bf16 fragment holding (128 + q_i), i = 0..7, exactly: bf16 0x4300 is
-// 128.0 with a unit last place, so OR-ing a nibble into the low mantissa bits adds it.
-// Element 2 j + h holds the nibble at bit 4 j + 16 h.  7 VALU ops per 8 values.
-__device__ __forceinline__ bf16x8_t unpack_biased(uint32_t w, const NibbleConsts& k) {
-  u32x4_t r;
-  r[0] = (w & k.mask) | k.bias;
-  r[1] = ((w >> 4) & k.mask) | k.bias;
-  r[2] = ((w >> 8) & k.mask) | k.bias;
-  r[3] = ((w >> 12) & k.mask) | k.bias;
-  return __builtin_bit_cast(bf16x8_t, r);
+// Tile word -> the two A operands (half-steps h = 0, 1) of the 4x4x4 dequant MFMAs, each
+// four exact bf16 values (128 + q): bf16 0x4300 is 128.0 with a unit last place, so OR-ing
+// a nibble into the low mantissa bits adds it.  7 VALU ops per 8 values.
+__device__ __forceinline__ void unpack_biased(s16x4_t (&a)[2], uint32_t w, const NibbleConsts& k) {
+  u32x2_t h0, h1;
+  h0[0] = (w & k.mask) | k.bias;
+  h0[1] = ((w >> 4) & k.mask) | k.bias;
+  h1[0] = ((w >> 8) & k.mask) | k.bias;
+  h1[1] = ((w >> 12) & k.mask) | k.bias;
+  a[0] = __builtin_bit_cast(s16x4_t, h0);
+  a[1] = __builtin_bit_cast(s16x4_t, h1);
 }
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
@@ -131,59 +137,53 @@ __device__ __forceinline__ uint32_t load_zero(const uint32_t* __restrict__ qzero
 // ---------------------------------------------------------------------------
 // Matrix-core dequant (see the layout note at the top of this file).
 
-// MFMA operands that scale one 16-column output tile u of a 32-column block: the
-// diagonal B (lane l carries s in element l % 8 iff lane / 16 == 2 u + (l / 8) % 2, i.e.
-// where its inner column 8 (l / 16) + l % 8 equals output column 16 u + l % 16) and the
-// accumulator input -(128 + z) s.  s and z are those of the lane's own output column c;
-// `s_pair` is the aligned 32-bit word of bf16 scales holding columns c & ~1 and c | 1, so
-// the lane's scale sits in half c % 2 == lane % 2 -- where the diagonal wants it.
+// MFMA operands that scale one lane's column c = 16 t + lane % 16 of a tile: the diagonal
+// B element (lane 4 b + j carries s in element j = lane % 4, zeros elsewhere) and the
+// accumulator input -(128 + z) s.  `s_pair` is the aligned 32-bit word of bf16 scales
+// holding columns c & ~1 and c | 1, so the lane's scale sits in half c % 2 == lane % 2 --
+// where element j = lane % 4 of the diagonal wants it.
 struct TileScale {
-  bf16x8_t diag;
+  s16x4_t diag;
   f32x4_t cin;
 };
 
-__device__ __forceinline__ TileScale make_tile_scale(uint32_t s_pair, uint32_t z, int u, int lane) {
+__device__ __forceinline__ TileScale make_tile_scale(uint32_t s_pair, uint32_t z, int lane) {
   TileScale t;
   const bool hi = (lane & 1) != 0;
   const uint32_t mine = s_pair & (hi ? 0xFFFF0000u : 0x0000FFFFu);
-  const bool active = (lane >> 4) == 2 * u + ((lane >> 3) & 1);
-  const uint32_t val = active ? mine : 0u;
-  const int slot = (lane & 7) >> 1;
-  u32x4_t d;
-  d[0] = slot == 0 ? val : 0u;
-  d[1] = slot == 1 ? val : 0u;
-  d[2] = slot == 2 ? val : 0u;
-  d[3] = slot == 3 ? val : 0u;
-  t.diag = __builtin_bit_cast(bf16x8_t, d);
+  const bool upper = (lane & 2) != 0;  // element j in 32-bit register j / 2
+  u32x2_t d;
+  d[0] = upper ? 0u : mine;
+  d[1] = upper ? mine : 0u;
+  t.diag = __builtin_bit_cast(s16x4_t, d);
   const float c = -((128.0f + static_cast<float>(z)) * __uint_as_float(hi ? mine : (mine << 16)));
   t.cin = f32x4_t{c, c, c, c};
   return t;
 }
 
-__device__ __forceinline__ uint32_t pack_pair(float a, float b) { return pack_bf16x2(a, b); }
-
-// Two AutoAWQ words (h = 0, 1) of one 32-row step of a 32-column block -> the B fragments
-// of its two 16-column tiles, bf16_rne((q - z) s).  4 scaling MFMAs, 14 + 8 VALU ops.
-__device__ __forceinline__ void dequant_block(bf16x8_t (&frag)[2], uint32_t w0, uint32_t w1, const TileScale (&ts)[2],
-                                              const NibbleConsts& k) {
-  const bf16x8_t a0 = unpack_biased(w0, k);
-  const bf16x8_t a1 = unpack_biased(w1, k);
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const f32x4_t d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ts[u].diag, ts[u].cin, 0, 0, 0);
-    const f32x4_t d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ts[u].diag, ts[u].cin, 0, 0, 0);
-    u32x4_t r;
-    r[0] = pack_pair(d0[0], d0[1]);
-    r[1] = pack_pair(d0[2], d0[3]);
-    r[2] = pack_pair(d1[0], d1[1]);
-    r[3] = pack_pair(d1[2], d1[3]);
-    frag[u] = __builtin_bit_cast(bf16x8_t, r);
-  }
+__device__ __forceinline__ f32x4_t mfma4(s16x4_t a, s16x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
 }
 
-// Word offset of lane `lane`'s 8 words in block (g, b) of the group-block layout.
-__device__ __forceinline__ size_t block_word(int g, int b, int NB, int lane) {
-  return ((static_cast<size_t>(g) * NB + b) * 64 + lane) * 8;
+// One tile word of step js -> the B fragment of the main MFMA for the lane's column,
+// bf16_rne((q - z) s) for rows 8 (lane / 16) .. +7.  2 scaling MFMAs, 7 + 4 VALU ops.
+__device__ __forceinline__ bf16x8_t dequant_step(uint32_t w, const TileScale& ts, const NibbleConsts& k) {
+  s16x4_t a[2];
+  unpack_biased(a, w, k);
+  const f32x4_t d0 = mfma4(a[0], ts.diag, ts.cin);
+  const f32x4_t d1 = mfma4(a[1], ts.diag, ts.cin);
+  u32x4_t r;
+  r[0] = pack_bf16x2(d0[0], d0[1]);
+  r[1] = pack_bf16x2(d0[2], d0[3]);
+  r[2] = pack_bf16x2(d1[0], d1[1]);
+  r[3] = pack_bf16x2(d1[2], d1[3]);
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// Word offset of lane `lane`'s 4 words in tile (g, t) of the group-tile layout
+// (NT = N / 16 tiles per group row).
+__device__ __forceinline__ size_t tile_word(int g, int t, int NT, int lane) {
+  return ((static_cast<size_t>(g) * NT + t) * 64 + lane) * 4;
 }
 
 }  // namespace w4a16

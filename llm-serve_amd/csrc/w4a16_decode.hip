@@ -1,12 +1,12 @@
 // Decode / speculative-verify regime (M <= 64): HBM-bound split-K kernel.
 //
-// Each wave streams (128-row group, 32-column block) weight blocks (2 KiB, two 16-byte
-// loads per lane), dequantizes them on the matrix cores (dequant_block: the reference's
+// Each wave streams (128-row group, 16-column tile) weight tiles (1 KiB, one 16-byte load
+// per lane), dequantizes them on the matrix cores (dequant_step: the reference's
 // bf16_rne((q - z) s) weights) and multiplies them with up to four 16-row activation
 // fragments by v_mfma_f32_16x16x32_bf16, accumulating in fp32.  The output is the
 // reference's matmul over the reference's bf16 weights up to fp32 summation order.
 //
-// Work split.  A workgroup owns TB 32-column blocks and one K range (blockIdx.y of
+// Work split.  A workgroup owns TN 16-column tiles and one K range (blockIdx.y of
 // `split`); its W waves take interleaved 128-row groups of that range, are reduced
 // through LDS in a fixed order, and with split > 1 the workgroups exchange fp32 partials
 // (store_partial / arrive / load_partial): the last one to finish a column block sums
@@ -27,14 +27,14 @@ struct DecodeArgs {
   int M, K, N, split;
 };
 
-// Everything one wave needs for one 128-row group: two 16-byte weight loads per block,
-// the raw scale-pair and zero words of its 2 TB output columns, and the MB x 4 activation
+// Everything one wave needs for one 128-row group: one 16-byte weight load per tile, the
+// raw scale-pair and zero words of its TN output columns, and the MB x 4 activation
 // fragments.  Loaded DEPTH groups ahead of use; decoded only when consumed.
-template <int MB, int TB>
+template <int MB, int TN>
 struct DecodeStage {
-  u32x4_t w[TB][2];
-  uint32_t s[TB][2];
-  uint32_t zw[TB][2];
+  u32x4_t w[TN];
+  uint32_t s[TN];
+  uint32_t zw[TN];
   u32x4_t a[MB][4];
 };
 
@@ -62,26 +62,22 @@ struct DecodeOffsets {
   uint32_t x_row[MB];  // (row K + 8 (lane / 16)) * 2, or kOutOfRange
 };
 
-template <int MB, int TB>
-__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TB>& st, const DecodeSources& src,
+template <int MB, int TN>
+__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN>& st, const DecodeSources& src,
                                                   const DecodeOffsets<MB>& off, int g, bool valid, int N, int cb,
                                                   int lane) {
-  const int NB = N / kBlockCols;
+  const int NT = N / kTileCols;
   const int c = lane & 15;
   const uint32_t oob = valid ? 0u : kOutOfRange;
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb) {
-    const int b = cb * TB + tb;
-    const uint32_t wo = (valid ? static_cast<uint32_t>(block_word(g, b, NB, lane)) * 4u : 0u) | oob;
-    st.w[tb][0] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
-    st.w[tb][1] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo + 16u, 0, 0);
-    const uint32_t so = oob | (static_cast<uint32_t>(g * N + kBlockCols * b + (c & ~1)) * 2u);
-    const uint32_t zo = oob | (static_cast<uint32_t>(g * (N >> 3) + 4 * b + (c >> 3)) * 4u);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      st.s[tb][u] = __builtin_amdgcn_raw_buffer_load_b32(src.s, so + 32u * u, 0, 0);
-      st.zw[tb][u] = __builtin_amdgcn_raw_buffer_load_b32(src.z, zo + 8u * u, 0, 0);
-    }
+  for (int tt = 0; tt < TN; ++tt) {
+    const int t = cb * TN + tt;
+    const uint32_t wo = (valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : 0u) | oob;
+    st.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
+    const int col = kTileCols * t + c;
+    st.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
+    st.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u),
+                                                     0, 0);
   }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -91,34 +87,26 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TB>& st, const
   }
 }
 
-template <int MB, int TB>
-__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][2 * TB], const DecodeStage<MB, TB>& st,
+template <int MB, int TN>
+__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN>& st,
                                                      const NibbleConsts& nib, int lane) {
   const int zshift = awq_shift(lane & 7);
-  TileScale ts[TB][2];
+  TileScale ts[TN];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) ts[tb][u] = make_tile_scale(st.s[tb][u], (st.zw[tb][u] >> zshift) & 0xFu, u, lane);
+  for (int tt = 0; tt < TN; ++tt) ts[tt] = make_tile_scale(st.s[tt], (st.zw[tt] >> zshift) & 0xFu, lane);
 #pragma unroll
   for (int js = 0; js < 4; ++js) {
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const u32x4_t& v = st.w[tb][js >> 1];
-      const uint32_t w0 = (js & 1) ? v[2] : v[0];
-      const uint32_t w1 = (js & 1) ? v[3] : v[1];
-      bf16x8_t frag[2];
-      dequant_block(frag, w0, w1, ts[tb], nib);
+    for (int tt = 0; tt < TN; ++tt) {
+      const bf16x8_t frag = dequant_step(st.w[tt][js], ts[tt], nib);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          acc[mb][2 * tb + u] = mfma16(__builtin_bit_cast(bf16x8_t, st.a[mb][js]), frag[u], acc[mb][2 * tb + u]);
+      for (int mb = 0; mb < MB; ++mb)
+        acc[mb][tt] = mfma16(__builtin_bit_cast(bf16x8_t, st.a[mb][js]), frag, acc[mb][tt]);
     }
   }
 }
 
-template <int MB, int TB, int DEPTH, int WAVES>
+template <int MB, int TN, int DEPTH, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -126,7 +114,6 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             uint16_t* __restrict__ y, float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
                                                             int split) {
-  constexpr int TN = 2 * TB;  // 16-column tiles per workgroup
   extern __shared__ f32x4_t red[];  // [W][MB][TN][64]
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
@@ -163,17 +150,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // each stage's wait is "all but the DEPTH - 1 younger stages".  Loads are issued
   // whether or not the group exists (out-of-range ones fetch nothing): no branch encloses
   // a load, and the scheduling barriers keep each stage's loads together and in order.
-  DecodeStage<MB, TB> ring[DEPTH];
+  DecodeStage<MB, TN> ring[DEPTH];
   const int g0 = g_begin + wave;
   const NibbleConsts nib = nibble_consts();
   for (int base = g0 - DEPTH * W; base < g_end; base += DEPTH * W) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int g = base + d * W;
-      if (g >= g0 && g < g_end) compute_decode_stage<MB, TB>(acc, ring[d], nib, lane);
+      if (g >= g0 && g < g_end) compute_decode_stage<MB, TN>(acc, ring[d], nib, lane);
       const int gn = g + DEPTH * W;
       __builtin_amdgcn_sched_barrier(0);
-      load_decode_stage<MB, TB>(ring[d], src, off, gn, gn < g_end, N, cb, lane);
+      load_decode_stage<MB, TN>(ring[d], src, off, gn, gn < g_end, N, cb, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -244,37 +231,46 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   if (threadIdx.x == 0) rearm(&counters[cb]);
 }
 
-template <int MB, int TB, int DEPTH, int WAVES>
+template <int MB, int TN, int DEPTH, int WAVES>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
-  const dim3 grid(a.N / (kBlockCols * TB), a.split);
-  const size_t lds = static_cast<size_t>(WAVES) * MB * 2 * TB * 64 * sizeof(f32x4_t);
-  decode_kernel<MB, TB, DEPTH, WAVES><<<grid, 64 * WAVES, lds, stream>>>(
+  // Configurations whose cross-wave reduction exceeds 64 KiB of LDS are rejected by the
+  // API before launch; they are not instantiated.
+  if constexpr (WAVES * MB * TN > 64) {
+    return hipErrorInvalidValue;
+  } else {
+  const dim3 grid(a.N / (kTileCols * TN), a.split);
+  const size_t lds = static_cast<size_t>(WAVES) * MB * TN * 64 * sizeof(f32x4_t);
+  decode_kernel<MB, TN, DEPTH, WAVES><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split);
   return hipGetLastError();
-}
-
-template <int MB, int TB, int DEPTH>
-static hipError_t launch_decode_w(const DecodeArgs& a, int waves, hipStream_t stream) {
-  switch (waves) {
-    case 4: return launch_decode_t<MB, TB, DEPTH, 4>(a, stream);
-    case 8: return launch_decode_t<MB, TB, DEPTH, 8>(a, stream);
-    default: return launch_decode_t<MB, TB, DEPTH, 16>(a, stream);
   }
 }
 
-template <int MB, int TB>
+template <int MB, int TN, int DEPTH>
+static hipError_t launch_decode_w(const DecodeArgs& a, int waves, hipStream_t stream) {
+  switch (waves) {
+    case 4: return launch_decode_t<MB, TN, DEPTH, 4>(a, stream);
+    case 8: return launch_decode_t<MB, TN, DEPTH, 8>(a, stream);
+    default: return launch_decode_t<MB, TN, DEPTH, 16>(a, stream);
+  }
+}
+
+template <int MB, int TN>
 static hipError_t launch_decode_d(const DecodeArgs& a, int depth, int waves, hipStream_t stream) {
   switch (depth) {
-    case 1: return launch_decode_w<MB, TB, 1>(a, waves, stream);
-    case 2: return launch_decode_w<MB, TB, 2>(a, waves, stream);
-    default: return launch_decode_w<MB, TB, 4>(a, waves, stream);
+    case 1: return launch_decode_w<MB, TN, 1>(a, waves, stream);
+    case 2: return launch_decode_w<MB, TN, 2>(a, waves, stream);
+    default: return launch_decode_w<MB, TN, 4>(a, waves, stream);
   }
 }
 
 template <int MB>
 static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int waves, hipStream_t stream) {
-  if (tn == 2) return launch_decode_d<MB, 1>(a, depth, waves, stream);
-  return launch_decode_d<MB, 2>(a, depth, waves, stream);
+  switch (tn) {
+    case 1: return launch_decode_d<MB, 1>(a, depth, waves, stream);
+    case 2: return launch_decode_d<MB, 2>(a, depth, waves, stream);
+    default: return launch_decode_d<MB, 4>(a, depth, waves, stream);
+  }
 }
 
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,

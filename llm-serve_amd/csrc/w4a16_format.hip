@@ -1,4 +1,4 @@
-// Format kernels: AutoAWQ unpack, bit-exact dequant, and the repack into the group-block
+// Format kernels: AutoAWQ unpack, bit-exact dequant, and the repack into the group-tile
 // layout described in w4a16_common.h.  All are HBM-bound byte/integer work.
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
@@ -57,63 +57,62 @@ __global__ __launch_bounds__(256) void dequant_awq_kernel(const uint32_t* __rest
   *reinterpret_cast<uint4*>(w_out + idx * 8) = make_uint4(outw[0], outw[1], outw[2], outw[3]);
 }
 
-// One thread per output word of the group-block layout (see w4a16_common.h): gathers the
-// AutoAWQ word it holds.  Writes are coalesced; this runs once per weight at load time.
+// One thread per output word of the group-tile layout (see w4a16_common.h): gathers the
+// 8 nibbles it holds from two AutoAWQ words (rows r and r + 4, the same 4 columns).
+// Writes are coalesced; this runs once per weight at load time.
 __global__ __launch_bounds__(256) void repack_kernel(const uint32_t* __restrict__ qweight,
                                                      uint32_t* __restrict__ packed, int K, int N) {
   const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const size_t total = static_cast<size_t>(K) * (N >> 3);
   if (idx >= total) return;
-  const int NB = N / kBlockCols;
-  const int slot = static_cast<int>(idx & 7);
-  const int lane = static_cast<int>((idx >> 3) & 63);
-  const size_t blk = idx >> 9;
-  const int g = static_cast<int>(blk / NB);
-  const int b = static_cast<int>(blk - static_cast<size_t>(g) * NB);
-  const int js = slot >> 1, h = slot & 1;
-  const int row = kGroup * g + 32 * js + 8 * ((lane & 15) >> 2) + 4 * h + (lane & 3);
-  const int cw = 4 * b + (lane >> 4);
-  packed[idx] = qweight[static_cast<size_t>(row) * (N >> 3) + cw];
+  const int NT = N / kTileCols;
+  const int js = static_cast<int>(idx & 3);
+  const int lane = static_cast<int>((idx >> 2) & 63);
+  const size_t tile = idx >> 8;
+  const int g = static_cast<int>(tile / NT);
+  const int t = static_cast<int>(tile - static_cast<size_t>(g) * NT);
+  const int col0 = kTileCols * t + 4 * ((lane >> 2) & 3);  // 4 columns of one AutoAWQ word
+  uint32_t out = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = kGroup * g + 32 * js + 8 * (lane >> 4) + 4 * h + (lane & 3);
+    const uint32_t src = qweight[static_cast<size_t>(row) * (N >> 3) + (col0 >> 3)];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t q = (src >> awq_shift((col0 + k) & 7)) & 0xFu;
+      out |= q << (8 * h + 4 * (k >> 1) + 16 * (k & 1));
+    }
+  }
+  packed[idx] = out;
 }
 
-// One wave per (group, 32-column block): the MFMA GEMMs' dequant (dequant_block) run on
-// the block, with every lane writing the 8 rows x 2 columns it produces.  Exists to check
+// One wave per (group, 16-column tile): the MFMA GEMMs' dequant (dequant_step) run on the
+// tile, with every lane writing the 8 rows x 1 column it produces per step.  Exists to check
 // that path bit for bit against the reference.
 __global__ __launch_bounds__(256) void dequant_packed_kernel(const uint4* __restrict__ packed,
                                                              const uint32_t* __restrict__ qzeros,
                                                              const uint16_t* __restrict__ scales,
                                                              uint16_t* __restrict__ w_out, int K, int N) {
-  const int NB = N / kBlockCols;
+  const int NT = N / kTileCols;
   const int lane = threadIdx.x & 63;
-  const size_t block = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + wave_id();
-  const size_t nblocks = static_cast<size_t>(K / kGroup) * NB;
-  if (block >= nblocks) return;  // whole wave exits together
-  const int g = static_cast<int>(block / NB);
-  const int b = static_cast<int>(block - static_cast<size_t>(g) * NB);
-  const uint4* src = packed + block * 128 + lane * 2;
-  const uint4 v0 = src[0], v1 = src[1];
-  const uint32_t words[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-  TileScale ts[2];
-  int cols[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    cols[u] = kBlockCols * b + 16 * u + (lane & 15);
-    const uint32_t s_pair = reinterpret_cast<const uint32_t*>(scales)[(static_cast<size_t>(g) * N + cols[u]) >> 1];
-    ts[u] = make_tile_scale(s_pair, load_zero(qzeros, g, N, cols[u]), u, lane);
-  }
+  const size_t tile = static_cast<size_t>(blockIdx.x) * (blockDim.x >> 6) + wave_id();
+  const size_t ntiles = static_cast<size_t>(K / kGroup) * NT;
+  if (tile >= ntiles) return;  // whole wave exits together
+  const int g = static_cast<int>(tile / NT);
+  const int t = static_cast<int>(tile - static_cast<size_t>(g) * NT);
+  const uint4 v = packed[tile * 64 + lane];
+  const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+  const int col = kTileCols * t + (lane & 15);
+  const uint32_t s_pair = reinterpret_cast<const uint32_t*>(scales)[(static_cast<size_t>(g) * N + col) >> 1];
+  const TileScale ts = make_tile_scale(s_pair, load_zero(qzeros, g, N, col), lane);
   const NibbleConsts nib = nibble_consts();
 #pragma unroll
   for (int js = 0; js < 4; ++js) {
-    bf16x8_t frag[2];
-    dequant_block(frag, words[2 * js], words[2 * js + 1], ts, nib);
+    const u32x4_t f = __builtin_bit_cast(u32x4_t, dequant_step(words[js], ts, nib));
     const int k0 = kGroup * g + 32 * js + 8 * (lane >> 4);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const u32x4_t f = __builtin_bit_cast(u32x4_t, frag[u]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        w_out[static_cast<size_t>(k0 + e) * N + cols[u]] = static_cast<uint16_t>(f[e >> 1] >> (16 * (e & 1)));
-    }
+    for (int e = 0; e < 8; ++e)
+      w_out[static_cast<size_t>(k0 + e) * N + col] = static_cast<uint16_t>(f[e >> 1] >> (16 * (e & 1)));
   }
 }
 
@@ -142,7 +141,7 @@ hipError_t launch_repack(const uint32_t* qweight, uint32_t* packed, int K, int N
 
 hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros, const uint16_t* scales,
                                  uint16_t* w_out, int K, int N, hipStream_t stream) {
-  const size_t waves = static_cast<size_t>(K / kGroup) * (N / kBlockCols);
+  const size_t waves = static_cast<size_t>(K / kGroup) * (N / kTileCols);
   dequant_packed_kernel<<<blocks_for(waves, 4), 256, 0, stream>>>(
       reinterpret_cast<const uint4*>(packed), qzeros, scales, w_out, K, N);
   return hipGetLastError();

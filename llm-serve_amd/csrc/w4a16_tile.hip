@@ -6,8 +6,9 @@
 // v_mfma_f32_16x16x32_bf16.  Because a wave's columns belong to it alone, each weight is
 // dequantized exactly once per workgroup, on the matrix cores straight from its 16-byte
 // loads into MFMA B fragments -- bf16_rne((q - z) s), the reference's weights, see
-// dequant_block -- with no LDS round trip.  The activation tile (BM rows x one 128-deep group) is shared by all four
-// waves through LDS: it is brought in by direct-to-LDS 16-byte loads
+// dequant_step -- with no LDS round trip.  The activation tile (BM rows x one 128-deep
+// group) is shared by all four waves through LDS: it is brought in by direct-to-LDS 16-byte
+// loads
 // (global_load_lds_dwordx4), double-buffered one group ahead, in a row-major layout whose
 // 16-byte chunks are XOR-swizzled by (row & 7) so the A-fragment reads are conflict-free.
 //
@@ -45,35 +46,29 @@ __device__ __forceinline__ void issue_a_stage(const uint16_t* __restrict__ x, ui
   }
 }
 
-// Raw loads of one group for a wave's 64 columns (two 32-column layout blocks): two
-// 16-byte weight loads per block, and the scale and zero words of the lane's column in
-// each of the 4 tiles.  Decoding waits until the group is consumed.
+// Raw loads of one group for a wave's 64 columns (four 16-column layout tiles): one
+// 16-byte weight load per tile, and the scale-pair and zero words of the lane's column in
+// each tile.  Decoding waits until the group is consumed.
 struct BGroup {
-  uint4 w[2][2];
-  uint32_t s[2][2];   // bf16 scale pair holding the lane's column
-  uint32_t zw[2][2];  // AutoAWQ zero word holding the lane's column
+  uint4 w[4];
+  uint32_t s[4];   // bf16 scale pair holding the lane's column
+  uint32_t zw[4];  // AutoAWQ zero word holding the lane's column
 };
 
 // Wave-uniform base pointers plus lane offsets (scalar-base addressing).
 __device__ __forceinline__ void load_b_group(BGroup& b, const uint4* __restrict__ packed,
                                              const uint32_t* __restrict__ qzeros,
-                                             const uint16_t* __restrict__ scales, int g, int N, int blk0,
+                                             const uint16_t* __restrict__ scales, int g, int N, int t0,
                                              int lane) {
-  const int NB = N / kBlockCols;
+  const int NT = N / kTileCols;
   const int c = lane & 15;
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const uint4* pw = packed + block_word(g, blk0 + tb, NB, 0) / 4;
-    b.w[tb][0] = pw[2 * lane];
-    b.w[tb][1] = pw[2 * lane + 1];
-    const uint32_t* ps = reinterpret_cast<const uint32_t*>(scales + static_cast<size_t>(g) * N +
-                                                           kBlockCols * (blk0 + tb));
-    const uint32_t* pz = qzeros + static_cast<size_t>(g) * (N >> 3) + 4 * (blk0 + tb);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      b.s[tb][u] = ps[8 * u + (c >> 1)];
-      b.zw[tb][u] = pz[2 * u + (c >> 3)];
-    }
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = t0 + tt;
+    b.w[tt] = packed[tile_word(g, t, NT, 0) / 4 + lane];
+    const int col = kTileCols * t + c;
+    b.s[tt] = reinterpret_cast<const uint32_t*>(scales)[(static_cast<size_t>(g) * N + col) >> 1];
+    b.zw[tt] = qzeros[static_cast<size_t>(g) * (N >> 3) + (col >> 3)];
   }
 }
 
@@ -84,18 +79,16 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
                                           const NibbleConsts& nib, int lane) {
   const int arow = lane & 15;
   const int zshift = awq_shift(lane & 7);
-  TileScale ts[2][2];
+  TileScale ts[4];
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) ts[tb][u] = make_tile_scale(b.s[tb][u], (b.zw[tb][u] >> zshift) & 0xFu, u, lane);
+  for (int tt = 0; tt < 4; ++tt) ts[tt] = make_tile_scale(b.s[tt], (b.zw[tt] >> zshift) & 0xFu, lane);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    bf16x8_t bf[2][2];
+    bf16x8_t bf[4];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      const uint4& v = b.w[tb][j >> 1];
-      dequant_block(bf[tb], (j & 1) ? v.z : v.x, (j & 1) ? v.w : v.y, ts[tb], nib);
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint4& v = b.w[tt];
+      bf[tt] = dequant_step(j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w, ts[tt], nib);
     }
     const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 7);
     const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
@@ -103,7 +96,7 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
     for (int mt = 0; mt < WM; ++mt) {
       const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = mfma16(a, bf[tt >> 1][tt & 1], acc[mt][tt]);
+      for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = mfma16(a, bf[tt], acc[mt][tt]);
     }
   }
 }
@@ -140,7 +133,7 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   const int g_end = (G * (sidx + 1)) / split;
   const int row0 = mbk * BM;
   const int col_w = nbk * kTileBN + 64 * wave;  // first column of this wave
-  const int blk0 = col_w / kBlockCols;
+  const int t0 = col_w / kTileCols;
   const bool active = col_w < N;  // wave-uniform: the last n-block may be partly past N
 
   f32x4_t acc[WM][4];
@@ -153,7 +146,7 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   BGroup cur, nxt;
   if (g_begin < g_end) {
     issue_a_stage<WM>(x, stage0, row0, M, K, g_begin, wave, lane);
-    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, N, blk0, lane);
+    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, N, t0, lane);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -162,7 +155,7 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   for (int g = g_begin; g < g_end; g += 2) {
     if (g + 1 < g_end) {
       issue_a_stage<WM>(x, stage1, row0, M, K, g + 1, wave, lane);
-      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, N, blk0, lane);
+      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, N, t0, lane);
     }
     if (active) mma_group<WM>(acc, stage0, cur, nib, lane);
     __builtin_amdgcn_s_waitcnt(0);
@@ -170,7 +163,7 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
     if (g + 1 >= g_end) break;
     if (g + 2 < g_end) {
       issue_a_stage<WM>(x, stage0, row0, M, K, g + 2, wave, lane);
-      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, N, blk0, lane);
+      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, N, t0, lane);
     }
     if (active) mma_group<WM>(acc, stage1, nxt, nib, lane);
     __builtin_amdgcn_s_waitcnt(0);

@@ -15,7 +15,7 @@ Same names, argument meaning and error behaviour as the reference:
 There is one execution backend, the HIP library (libw4a16.so): every tensor operation
 runs there and raises when the library or a GPU is missing -- nothing falls back to a CPU
 path.  ``process_weights_after_loading`` reorders the ``qweight`` words once into the kernels'
-group-block order (``awq_qweight``); ``qzeros`` and ``scales`` are consumed as stored.
+group-tile layout (``awq_qweight``); ``qzeros`` and ``scales`` are consumed as stored.
 """
 from __future__ import annotations
 
@@ -224,14 +224,14 @@ def dequantize_awq_gemm(qweight: torch.Tensor, qzeros: torch.Tensor, scales: tor
 
 
 def repack_awq_qweight(qweight: torch.Tensor) -> torch.Tensor:
-    """AutoAWQ qweight [K, N/8] -> the kernels' group-block word order (flat int32, same bytes)."""
+    """AutoAWQ qweight [K, N/8] -> the kernels' group-tile layout (flat int32, same bytes)."""
     if qweight.ndim != 2 or qweight.dtype != torch.int32:
         raise ValueError("qweight must be a two-dimensional int32 tensor")
     k, n = qweight.shape[0], qweight.shape[1] * 8
     if k % 128:
         raise ValueError("qweight K must be divisible by 128")
-    if n % 32:
-        raise ValueError("qweight N must be divisible by 32")
+    if n % 16:
+        raise ValueError("qweight N must be divisible by 16")
     return lib().repack_qweight(qweight.contiguous())
 
 

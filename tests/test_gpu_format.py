@@ -60,21 +60,26 @@ def test_dequant_bit_exact_full_qwen3_shapes(gpu_lib, shape):
     np.testing.assert_array_equal(bits_of(w), want)
 
 
-def group_block_layout_numpy(qweight: np.ndarray) -> np.ndarray:
-    """The repacked word order restated from its definition: per (128-row group g,
-    32-column block b), lane l and slot 2 js + h hold qweight[k][4 b + l // 16] with
-    k = 128 g + 32 js + 8 ((l % 16) // 4) + 4 h + l % 4."""
-    k, c8 = qweight.shape
-    n = c8 * 8
-    out = np.zeros(k * c8, dtype=np.int32)
+def group_tile_layout_numpy(qweight: np.ndarray) -> np.ndarray:
+    """The repacked layout restated from its definition, starting from the logical 4-bit
+    values q[row, col] (the oracle's AutoAWQ unpack): per (128-row group g, 16-column tile
+    t), lane l and step js hold a word whose bit 8 h + 4 (k // 2) + 16 (k % 2) carries
+    q[128 g + 32 js + 8 (l // 16) + 4 h + l % 4, 16 t + 4 ((l // 4) % 4) + k]."""
+    q = ora.unpack_awq_int4(qweight).astype(np.uint32)  # [K, N]
+    k, n = q.shape
+    out = np.zeros(k * n // 8, dtype=np.uint32)
     for g in range(k // 128):
-        for b in range(n // 32):
+        for t in range(n // 16):
             for lane in range(64):
                 for js in range(4):
+                    word = 0
                     for h in range(2):
-                        row = 128 * g + 32 * js + 8 * ((lane % 16) // 4) + 4 * h + lane % 4
-                        out[((g * (n // 32) + b) * 64 + lane) * 8 + 2 * js + h] = qweight[row, 4 * b + lane // 16]
-    return out
+                        for kk in range(4):
+                            row = 128 * g + 32 * js + 8 * (lane // 16) + 4 * h + lane % 4
+                            col = 16 * t + 4 * ((lane // 4) % 4) + kk
+                            word |= int(q[row, col]) << (8 * h + 4 * (kk // 2) + 16 * (kk % 2))
+                    out[((g * (n // 16) + t) * 64 + lane) * 4 + js] = word
+    return out.view(np.int32)
 
 
 def test_repack_matches_layout_definition(gpu_lib):
@@ -82,14 +87,19 @@ def test_repack_matches_layout_definition(gpu_lib):
     rng = np.random.default_rng(8)
     qw = rng.integers(-2 ** 31, 2 ** 31, size=(256, 8), dtype=np.int64).astype(np.int32)  # K=256, N=64
     got = awq.repack_awq_qweight(torch.from_numpy(qw).cuda()).cpu().numpy()
-    np.testing.assert_array_equal(got, group_block_layout_numpy(qw))
+    np.testing.assert_array_equal(got, group_tile_layout_numpy(qw))
 
 
-def test_repack_is_a_permutation_of_the_words(gpu_lib):
+def test_repack_keeps_every_tiles_values(gpu_lib):
+    """Each 1 KiB tile holds exactly the 2048 values of its (group, 16 columns) block."""
     awq = awq_mod()
-    qw = torch.arange(512 * 96, dtype=torch.int32, device="cuda").view(512, 96)  # K=512, N=768
-    got = awq.repack_awq_qweight(qw)
-    assert torch.equal(torch.sort(got).values, qw.flatten())
+    rng = np.random.default_rng(9)
+    k, n = 512, 768
+    qw = rng.integers(-2 ** 31, 2 ** 31, size=(k, n // 8), dtype=np.int64).astype(np.int32)
+    got = awq.repack_awq_qweight(torch.from_numpy(qw).cuda()).cpu().numpy().view(np.uint32)
+    nib = np.stack([(got >> (4 * i)) & 0xF for i in range(8)], axis=-1).reshape(k // 128, n // 16, 2048)
+    q = ora.unpack_awq_int4(qw).reshape(k // 128, 128, n // 16, 16).transpose(0, 2, 1, 3).reshape(k // 128, n // 16, 2048)
+    np.testing.assert_array_equal(np.sort(nib, axis=-1), np.sort(q, axis=-1))
 
 
 @pytest.mark.parametrize("case", sorted(golden_cases()))
