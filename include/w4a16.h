@@ -111,7 +111,8 @@ int w4a16_split_k(int M, int K, int N);
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
  * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,4}, p1 = waves per
  * workgroup in {4,8,16}, p2 = 128-row groups in flight per wave in {1,2,4}, M <= 64) or
- * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {8,16}; p1, p2 ignored);
+ * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {4,8,16}, p1 = waves per SIMD the
+ * register allocation targets in {1,2} (1 for p0 = 16); p2 ignored);
  * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises
  * every split-K reduction path at small sizes). */
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,

@@ -46,7 +46,7 @@ size_t decode_lds_bytes(int M, int tn, int waves) {
 struct GemmPlan {
   int regime;  // w4a16_regime_id
   int p0;      // decode: column tiles per workgroup; tile: wm (16-row tiles per wave)
-  int p1;      // decode: waves per workgroup; tile: unused
+  int p1;      // decode: waves per workgroup; tile: waves per SIMD the registers allow
   int p2;      // decode: groups in flight per wave; tile: unused
   int split;   // K splits (1 = none)
 };
@@ -54,46 +54,55 @@ struct GemmPlan {
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // Decode regime, chosen from measured sweeps over the Qwen3-8B projection shapes.
-//  * Narrow layers (N <= 4096) at M <= 16 use one 16-column tile per workgroup, so that
-//    every CU gets work; long K (>= 8192) at M > 4 instead splits K in two with 32-column
-//    workgroups, which keeps the activation traffic per weight down.
-//  * Wider layers use 32-column workgroups (tn = 2), and at M > 48 on N >= 16384 64-column
-//    workgroups (tn = 4) that share each activation fragment among four tiles.
-//  * 8 waves with one group in flight per wave, or 4 waves with two; K is split only where
-//    the column tiles alone cannot cover the CUs (every split costs a round of fp32
-//    partials).
+//  * Narrow layers (N <= 4096) at M <= 16 use one 16-column tile per workgroup so that
+//    every CU gets work; with long K (>= 8192) and M > 4, 32-column workgroups with K split
+//    in two instead (64-column ones split in four at M = 17..32), which keeps the
+//    activation traffic per weight down.
+//  * Wider layers use 32-column workgroups (tn = 2) at M <= 32 and 64-column workgroups
+//    (tn = 4, 4 waves) at M > 32, where each activation fragment feeds four tiles.
+//  * 8 waves with one group in flight each, or 4 waves with two.  K is split where the
+//    column tiles alone cannot cover the CUs.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
+  const bool narrow = N <= 4096, long_k = K >= 8192;
   int tn = 2, waves = 8, depth = 1, split = 1;
-  if (MB == 1) {
-    if (N <= 4096 && !(K >= 8192 && M > 4)) {
-      tn = 1;
-      waves = M <= 4 ? 8 : 4;
-      depth = 2;
-    } else if (N <= 4096) {
-      split = 2;
-    }
-  } else if (MB == 2) {
-    split = N <= 4096 ? 2 : 1;
-  } else {
-    tn = N >= 16384 ? 4 : 2;
-    waves = (tn == 4 || N > 4096) ? 4 : 8;  // decode_lds_bytes(64, tn, waves) <= 64 KiB
+  if (MB == 1 && narrow && long_k && M > 4) {
+    split = 2;
+  } else if (MB == 2 && narrow && long_k) {
+    tn = 4;
+    split = 4;
+  } else if (MB == 1 && narrow) {
+    tn = 1;
+    waves = M <= 4 ? 8 : 4;
     depth = 2;
-    split = N <= 4096 ? 2 : 1;
+  } else if (MB == 2) {
+    split = narrow ? 2 : 1;
+  } else if (MB >= 3) {
+    if (narrow && !long_k) {
+      split = 2;
+    } else {
+      tn = 4;
+      waves = 4;  // decode_lds_bytes(64, 4, 4) = 64 KiB
+      depth = 2;
+      split = N >= 16384 ? 1 : narrow ? 4 : 2;
+    }
   }
   if (split > G) split = G;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
-// Tile regime: 128-row tiles (wm = 8) everywhere; split K in two when the tiles alone
-// cannot cover the CUs and K is long enough that each split keeps >= 32 groups.
+// Tile regime: 64-row tiles (wm = 4) with registers for two waves per SIMD everywhere
+// (measured best from M = 128 to 2048 on all four shapes).  K is split by the largest power
+// of two (at most 8, keeping >= 4 groups per split) that brings the grid up to about one
+// workgroup per CU; the fp32 partials are reduced by the last workgroup of each tile.
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  const int wm = 8;
+  const int wm = 4;
   const int tiles = ceil_div(M, 16 * wm) * ceil_div(N, 256);
-  const int split = (tiles < 128 && G >= 64) ? 2 : 1;
-  return GemmPlan{W4A16_REGIME_TILE, wm, 0, 0, split};
+  int split = 1;
+  while (split < 8 && tiles * split * 2 <= 256 && split * 2 * 4 <= G) split *= 2;
+  return GemmPlan{W4A16_REGIME_TILE, wm, 2, 0, split};
 }
 
 GemmPlan plan(int M, int K, int N) {
@@ -112,9 +121,18 @@ size_t counters_needed(const GemmPlan& p, int M, int N) {
   return static_cast<size_t>(ceil_div(M, 16 * p.p0)) * ceil_div(N, 256);
 }
 
+// fp32 partial tiles: split x (M padded to the kernel's row block) x (N padded to its
+// column block), stored as lane-major 16-byte fragments.
+size_t partial_bytes(const GemmPlan& p, int M, int N) {
+  if (p.regime == W4A16_REGIME_DECODE)
+    return static_cast<size_t>(p.split) * (16 * ceil_div(M, 16)) * N * sizeof(float);
+  const int bm = 16 * p.p0;
+  return static_cast<size_t>(p.split) * (bm * ceil_div(M, bm)) * (256 * ceil_div(N, 256)) * sizeof(float);
+}
+
 size_t workspace_for(const GemmPlan& p, int M, int N) {
   if (p.regime == W4A16_REGIME_NONE || p.split <= 1) return 0;
-  return kCounterBytes + static_cast<size_t>(p.split) * M * N * sizeof(float);
+  return kCounterBytes + partial_bytes(p, M, N);
 }
 
 int validate_gemm(const void* x, const void* packed, const void* qzeros, const void* scales, const void* y, int M,
@@ -145,6 +163,8 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(W4A16_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
   if (need > 0 && !aligned(workspace, 256)) return fail(W4A16_ERR_ALIGN, "workspace must be 256-byte aligned");
+  if (need > 0 && partial_bytes(p, M, N) >= kMaxTensorBytes)
+    return fail(W4A16_ERR_SHAPE, "split-K partials of %zu bytes exceed 2 GiB", partial_bytes(p, M, N));
   if (need > 0 && counters_needed(p, M, N) > kMaxCounters)
     return fail(W4A16_ERR_SHAPE, "split-K needs %zu arrival counters (limit %zu)", counters_needed(p, M, N),
                 kMaxCounters);
@@ -156,8 +176,8 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
     return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p2,
                                                  p.p1, p.split, stream),
                         "decode");
-  return check_launch(w4a16::launch_tile_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.split, stream),
-                      "tile");
+  return check_launch(
+      w4a16::launch_tile_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p1, p.split, stream), "tile");
 }
 
 }  // namespace
@@ -260,7 +280,9 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
                   decode_lds_bytes(M, p0, p1), kDecodeMaxLds);
   } else if (regime == W4A16_REGIME_TILE) {
-    if (p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 8 or 16");
+    if (p0 != 4 && p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 4, 8 or 16");
+    if (p1 != 1 && p1 != 2) return fail(W4A16_ERR_ARG, "tile occupancy must be 1 or 2");
+    if (p0 == 16 && p1 != 1) return fail(W4A16_ERR_ARG, "tile wm 16 supports occupancy 1 only");
   } else {
     return fail(W4A16_ERR_ARG, "unknown regime %d", regime);
   }

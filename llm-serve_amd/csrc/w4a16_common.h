@@ -100,19 +100,30 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 // ---------------------------------------------------------------------------
 // Split-K exchange between workgroups.
 //
-// Partial sums travel as relaxed agent-scope atomic stores and loads, which CDNA
-// performs coherently across XCDs (sc1 accesses), so no L2-wide write-back or
+// Partial sums travel as lane-major 16-byte fragments written and read with the
+// device-coherent cache policy sc1 (coherent across XCDs), so no L2-wide write-back or
 // invalidate is needed -- a release/acquire fence at agent scope would emit both
-// (buffer_wbl2 / buffer_inv) for every workgroup.  Ordering comes from the hardware:
-// each writer's partial stores complete (the workgroup barrier waits for vmcnt(0))
-// before one lane increments the arrival counter, and the last arriver issues its
-// partial loads only after that increment has returned.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// (buffer_wbl2 / buffer_inv) for every workgroup.  Ordering comes from the hardware: each
+// writer waits for its fragment stores to complete (s_waitcnt vmcnt(0)) before one lane
+// increments the arrival counter with a relaxed agent-scope atomic, and the last arriver
+// issues its fragment loads only after that increment has returned.  Plain buffer
+// operations rather than atomic loads let the reducer issue many loads before one wait.
+constexpr int kCoherentPolicy = 16;        // buffer-op cache policy bits: sc1
+constexpr int kRawBufferWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit data format
+
+// Buffer descriptor over `bytes` bytes at p: loads past the end return zeros without a
+// memory access, stores past the end are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                           kRawBufferWord3);
 }
 
-__device__ __forceinline__ float load_partial(float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store_fragment(__amdgpu_buffer_rsrc_t r, uint32_t offset, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, offset, 0, kCoherentPolicy);
+}
+
+__device__ __forceinline__ f32x4_t load_fragment(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kCoherentPolicy));
 }
 
 // Arrival count before this workgroup's increment.

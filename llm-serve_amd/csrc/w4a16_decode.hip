@@ -9,7 +9,7 @@
 // Work split.  A workgroup owns TN 16-column tiles and one K range (blockIdx.y of
 // `split`); its W waves take interleaved 128-row groups of that range, are reduced
 // through LDS in a fixed order, and with split > 1 the workgroups exchange fp32 partials
-// (store_partial / arrive / load_partial): the last one to finish a column block sums
+// (store_fragment / arrive / load_fragment): the last one to finish a column block sums
 // them in split order, writes bf16 and re-arms the counter.  Results are deterministic.
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
@@ -48,12 +48,6 @@ struct DecodeSources {
 };
 
 constexpr uint32_t kOutOfRange = 0x80000000u;  // >= every num_records (checked on the host)
-constexpr int kRawBufferWord3 = 0x00020000;    // raw (untyped) buffer, 32-bit data format
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0), static_cast<int>(bytes),
-                                           kRawBufferWord3);
-}
 
 // Byte offsets that do not depend on the group: per activation fragment row (or
 // kOutOfRange for rows >= M), and per block of the lane's weight words.
@@ -127,10 +121,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const int col0 = cb * (16 * TN) + (lane & 15);  // this lane's column in tile 0
 
   DecodeSources src;
-  src.x = make_rsrc(x, static_cast<uint32_t>(M) * K * 2u);
-  src.w = make_rsrc(packed, static_cast<uint32_t>(K) * (N / 2));
-  src.s = make_rsrc(scales, static_cast<uint32_t>(G) * N * 2u);
-  src.z = make_rsrc(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u);
+  src.x = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
+  src.w = make_buffer(packed, static_cast<uint32_t>(K) * (N / 2));
+  src.s = make_buffer(scales, static_cast<uint32_t>(G) * N * 2u);
+  src.z = make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u);
   DecodeOffsets<MB> off;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -199,16 +193,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
     return;
   }
 
+  // Split K: every workgroup stores its fp32 fragments (lane-major, 1 KiB per output pair)
+  // into partials[sidx][cb]; the last to arrive sums all splits in split order.
+  const int nwg = gridDim.x;
+  const __amdgpu_buffer_rsrc_t rp = make_buffer(partials, static_cast<uint32_t>(split) * nwg * kPairs * 1024u);
+  const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
     if (p % W != wave) continue;
-    const int n = col0 + 16 * (p % TN);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * (p / TN) + 4 * (lane >> 4) + i;
-      if (row < M) store_partial(partials + (static_cast<size_t>(sidx) * M + row) * N + n, out[p][i]);
-    }
+    store_fragment(rp, ((static_cast<uint32_t>(sidx) * nwg + cb) * kPairs + p) * 1024u + lane_off, out[p]);
   }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) is_last = (arrive(&counters[cb]) == split - 1);
   __syncthreads();
@@ -216,16 +211,21 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
     if (p % W != wave) continue;
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < split; s0 += 4) {
+      f32x4_t part[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)  // splits past `split` lie past the buffer: zeros, no access
+        part[u] = load_fragment(rp, ((static_cast<uint32_t>(s0 + u) * nwg + cb) * kPairs + p) * 1024u + lane_off);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < split) v += (s0 + u == sidx) ? out[p] : part[u];
+    }
     const int n = col0 + 16 * (p % TN);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * (p / TN) + 4 * (lane >> 4) + i;
-      if (row < M) {
-        float v = 0.0f;
-        for (int s = 0; s < split; ++s)
-          v += (s == sidx) ? out[p][i] : load_partial(partials + (static_cast<size_t>(s) * M + row) * N + n);
-        y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(v);
-      }
+      if (row < M) y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(v[i]);
     }
   }
   if (threadIdx.x == 0) rearm(&counters[cb]);

@@ -17,16 +17,17 @@ hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros,
 
 // Split-K decode kernel, M <= 64.  tn in {1, 2, 4} 16-column tiles per workgroup, depth in
 // {1, 2, 4} groups in flight per wave, waves in {4, 8, 16}, 1 <= split <= K / 128.
-// `partials` holds split * M * N floats and `counters` N / (16 tn) ints (both unused when
-// split == 1).
+// `partials` holds the split-K fp32 fragments and `counters` N / (16 tn) ints (both unused
+// when split == 1).
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
                              int N, int tn, int depth, int waves, int split, hipStream_t stream);
 
-// LDS-tiled MFMA GEMM: workgroup tile (16 wm) x 256, wm in {8, 16}.  `partials` holds
-// split * M * N floats and `counters` one int per output tile (unused when split == 1).
+// LDS-tiled MFMA GEMM: workgroup tile (16 wm) x 256, wm in {4, 8, 16}; occ in {1, 2} waves
+// per SIMD the register allocation targets (wm 16: 1 only).  `partials` holds the split-K
+// fp32 fragments and `counters` one int per output tile (both unused when split == 1).
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                            const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int split, hipStream_t stream);
+                           int N, int wm, int occ, int split, hipStream_t stream);
 
 }  // namespace w4a16

@@ -101,8 +101,9 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
   }
 }
 
-template <int WM>
-__global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict__ x,
+// OCC = waves per SIMD the register allocation must allow (1 or 2).
+template <int WM, int OCC>
+__global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restrict__ x,
                                                       const uint4* __restrict__ packed,
                                                       const uint32_t* __restrict__ qzeros,
                                                       const uint16_t* __restrict__ scales,
@@ -171,39 +172,44 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   }
 
   if (split > 1) {
-    if (active) {
-#pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = row0 + 16 * mt + 4 * (lane >> 4) + i;
-          const int n = col_w + 16 * tt + (lane & 15);
-          if (row < M) store_partial(partials + (static_cast<size_t>(sidx) * M + row) * N + n, acc[mt][tt][i]);
-        }
-    }
-    __syncthreads();
+    // Every workgroup stores its fp32 fragments (lane-major, 1 KiB per 16 x 16 MFMA tile)
+    // into partials[sidx][tile][wave]; the last to arrive sums all splits in split order,
+    // 8 fragments at a time so that the loads of a chunk share one wait.
+    const int ntiles = m_blocks * n_blocks;
     const int tile = mbk * n_blocks + nbk;
+    constexpr int kFrags = WM * 4;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_buffer(partials, static_cast<uint32_t>(split) * ntiles * kTileWaves * kFrags * 1024u);
+    const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
+    auto frag_off = [&](int sp, int f) {
+      return (((static_cast<uint32_t>(sp) * ntiles + tile) * kTileWaves + wave) * kFrags + f) * 1024u + lane_off;
+    };
+#pragma unroll
+    for (int f = 0; f < kFrags; ++f) store_fragment(rp, frag_off(sidx, f), acc[f / 4][f % 4]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (threadIdx.x == 0) is_last = (arrive(&counters[tile]) == split - 1);
     __syncthreads();
     if (!is_last) return;
-    if (active) {
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
+    for (int c = 0; c < kFrags; c += 8) {
+      f32x4_t tot[8];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int f = 0; f < 8; ++f) tot[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < split; ++sp) {
+        if (sp == sidx) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = row0 + 16 * mt + 4 * (lane >> 4) + i;
-          const int n = col_w + 16 * tt + (lane & 15);
-          if (row < M) {
-            float v = 0.0f;
-            for (int s = 0; s < split; ++s)
-              v += (s == sidx) ? acc[mt][tt][i] : load_partial(partials + (static_cast<size_t>(s) * M + row) * N + n);
-            acc[mt][tt][i] = v;
-          }
+          for (int f = 0; f < 8; ++f) tot[f] += acc[(c + f) / 4][(c + f) % 4];
+        } else {
+          f32x4_t part[8];
+#pragma unroll
+          for (int f = 0; f < 8; ++f) part[f] = load_fragment(rp, frag_off(sp, c + f));
+#pragma unroll
+          for (int f = 0; f < 8; ++f) tot[f] += part[f];
         }
+      }
+#pragma unroll
+      for (int f = 0; f < 8; ++f) acc[(c + f) / 4][(c + f) % 4] = tot[f];
     }
     if (threadIdx.x == 0) rearm(&counters[tile]);
   }
@@ -235,23 +241,31 @@ __global__ __launch_bounds__(256, 1) void tile_kernel(const uint16_t* __restrict
   }
 }
 
-template <int WM>
+template <int WM, int OCC>
 static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                                 const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
                                 int N, int split, hipStream_t stream) {
   const int m_blocks = (M + 16 * WM - 1) / (16 * WM);
   const int n_blocks = (N + kTileBN - 1) / kTileBN;
   const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
-  tile_kernel<WM><<<grid, 64 * kTileWaves, 0, stream>>>(x, reinterpret_cast<const uint4*>(packed), qzeros, scales,
-                                                        y, partials, counters, M, K, N, split, m_blocks, n_blocks);
+  tile_kernel<WM, OCC><<<grid, 64 * kTileWaves, 0, stream>>>(x, reinterpret_cast<const uint4*>(packed), qzeros,
+                                                             scales, y, partials, counters, M, K, N, split, m_blocks,
+                                                             n_blocks);
   return hipGetLastError();
 }
 
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                            const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int split, hipStream_t stream) {
-  if (wm == 8) return launch_tile_t<8>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
-  return launch_tile_t<16>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+                           int N, int wm, int occ, int split, hipStream_t stream) {
+  if (wm == 4) {
+    if (occ == 2) return launch_tile_t<4, 2>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+    return launch_tile_t<4, 1>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+  }
+  if (wm == 8) {
+    if (occ == 2) return launch_tile_t<8, 2>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+    return launch_tile_t<8, 1>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
+  }
+  return launch_tile_t<16, 1>(x, packed, qzeros, scales, y, partials, counters, M, K, N, split, stream);
 }
 
 }  // namespace w4a16

@@ -87,6 +87,9 @@ def test_every_decode_configuration(gpu_lib, m):
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
 
+TILE_CONFIGS = [(wm, occ, split) for wm in (4, 8) for occ in (1, 2) for split in (1, 2, 3)] + [(16, 1, 1), (16, 1, 2)]
+
+
 @pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256)])
 def test_every_tile_configuration(gpu_lib, m, n):
     k = 1024
@@ -94,14 +97,15 @@ def test_every_tile_configuration(gpu_lib, m, n):
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
-    for wm in (8, 16):
-        for split in (1, 2, 3):
-            ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
-            ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
-            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-            gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, 0, split, ws)
-            err = rel_err(y, want)
-            assert err <= GEMM_REL_TOL, (wm, split, err)
+    for wm, occ, split in TILE_CONFIGS:
+        ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
+        ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, occ, split, ws)
+        err = rel_err(y, want)
+        assert err <= GEMM_REL_TOL, (wm, occ, split, err)
+        if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
+            assert int(torch.count_nonzero(ws[:65536])) == 0
 
 
 def test_shared_workspace_across_shapes_and_m(gpu_lib):
