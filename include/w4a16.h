@@ -109,7 +109,7 @@ int w4a16_regime(int M, int K, int N);
 int w4a16_split_k(int M, int K, int N);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
- * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,4}, p1 = waves per
+ * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,3,4} dividing N/16, p1 = waves per
  * workgroup in {4,8,16}, p2 = 128-row groups in flight per wave in {1,2,4}, M <= 64) or
  * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {4,8,16}, p1 = waves per SIMD the
  * register allocation targets in {1,2} (1 for p0 = 16); p2 ignored);

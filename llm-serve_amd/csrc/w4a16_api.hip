@@ -53,41 +53,56 @@ struct GemmPlan {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Decode regime, chosen from measured sweeps over the Qwen3-8B projection shapes.
-//  * Narrow layers (N <= 4096) at M <= 16 use one 16-column tile per workgroup so that
-//    every CU gets work; with long K (>= 8192) and M > 4, 32-column workgroups with K split
-//    in two instead (64-column ones split in four at M = 17..32), which keeps the
-//    activation traffic per weight down.
-//  * Wider layers use 32-column workgroups (tn = 2) at M <= 32 and 64-column workgroups
-//    (tn = 4, 4 waves) at M > 32, where each activation fragment feeds four tiles.
-//  * 8 waves with one group in flight each, or 4 waves with two.  K is split where the
-//    column tiles alone cannot cover the CUs.
+// Decode regime, chosen from measured sweeps over the Qwen3-8B projection shapes.  The
+// guiding rule is a balanced grid: a number of workgroups that is a small multiple of the
+// CU count, so that every CU streams the same share of the weights in one round.
+//  * Wide layers (N >= 16384, N / 16 divisible by 3): 48-column workgroups (tn = 3), e.g.
+//    512 workgroups (two per CU) for gate_up.
+//  * Medium layers (4096 < N < 16384): 32-column workgroups at M <= 16; beyond, 48-column
+//    ones with K split in two.
+//  * Narrow layers (N <= 4096) with K <= 4096: 16-column workgroups at M <= 16 (one per
+//    CU for N = 4096), 32-column ones with K split in two beyond.
+//  * Narrow layers with long K (>= 8192): 16-column workgroups at M <= 4; beyond, wider
+//    workgroups with K split in two or four, which keeps the activation traffic per
+//    weight down.
+// 8 waves with one group in flight each, or 4 waves with two.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
-  const bool narrow = N <= 4096, long_k = K >= 8192;
+  const int T = N / 16;
   int tn = 2, waves = 8, depth = 1, split = 1;
-  if (MB == 1 && narrow && long_k && M > 4) {
-    split = 2;
-  } else if (MB == 2 && narrow && long_k) {
-    tn = 4;
-    split = 4;
-  } else if (MB == 1 && narrow) {
-    tn = 1;
-    waves = M <= 4 ? 8 : 4;
-    depth = 2;
-  } else if (MB == 2) {
-    split = narrow ? 2 : 1;
-  } else if (MB >= 3) {
-    if (narrow && !long_k) {
+  auto four_two = [&]() { waves = 4; depth = 2; };
+  if (N >= 16384 && T % 3 == 0) {
+    tn = 3;
+    if (MB > 1) four_two();
+  } else if (N > 4096) {
+    if (MB > 1) {
+      tn = T % 3 == 0 ? 3 : 2;
+      split = 2;
+      if (MB > 2) four_two();
+    }
+  } else if (K < 8192) {
+    if (MB == 1) {
+      tn = 1;
+      if (M > 8) four_two();
+      else depth = 1;
+    } else {
+      split = 2;
+      if (MB == 2) four_two();
+    }
+  } else {
+    if (M <= 4) {
+      tn = 1;
+      depth = 2;
+    } else if (M <= 8) {
       split = 2;
     } else {
       tn = 4;
-      waves = 4;  // decode_lds_bytes(64, 4, 4) = 64 KiB
-      depth = 2;
-      split = N >= 16384 ? 1 : narrow ? 4 : 2;
+      split = 4;
+      if (MB > 2) four_two();
     }
   }
+  if ((T % tn) != 0) tn = (T % 2 == 0) ? 2 : 1;  // other shapes: a tile count that divides
   if (split > G) split = G;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
@@ -273,7 +288,8 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
   if (split < 1 || split > G) return fail(W4A16_ERR_ARG, "split must be in [1, K/128] (got %d)", split);
   if (regime == W4A16_REGIME_DECODE) {
     if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
-    if (p0 != 1 && p0 != 2 && p0 != 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2 or 4");
+    if (p0 < 1 || p0 > 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2, 3 or 4");
+    if ((N / 16) % p0) return fail(W4A16_ERR_SHAPE, "N / 16 = %d is not a multiple of %d column tiles", N / 16, p0);
     if (p1 != 4 && p1 != 8 && p1 != 16) return fail(W4A16_ERR_ARG, "decode waves must be 4, 8 or 16");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
     if (decode_lds_bytes(M, p0, p1) > kDecodeMaxLds)

@@ -269,6 +269,7 @@ static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int wa
   switch (tn) {
     case 1: return launch_decode_d<MB, 1>(a, depth, waves, stream);
     case 2: return launch_decode_d<MB, 2>(a, depth, waves, stream);
+    case 3: return launch_decode_d<MB, 3>(a, depth, waves, stream);
     default: return launch_decode_d<MB, 4>(a, depth, waves, stream);
   }
 }

@@ -15,7 +15,8 @@ hipError_t launch_repack(const uint32_t* qweight, uint32_t* packed, int K, int N
 hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros, const uint16_t* scales,
                                  uint16_t* w_out, int K, int N, hipStream_t stream);
 
-// Split-K decode kernel, M <= 64.  tn in {1, 2, 4} 16-column tiles per workgroup, depth in
+// Split-K decode kernel, M <= 64.  tn in {1, 2, 3, 4} 16-column tiles per workgroup (tn
+// divides N / 16), depth in
 // {1, 2, 4} groups in flight per wave, waves in {4, 8, 16}, 1 <= split <= K / 128.
 // `partials` holds the split-K fp32 fragments and `counters` N / (16 tn) ints (both unused
 // when split == 1).

@@ -114,7 +114,8 @@ def test_forced_config_validation(pkg):
     buf = (ctypes.c_uint8 * 64)()
     p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
     assert f(p, p, p, p, p, 128, 4096, 4096, 128, 1, 4, 4, 2, 1, None, 0, None) == 2  # decode needs M <= 64
-    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 3, 4, 2, 1, None, 0, None) == 1  # bad tiles
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 5, 4, 2, 1, None, 0, None) == 1  # bad tiles
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 3, 4, 2, 1, None, 0, None) == 2  # 3 does not divide N/16
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 5, 2, 1, None, 0, None) == 1  # bad waves
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 33, None, 0, None) == 1  # split > K/128
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 3, 1, None, 0, None) == 1  # bad depth

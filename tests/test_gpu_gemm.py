@@ -62,14 +62,15 @@ def test_single_token_wide_gemv_reference_recipe(gpu_lib):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.01, atol=0.02)
 
 
-DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 4) for w in (4, 8, 16) for d in (1, 2, 4) for s in (1, 3, 8)]
+DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4) for w in (4, 8, 16) for d in (1, 2, 4) for s in (1, 3, 8)]
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 33, 64])
 def test_every_decode_configuration(gpu_lib, m):
     """All column-tile / wave / depth / split combinations of the decode kernel, incl. uneven
-    splits, waves with no group and prefetch rings that wrap (K = 2048: 16 groups)."""
-    k, n = 2048, 512
+    splits, waves with no group and prefetch rings that wrap (K = 2048: 16 groups; N = 768:
+    48 column tiles, divisible by every tile count)."""
+    k, n = 2048, 768
     p = ora.make_problem(seed=100 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
