@@ -32,8 +32,8 @@ int check_launch(hipError_t e, const char* what) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr int kDecodeMaxM = 64;
-// The decode kernel addresses each input through a buffer descriptor with 32-bit byte
-// offsets and uses offsets >= 2^31 as "fetch nothing".
+// Both GEMM kernels address their inputs through buffer descriptors with 32-bit byte
+// offsets and use offsets >= 2^31 as "fetch nothing".
 constexpr size_t kMaxTensorBytes = size_t(1) << 31;
 constexpr size_t kDecodeMaxLds = 64 * 1024;  // LDS of the decode kernel's wave reduction
 
@@ -191,8 +191,22 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
     return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p2,
                                                  p.p1, p.split, stream),
                         "decode");
-  return check_launch(
-      w4a16::launch_tile_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p1, p.split, stream), "tile");
+  // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
+  // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
+  // one launch each, in order on the stream (each launch re-arms the counters it used).
+  const int bm = 16 * p.p0;
+  const size_t fit = (kMaxTensorBytes - 1) / (2 * static_cast<size_t>(K));
+  const int chunk = fit >= static_cast<size_t>(M) ? M : static_cast<int>(fit / bm) * bm;
+  if (chunk <= 0) return fail(W4A16_ERR_SHAPE, "K=%d is too long for one %d-row tile below 2 GiB", K, bm);
+  for (int r0 = 0; r0 < M; r0 += chunk) {
+    const int mc = M - r0 < chunk ? M - r0 : chunk;
+    const int rc = check_launch(w4a16::launch_tile_cfg(x + static_cast<size_t>(r0) * K, pk, qz, scales,
+                                                       y + static_cast<size_t>(r0) * N, partials, counters, mc, K,
+                                                       N, p.p0, p.p1, p.split, stream),
+                                "tile");
+    if (rc != W4A16_OK) return rc;
+  }
+  return ok();
 }
 
 }  // namespace

@@ -111,6 +111,10 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 constexpr int kCoherentPolicy = 16;        // buffer-op cache policy bits: sc1
 constexpr int kRawBufferWord3 = 0x00020000;  // raw (untyped) buffer, 32-bit data format
 
+// Offset used for "fetch nothing": >= every descriptor's size (tensors are < 2 GiB, checked
+// on the host).
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
 // Buffer descriptor over `bytes` bytes at p: loads past the end return zeros without a
 // memory access, stores past the end are dropped.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer(const void* p, uint32_t bytes) {

@@ -47,8 +47,6 @@ struct DecodeSources {
   __amdgpu_buffer_rsrc_t x, w, s, z;
 };
 
-constexpr uint32_t kOutOfRange = 0x80000000u;  // >= every num_records (checked on the host)
-
 // Byte offsets that do not depend on the group: per activation fragment row (or
 // kOutOfRange for rows >= M), and per block of the lane's weight words.
 template <int MB>

@@ -8,9 +8,10 @@
 // loads into MFMA B fragments -- bf16_rne((q - z) s), the reference's weights, see
 // dequant_step -- with no LDS round trip.  The activation tile (BM rows x one 128-deep
 // group) is shared by all four waves through LDS: it is brought in by direct-to-LDS 16-byte
-// loads
-// (global_load_lds_dwordx4), double-buffered one group ahead, in a row-major layout whose
-// 16-byte chunks are XOR-swizzled by (row & 7) so the A-fragment reads are conflict-free.
+// buffer loads in a three-stage ring (two groups in flight while one is computed), in a
+// row-major layout whose 16-byte chunks are XOR-swizzled by (row & 7) so the A-fragment
+// reads are conflict-free.  The weights, scales and zeros of those groups travel in a
+// matching ring of registers.
 //
 // Grid: one workgroup per (m-block, n-block, k-split), enumerated XCD-major so the ~32
 // workgroups resident on one XCD cover a few n-blocks x all m-blocks and share their
@@ -30,45 +31,53 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Issue the direct-to-LDS loads of activation rows [row0, row0 + BM) x group g into `stage`.
 // Instruction i of wave w fills rows 16 i + 4 w .. +3 (1 KiB); lane -> (row, physical chunk).
+// An invalid group (past the workgroup's K range) fetches nothing.
 template <int WM>
-__device__ __forceinline__ void issue_a_stage(const uint16_t* __restrict__ x, uint8_t* stage, int row0, int M,
-                                              int K, int g, int wave, int lane) {
+__device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t* stage, int row0, int M, int K,
+                                              int g, bool valid, int wave, int lane) {
   const int p = lane & 15;
-  const uint16_t* xg = x + kGroup * g;  // wave-uniform
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int r = 16 * i + 4 * wave + (lane >> 4);
     const int c = p ^ (r & 7);
     int row = row0 + r;
     row = row < M ? row : M - 1;  // rows past M load a valid row; their outputs are dropped
-    const uint16_t* src = xg + (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + 8u * c);
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(stage + (16 * i + 4 * wave) * kARowBytes), 16, 0, 0);
+    const uint32_t off =
+        valid ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + kGroup * g + 8u * c) * 2u : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(stage + (16 * i + 4 * wave) * kARowBytes), 16, off,
+                                             0, 0, 0);
   }
 }
 
 // Raw loads of one group for a wave's 64 columns (four 16-column layout tiles): one
 // 16-byte weight load per tile, and the scale-pair and zero words of the lane's column in
-// each tile.  Decoding waits until the group is consumed.
+// each tile.  Decoding waits until the group is consumed.  An invalid group (past the K
+// range, or a wave whose columns lie past N) fetches nothing.
 struct BGroup {
-  uint4 w[4];
+  u32x4_t w[4];
   uint32_t s[4];   // bf16 scale pair holding the lane's column
   uint32_t zw[4];  // AutoAWQ zero word holding the lane's column
 };
+constexpr int kBLoads = 12;  // buffer loads per BGroup
 
-// Wave-uniform base pointers plus lane offsets (scalar-base addressing).
-__device__ __forceinline__ void load_b_group(BGroup& b, const uint4* __restrict__ packed,
-                                             const uint32_t* __restrict__ qzeros,
-                                             const uint16_t* __restrict__ scales, int g, int N, int t0,
+struct BSources {
+  __amdgpu_buffer_rsrc_t w, s, z;
+};
+
+__device__ __forceinline__ void load_b_group(BGroup& b, const BSources& src, int g, bool valid, int N, int t0,
                                              int lane) {
   const int NT = N / kTileCols;
   const int c = lane & 15;
+  const uint32_t oob = valid ? 0u : kOutOfRange;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     const int t = t0 + tt;
-    b.w[tt] = packed[tile_word(g, t, NT, 0) / 4 + lane];
+    const uint32_t wo = valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : kOutOfRange;
+    b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
     const int col = kTileCols * t + c;
-    b.s[tt] = reinterpret_cast<const uint32_t*>(scales)[(static_cast<size_t>(g) * N + col) >> 1];
-    b.zw[tt] = qzeros[static_cast<size_t>(g) * (N >> 3) + (col >> 3)];
+    b.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
+    b.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u),
+                                                    0, 0);
   }
 }
 
@@ -87,8 +96,7 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
     bf16x8_t bf[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      const uint4& v = b.w[tt];
-      bf[tt] = dequant_step(j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w, ts[tt], nib);
+      bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
     }
     const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 7);
     const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
@@ -104,7 +112,7 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][4], const uint8_t* 
 // OCC = waves per SIMD the register allocation must allow (1 or 2).
 template <int WM, int OCC>
 __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restrict__ x,
-                                                      const uint4* __restrict__ packed,
+                                                      const uint32_t* __restrict__ packed,
                                                       const uint32_t* __restrict__ qzeros,
                                                       const uint16_t* __restrict__ scales,
                                                       uint16_t* __restrict__ y, float* __restrict__ partials,
@@ -112,8 +120,8 @@ __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restri
                                                       int m_blocks, int n_blocks) {
   constexpr int BM = 16 * WM;
   constexpr int kStage = BM * kARowBytes;
-  __shared__ __attribute__((aligned(1024))) uint8_t stage0[kStage];
-  __shared__ __attribute__((aligned(1024))) uint8_t stage1[kStage];
+  constexpr int S = WM >= 16 ? 2 : 3;  // pipeline stages (LDS: S * kStage bytes)
+  __shared__ __attribute__((aligned(1024))) uint8_t stages[S][kStage];
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63;
@@ -143,33 +151,48 @@ __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restri
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // S-stage ring over the workgroup's groups: item i (group g_begin + i) lives in LDS stage
+  // and register slot i % S.  Step i waits for item i's loads (items i + 1 .. i + S - 2 may
+  // still be in flight), passes one barrier -- after which every wave has finished item
+  // i - 1, whose slot is refilled with item i + S - 1 -- and computes item i.  The first
+  // trip only issues loads.  Every load is issued unconditionally (invalid items fetch
+  // nothing), so the per-step wait count is exact.
   const NibbleConsts nib = nibble_consts();
-  BGroup cur, nxt;
-  if (g_begin < g_end) {
-    issue_a_stage<WM>(x, stage0, row0, M, K, g_begin, wave, lane);
-    if (active) load_b_group(cur, packed, qzeros, scales, g_begin, N, t0, lane);
+  const __amdgpu_buffer_rsrc_t rx = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
+  const BSources bsrc{make_buffer(packed, static_cast<uint32_t>(K) * (N / 2)),
+                      make_buffer(scales, static_cast<uint32_t>(G) * N * 2u),
+                      make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u)};
+  constexpr int kStageLoads = WM + kBLoads;  // vector-memory instructions per item and wave
+  constexpr int kAhead = kStageLoads * (S - 2);
+  constexpr int kWaitAhead = (kAhead & 15) | (((kAhead >> 4) & 3) << 14) | (7 << 4) | (15 << 8);
+  const int n_items = g_end - g_begin;
+  BGroup ring[S];
+  for (int base = -S; base < n_items; base += S) {
+#pragma unroll
+    for (int d = 0; d < S; ++d) {
+      const int i = base + d;
+      const bool live = i >= 0 && i < n_items;
+      if (live) {
+        __builtin_amdgcn_s_waitcnt(kWaitAhead);  // item i's LDS and register loads have landed
+        __syncthreads();
+      }
+      const int ds = (d + S - 1) % S;  // a constant once the loop is unrolled
+      const int j = i + S - 1;
+      const bool valid = j >= 0 && j < n_items;
+      __builtin_amdgcn_sched_barrier(0);
+      // Past the last item nothing is issued: no barrier separates those steps from other
+      // waves still reading stage ds (item n_items - 1), and an out-of-range direct-to-LDS
+      // load may still write its zeros there.  No later step waits on these loads.
+      if (i < n_items) {
+        issue_a_stage<WM>(rx, stages[ds], row0, M, K, g_begin + j, valid, wave, lane);
+        load_b_group(ring[ds], bsrc, g_begin + j, valid && active, N, t0, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (live && active) mma_group<WM>(acc, stages[d], ring[d], nib, lane);
+    }
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0);  // trailing (empty) loads, before the stages are reused
   __syncthreads();
-
-  // Two groups per trip so each half reads one fixed stage while the other is refilled.
-  for (int g = g_begin; g < g_end; g += 2) {
-    if (g + 1 < g_end) {
-      issue_a_stage<WM>(x, stage1, row0, M, K, g + 1, wave, lane);
-      if (active) load_b_group(nxt, packed, qzeros, scales, g + 1, N, t0, lane);
-    }
-    if (active) mma_group<WM>(acc, stage0, cur, nib, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (g + 1 >= g_end) break;
-    if (g + 2 < g_end) {
-      issue_a_stage<WM>(x, stage0, row0, M, K, g + 2, wave, lane);
-      if (active) load_b_group(cur, packed, qzeros, scales, g + 2, N, t0, lane);
-    }
-    if (active) mma_group<WM>(acc, stage1, nxt, nib, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
 
   if (split > 1) {
     // Every workgroup stores its fp32 fragments (lane-major, 1 KiB per 16 x 16 MFMA tile)
@@ -216,8 +239,8 @@ __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restri
 
   if (!active) return;
   // Epilogue: bf16 through LDS (row-major BM x 64 per wave, 16-byte chunks swizzled by
-  // row & 7), then 16-byte coalesced stores.  Both stages are free after the last barrier.
-  uint8_t* ep = (wave < 2 ? stage0 : stage1) + (wave & 1) * (BM * 128);
+  // row & 7), then 16-byte coalesced stores.  The stages are free after the last barrier.
+  uint8_t* ep = &stages[0][0] + wave * (BM * 128);
 #pragma unroll
   for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
@@ -248,9 +271,8 @@ static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const
   const int m_blocks = (M + 16 * WM - 1) / (16 * WM);
   const int n_blocks = (N + kTileBN - 1) / kTileBN;
   const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
-  tile_kernel<WM, OCC><<<grid, 64 * kTileWaves, 0, stream>>>(x, reinterpret_cast<const uint4*>(packed), qzeros,
-                                                             scales, y, partials, counters, M, K, N, split, m_blocks,
-                                                             n_blocks);
+  tile_kernel<WM, OCC><<<grid, 64 * kTileWaves, 0, stream>>>(x, packed, qzeros, scales, y, partials, counters, M,
+                                                             K, N, split, m_blocks, n_blocks);
   return hipGetLastError();
 }
 
