@@ -35,12 +35,6 @@ constexpr int kDecodeMaxM = 64;
 // Both GEMM kernels address their inputs through buffer descriptors with 32-bit byte
 // offsets and use offsets >= 2^31 as "fetch nothing".
 constexpr size_t kMaxTensorBytes = size_t(1) << 31;
-constexpr size_t kDecodeMaxLds = 64 * 1024;  // LDS of the decode kernel's wave reduction
-
-// LDS the decode kernel's cross-wave reduction needs: one f32x4 per lane per (wave, m-block, tile).
-size_t decode_lds_bytes(int M, int tn, int waves) {
-  return static_cast<size_t>(waves) * ((M + 15) / 16) * tn * 64 * 16;
-}
 
 // Kernel configuration for one GEMM problem.
 struct GemmPlan {
@@ -53,57 +47,52 @@ struct GemmPlan {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Decode regime, chosen from measured sweeps over the Qwen3-8B projection shapes.  The
-// guiding rule is a balanced grid: a number of workgroups that is a small multiple of the
-// CU count, so that every CU streams the same share of the weights in one round.
-//  * Wide layers (N >= 16384, N / 16 divisible by 3): 48-column workgroups (tn = 3), e.g.
-//    512 workgroups (two per CU) for gate_up.
-//  * Medium layers (4096 < N < 16384): 32-column workgroups at M <= 16; beyond, 48-column
-//    ones with K split in two.
-//  * Narrow layers (N <= 4096) with K <= 4096: 16-column workgroups at M <= 16 (one per
-//    CU for N = 4096), 32-column ones with K split in two beyond.
-//  * Narrow layers with long K (>= 8192): 16-column workgroups at M <= 4; beyond, wider
-//    workgroups with K split in two or four, which keeps the activation traffic per
-//    weight down.
-// 8 waves with one group in flight each, or 4 waves with two.
+// Decode regime, chosen from a sweep of every configuration on MI355X over the Qwen3-8B
+// projection shapes (tn 16-column tiles per workgroup, waves, depth = groups in flight per
+// wave, split = K splits).  The activation traffic per weight byte falls as tn grows (each
+// workgroup reads its K range of x once), the grid shrinks with it, and the exchange of
+// split-K partials costs an extra pass over M x N fp32:
+//  * wide layers (N >= 16384): 32-column workgroups at M = 1 (768 for gate_up), 48 up to
+//    M = 8, 96 beyond (fewer, wider workgroups once x is 16 rows), 64 at M > 32;
+//  * medium layers (4096 < N < 16384): 32 columns up to M = 16, then 48 with K in two;
+//  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
+//    N = 4096, four groups in flight per wave beyond M = 4), then wider ones with K split;
+//  * narrow layers with long K: 16 columns up to M = 4, then wider ones with K split in two
+//    or four.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
   const int T = N / 16;
-  int tn = 2, waves = 8, depth = 1, split = 1;
-  auto four_two = [&]() { waves = 4; depth = 2; };
-  if (N >= 16384 && T % 3 == 0) {
-    tn = 3;
-    if (MB > 1) four_two();
+  int tn = 2, waves = 8, depth = 2, split = 1;
+  if (N >= 16384) {
+    if (M <= 1) tn = 2;
+    else if (M <= 8) tn = 3;
+    else if (M <= 16) tn = 6;
+    else if (M <= 32) { tn = 6; waves = 4; }
+    else { tn = 4; waves = 4; depth = 1; }
   } else if (N > 4096) {
-    if (MB > 1) {
-      tn = T % 3 == 0 ? 3 : 2;
-      split = 2;
-      if (MB > 2) four_two();
-    }
+    if (M <= 8) tn = 2;
+    else if (M <= 16) { tn = 2; waves = 4; }
+    else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
-    if (MB == 1) {
-      tn = 1;
-      if (M > 8) four_two();
-      else depth = 1;
-    } else {
-      split = 2;
-      if (MB == 2) four_two();
-    }
+    if (M <= 4) tn = 1;
+    else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
+    else if (M <= 32) { tn = 4; depth = 1; split = 4; }
+    else { tn = 2; depth = 1; split = 2; }
   } else {
-    if (M <= 4) {
-      tn = 1;
-      depth = 2;
-    } else if (M <= 8) {
-      split = 2;
-    } else {
-      tn = 4;
-      split = 4;
-      if (MB > 2) four_two();
-    }
+    if (M <= 1) { tn = 1; depth = 4; }
+    else if (M <= 4) tn = 1;
+    else if (M <= 8) { tn = 2; split = 2; }
+    else { tn = 4; depth = 1; split = 4; if (M > 32) waves = 4; }
   }
-  if ((T % tn) != 0) tn = (T % 2 == 0) ? 2 : 1;  // other shapes: a tile count that divides
   if (split > G) split = G;
+  const bool xl = w4a16::decode_stages_x(M, K, split);
+  // Other shapes: the widest tile count <= tn that divides N / 16 and fits the registers.
+  while (depth > 1 && !w4a16::decode_config_fits(MB, tn, depth, xl)) depth /= 2;
+  while (tn > 1 && (T % tn != 0 || tn == 5 || !w4a16::decode_config_fits(MB, tn, depth, xl))) --tn;
+  // Very long K: split it until the staged operands of a workgroup fit in LDS.
+  while (w4a16::decode_lds_bytes(M, K, tn, waves, split) > w4a16::kDecodeMaxLds && split < G)
+    split = split * 2 > G ? G : split * 2;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
@@ -302,13 +291,16 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
   if (split < 1 || split > G) return fail(W4A16_ERR_ARG, "split must be in [1, K/128] (got %d)", split);
   if (regime == W4A16_REGIME_DECODE) {
     if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
-    if (p0 < 1 || p0 > 4) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2, 3 or 4");
+    if (p0 < 1 || p0 > 6 || p0 == 5) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2, 3, 4 or 6");
     if ((N / 16) % p0) return fail(W4A16_ERR_SHAPE, "N / 16 = %d is not a multiple of %d column tiles", N / 16, p0);
-    if (p1 != 4 && p1 != 8 && p1 != 16) return fail(W4A16_ERR_ARG, "decode waves must be 4, 8 or 16");
+    if (p1 != 4 && p1 != 8) return fail(W4A16_ERR_ARG, "decode waves must be 4 or 8");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
-    if (decode_lds_bytes(M, p0, p1) > kDecodeMaxLds)
+    if (w4a16::decode_lds_bytes(M, K, p0, p1, split) > w4a16::kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
-                  decode_lds_bytes(M, p0, p1), kDecodeMaxLds);
+                  w4a16::decode_lds_bytes(M, K, p0, p1, split), w4a16::kDecodeMaxLds);
+    if (!w4a16::decode_config_fits((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)))
+      return fail(W4A16_ERR_ARG, "decode configuration needs %d ring and accumulator registers per lane (limit 176)",
+                  w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
     if (p0 != 4 && p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 4, 8 or 16");
     if (p1 != 1 && p1 != 2) return fail(W4A16_ERR_ARG, "tile occupancy must be 1 or 2");

@@ -11,10 +11,23 @@
 // through LDS in a fixed order, and with split > 1 the workgroups exchange fp32 partials
 // (store_fragment / arrive / load_fragment): the last one to finish a column block sums
 // them in split order, writes bf16 and re-arms the counter.  Results are deterministic.
+//
+// Memory traffic.  The weight stream is the only per-group global load of a wave: each
+// wave copies the scales and zero words of its own groups and tiles (2.5 bytes per column
+// and group) into a private slice of LDS once, at the start, by direct-to-LDS buffer loads
+// with every lane busy, and so the activation rows of its groups when they are small (XL:
+// M <= 4 rows and at most kDecodeMaxStagedX bytes per workgroup).  Small per-lane loads of
+// scales, zeros and partly used activation rows issued per group cost memory-pipeline time
+// out of proportion to their bytes; staging removes them from the streaming loop, whose
+// vector-memory instructions are then the TN weight loads per group (plus the activation
+// fragments when they are not staged).  The slices are private, so no barrier delays the
+// start of the stream: a wave waits only for its own loads.
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
 
 namespace w4a16 {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 struct DecodeArgs {
   const uint16_t* x;
@@ -27,18 +40,43 @@ struct DecodeArgs {
   int M, K, N, split;
 };
 
-// Everything one wave needs for one 128-row group: one 16-byte weight load per tile, the
-// raw scale-pair and zero words of its TN output columns, and the MB x 4 activation
-// fragments.  Loaded DEPTH groups ahead of use; decoded only when consumed.
-template <int MB, int TN>
-struct DecodeStage {
-  u32x4_t w[TN];
-  uint32_t s[TN];
-  uint32_t zw[TN];
-  u32x4_t a[MB][4];
+// LDS layout of the staged operands.  A wave owns at most `items` groups (its groups
+// gi = wave + i W of the workgroup's K range); its slice holds, per item i, scale pairs
+// [items][TN * 8] words, zero words [items][TN * 2], then (XL) activations [items][M][128]
+// bf16 with 16-byte chunks swizzled by row.  Region sizes are rounded so that the last
+// direct-to-LDS load of a region (64 lanes x 4 or 16 bytes) stays in it.  The cross-wave
+// reduction reuses the same memory after the streaming loop.
+struct DecodeLds {
+  uint32_t s_off, z_off, x_off, wave_bytes, staged, reduce, total;
 };
 
-// Buffer descriptors of the four inputs.  Every load of the decode kernel is an
+__host__ __device__ constexpr uint32_t round_up(uint32_t v, uint32_t a) { return (v + a - 1) / a * a; }
+
+__host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int waves, int split, bool xl) {
+  const int G = K / kGroup;
+  const uint32_t n_gmax = static_cast<uint32_t>((G + split - 1) / split);
+  const uint32_t items = (n_gmax + waves - 1) / waves;
+  DecodeLds l{};
+  l.s_off = 0;
+  l.z_off = round_up(items * tn * 8u * 4u, 256u);
+  l.x_off = l.z_off + round_up(items * tn * 2u * 4u, 256u);
+  l.wave_bytes = round_up(l.x_off + (xl ? round_up(items * static_cast<uint32_t>(M) * 256u, 1024u) : 0u), 1024u);
+  l.staged = l.wave_bytes * static_cast<uint32_t>(waves);
+  l.reduce = static_cast<uint32_t>(waves) * ((M + 15) / 16) * tn * 1024u;
+  l.total = l.staged > l.reduce ? l.staged : l.reduce;
+  return l;
+}
+
+// Everything one wave loads from global memory for one 128-row group: one 16-byte weight
+// load per tile and, when the activations are not staged, the MB x 4 activation fragments.
+// Loaded DEPTH groups ahead of use; decoded only when consumed.
+template <int MB, int TN, bool XL>
+struct DecodeStage {
+  u32x4_t w[TN];
+  u32x4_t a[XL ? 1 : MB][4];
+};
+
+// Buffer descriptors of the four inputs.  Every global load of the decode kernel is an
 // unconditional buffer load: a lane or a group with nothing to fetch (activation row >= M,
 // group past the workgroup's K range) uses kOutOfRange, which the hardware answers with
 // zeros and no memory access.  With no branch around any load the compiler's wait counts
@@ -47,45 +85,55 @@ struct DecodeSources {
   __amdgpu_buffer_rsrc_t x, w, s, z;
 };
 
-// Byte offsets that do not depend on the group: per activation fragment row (or
-// kOutOfRange for rows >= M), and per block of the lane's weight words.
-template <int MB>
-struct DecodeOffsets {
-  uint32_t x_row[MB];  // (row K + 8 (lane / 16)) * 2, or kOutOfRange
-};
-
-template <int MB, int TN>
-__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN>& st, const DecodeSources& src,
-                                                  const DecodeOffsets<MB>& off, int g, bool valid, int N, int cb,
+template <int MB, int TN, bool XL>
+__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, const DecodeSources& src,
+                                                  const uint32_t (&x_row)[MB], int g, bool valid, int N, int cb,
                                                   int lane) {
   const int NT = N / kTileCols;
-  const int c = lane & 15;
   const uint32_t oob = valid ? 0u : kOutOfRange;
 #pragma unroll
   for (int tt = 0; tt < TN; ++tt) {
     const int t = cb * TN + tt;
     const uint32_t wo = (valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : 0u) | oob;
     st.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
-    const int col = kTileCols * t + c;
-    st.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
-    st.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u),
-                                                     0, 0);
   }
+  if constexpr (!XL) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const uint32_t xo = (off.x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 2u;
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t xo = (x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 2u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st.a[mb][j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 64u * j, 0, 0);
+      for (int j = 0; j < 4; ++j) st.a[mb][j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 64u * j, 0, 0);
+    }
   }
 }
 
-template <int MB, int TN>
-__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN>& st,
+// Multiply-accumulate one group: scales and zeros (and, with XL, the activation fragments)
+// come from the wave's LDS slice `wl`; i is the group's item index within the wave.
+template <int MB, int TN, bool XL>
+__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL>& st,
+                                                     const uint8_t* wl, const DecodeLds& lay, int i, int M,
                                                      const NibbleConsts& nib, int lane) {
+  const int c = lane & 15;
+  const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off) + i * (TN * 8) + (c >> 1);
+  const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off) + i * (TN * 2) + (c >> 3);
   const int zshift = awq_shift(lane & 7);
   TileScale ts[TN];
 #pragma unroll
-  for (int tt = 0; tt < TN; ++tt) ts[tt] = make_tile_scale(st.s[tt], (st.zw[tt] >> zshift) & 0xFu, lane);
+  for (int tt = 0; tt < TN; ++tt) ts[tt] = make_tile_scale(ls[tt * 8], (lz[tt * 2] >> zshift) & 0xFu, lane);
+  u32x4_t a[MB][4];
+  if constexpr (XL) {
+    // Rows >= M read row M - 1: their outputs are never stored.
+    const int r = (c < M ? c : M - 1);
+    const uint8_t* lx = wl + lay.x_off + (i * M + r) * 256;
+#pragma unroll
+    for (int js = 0; js < 4; ++js)
+      a[0][js] = *reinterpret_cast<const u32x4_t*>(lx + ((((js << 2) | (lane >> 4)) ^ ((r & 3) << 2)) << 4));
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int js = 0; js < 4; ++js) a[mb][js] = st.a[mb][js];
+  }
 #pragma unroll
   for (int js = 0; js < 4; ++js) {
 #pragma unroll
@@ -93,12 +141,57 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
       const bf16x8_t frag = dequant_step(st.w[tt][js], ts[tt], nib);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
-        acc[mb][tt] = mfma16(__builtin_bit_cast(bf16x8_t, st.a[mb][js]), frag, acc[mb][tt]);
+        acc[mb][tt] = mfma16(__builtin_bit_cast(bf16x8_t, a[mb][js]), frag, acc[mb][tt]);
     }
   }
 }
 
-template <int MB, int TN, int DEPTH, int WAVES>
+// Copy the scale pairs, zero words and (XL) activation rows of the wave's items (groups
+// g_first + i W, i < n_items) into its LDS slice `wl` with direct-to-LDS buffer loads (64
+// consecutive LDS words or 16-byte chunks per instruction, every lane busy; lanes past the
+// end fetch nothing).
+template <int TN, bool XL, int W>
+__device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay, const DecodeSources& src, int M,
+                                               int K, int N, int cb, int g_first, int n_items, int lane) {
+  constexpr int kSW = TN * 8;  // scale-pair words per group
+  constexpr int kZW = TN * 2;  // zero words per group
+  const int s_words = n_items * kSW;
+  for (int b = 0; b < s_words; b += 64) {
+    const int w = b + lane;
+    const int i = w / kSW;
+    const int j = w - i * kSW;
+    const uint32_t off =
+        w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + cb * kSW + j) * 4u : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)(wl + lay.s_off + b * 4), 4, off, 0, 0, 0);
+  }
+  const int z_words = n_items * kZW;
+  for (int b = 0; b < z_words; b += 64) {
+    const int w = b + lane;
+    const int i = w / kZW;
+    const int j = w - i * kZW;
+    const uint32_t off =
+        w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + cb * kZW + j) * 4u : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(wl + lay.z_off + b * 4), 4, off, 0, 0, 0);
+  }
+  if constexpr (XL) {
+    // LDS chunk C = (i M + r) 16 + cc holds global chunk cc ^ ((r & 3) << 2) of row r of
+    // item i's group (the XOR spreads the rows of one fragment read over the banks).
+    const int chunks = n_items * M * 16;
+    for (int b = 0; b < chunks; b += 64) {
+      const int C = b + lane;
+      const int im = C >> 4;
+      const int i = im / M;
+      const int r = im - i * M;
+      const int cc = (C & 15) ^ ((r & 3) << 2);
+      const uint32_t off =
+          C < chunks ? (static_cast<uint32_t>(r) * K + static_cast<uint32_t>(g_first + i * W) * kGroup) * 2u + cc * 16u
+                     : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_void_t*)(wl + lay.x_off + b * 16), 16, off, 0, 0, 0);
+    }
+  }
+}
+
+template <int MB, int TN, int DEPTH, int WAVES, bool XL>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -106,7 +199,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             uint16_t* __restrict__ y, float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
                                                             int split) {
-  extern __shared__ f32x4_t red[];  // [W][MB][TN][64]
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -116,18 +209,20 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const int sidx = blockIdx.y;
   const int g_begin = (G * sidx) / split;
   const int g_end = (G * (sidx + 1)) / split;
+  const int nG = g_end - g_begin;
   const int col0 = cb * (16 * TN) + (lane & 15);  // this lane's column in tile 0
+  const DecodeLds lay = decode_lds_layout(M, K, TN, W, split, XL);
 
   DecodeSources src;
   src.x = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
   src.w = make_buffer(packed, static_cast<uint32_t>(K) * (N / 2));
   src.s = make_buffer(scales, static_cast<uint32_t>(G) * N * 2u);
   src.z = make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u);
-  DecodeOffsets<MB> off;
+  uint32_t x_row[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int row = 16 * mb + (lane & 15);
-    off.x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * 2u : kOutOfRange;
+    x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * 2u : kOutOfRange;
   }
 
   f32x4_t acc[MB][TN];
@@ -136,28 +231,42 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
     for (int tt = 0; tt < TN; ++tt) acc[mb][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Depth-DEPTH ring over the wave's groups g0 + i W (g0 = g_begin + wave): group i is
-  // loaded while group i - DEPTH is being consumed.  The first trip only loads (its
-  // compute guards are all false), so the loop is the only place loads are issued and
-  // each stage's wait is "all but the DEPTH - 1 younger stages".  Loads are issued
-  // whether or not the group exists (out-of-range ones fetch nothing): no branch encloses
-  // a load, and the scheduling barriers keep each stage's loads together and in order.
-  DecodeStage<MB, TN> ring[DEPTH];
-  const int g0 = g_begin + wave;
+  // The wave's groups: gi = wave + i W of the K range, i < n_items.
+  const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
+  uint8_t* wl = lds + wave * lay.wave_bytes;
+  stage_operands<TN, XL, W>(wl, lay, src, M, K, N, cb, g_begin + wave, n_items, lane);
+  __builtin_amdgcn_sched_barrier(0);  // the staging loads stay ahead of the ring's
+
+  // Depth-DEPTH ring over the wave's items: item i is loaded while item i - DEPTH is being
+  // consumed.  The ring is filled first; then every load is issued whether or not its item
+  // exists (out-of-range ones fetch nothing), so no branch encloses a load and the
+  // scheduling barriers keep each item's loads together and in order.
+  DecodeStage<MB, TN, XL> ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d)
+    load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, cb, lane);
+  // Direct-to-LDS loads may complete out of order with the register loads issued after
+  // them (they do when those hit in cache), so a partial vmcnt wait does not cover them:
+  // wait for everything, the ring included, before the first group reads the slice.
+  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);  // vmcnt(0), expcnt and lgkmcnt untouched
+
   const NibbleConsts nib = nibble_consts();
-  for (int base = g0 - DEPTH * W; base < g_end; base += DEPTH * W) {
+  for (int base = 0; base < n_items; base += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int g = base + d * W;
-      if (g >= g0 && g < g_end) compute_decode_stage<MB, TN>(acc, ring[d], nib, lane);
-      const int gn = g + DEPTH * W;
+      const int i = base + d;
+      if (i < n_items) compute_decode_stage<MB, TN, XL>(acc, ring[d], wl, lay, i, M, nib, lane);
+      const int in = i + DEPTH;
       __builtin_amdgcn_sched_barrier(0);
-      load_decode_stage<MB, TN>(ring[d], src, off, gn, gn < g_end, N, cb, lane);
+      load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, cb, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // Reduce the W waves' partial sums in wave order.
+  // Reduce the W waves' partial sums in wave order (through the staging memory, once every
+  // wave has finished reading it).
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);  // [W][MB][TN][64]
+  __syncthreads();
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -229,27 +338,42 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   if (threadIdx.x == 0) rearm(&counters[cb]);
 }
 
-template <int MB, int TN, int DEPTH, int WAVES>
+bool decode_stages_x(int M, int K, int split) {
+  const int G = K / kGroup;
+  const size_t n_gmax = static_cast<size_t>((G + split - 1) / split);
+  return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
+}
+
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int split) {
+  return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split)).total;
+}
+
+template <int MB, int TN, int DEPTH, int WAVES, bool XL>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
-  // Configurations whose cross-wave reduction exceeds 64 KiB of LDS are rejected by the
-  // API before launch; they are not instantiated.
-  if constexpr (WAVES * MB * TN > 64) {
-    return hipErrorInvalidValue;
+  if constexpr (!decode_config_fits(MB, TN, DEPTH, XL)) {
+    return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
-  const size_t lds = static_cast<size_t>(WAVES) * MB * TN * 64 * sizeof(f32x4_t);
-  decode_kernel<MB, TN, DEPTH, WAVES><<<grid, 64 * WAVES, lds, stream>>>(
+  const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL).total;
+  decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split);
   return hipGetLastError();
   }
 }
 
+template <int MB, int TN, int DEPTH, int WAVES>
+static hipError_t launch_decode_x(const DecodeArgs& a, hipStream_t stream) {
+  if constexpr (MB == 1) {
+    if (decode_stages_x(a.M, a.K, a.split)) return launch_decode_t<MB, TN, DEPTH, WAVES, true>(a, stream);
+  }
+  return launch_decode_t<MB, TN, DEPTH, WAVES, false>(a, stream);
+}
+
 template <int MB, int TN, int DEPTH>
 static hipError_t launch_decode_w(const DecodeArgs& a, int waves, hipStream_t stream) {
   switch (waves) {
-    case 4: return launch_decode_t<MB, TN, DEPTH, 4>(a, stream);
-    case 8: return launch_decode_t<MB, TN, DEPTH, 8>(a, stream);
-    default: return launch_decode_t<MB, TN, DEPTH, 16>(a, stream);
+    case 4: return launch_decode_x<MB, TN, DEPTH, 4>(a, stream);
+    default: return launch_decode_x<MB, TN, DEPTH, 8>(a, stream);
   }
 }
 
@@ -268,7 +392,8 @@ static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int wa
     case 1: return launch_decode_d<MB, 1>(a, depth, waves, stream);
     case 2: return launch_decode_d<MB, 2>(a, depth, waves, stream);
     case 3: return launch_decode_d<MB, 3>(a, depth, waves, stream);
-    default: return launch_decode_d<MB, 4>(a, depth, waves, stream);
+    case 4: return launch_decode_d<MB, 4>(a, depth, waves, stream);
+    default: return launch_decode_d<MB, 6>(a, depth, waves, stream);
   }
 }
 

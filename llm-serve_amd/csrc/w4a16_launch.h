@@ -15,11 +15,30 @@ hipError_t launch_repack(const uint32_t* qweight, uint32_t* packed, int K, int N
 hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros, const uint16_t* scales,
                                  uint16_t* w_out, int K, int N, hipStream_t stream);
 
-// Split-K decode kernel, M <= 64.  tn in {1, 2, 3, 4} 16-column tiles per workgroup (tn
-// divides N / 16), depth in
-// {1, 2, 4} groups in flight per wave, waves in {4, 8, 16}, 1 <= split <= K / 128.
+// Split-K decode kernel, M <= 64.  tn in {1, 2, 3, 4, 6} 16-column tiles per workgroup (tn
+// divides N / 16), depth in {1, 2, 4} groups in flight per wave, waves in {4, 8},
+// 1 <= split <= K / 128, decode_config_fits() and decode_lds_bytes() <= kDecodeMaxLds.
 // `partials` holds the split-K fp32 fragments and `counters` N / (16 tn) ints (both unused
 // when split == 1).
+constexpr size_t kDecodeMaxLds = 64 * 1024;      // LDS of one decode workgroup
+constexpr size_t kDecodeMaxStagedX = 32 * 1024;  // activations staged in LDS (M <= 4 only)
+
+// Whether the activations of an (M, K, split) problem are staged in LDS.
+bool decode_stages_x(int M, int K, int split);
+// LDS bytes of a decode workgroup: staged scales, zeros (and activations), or the
+// cross-wave reduction, whichever is larger.
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int split);
+
+// Register budget of a decode configuration (16-row activation blocks mb, tiles tn, ring
+// depth, activations staged or not): fp32 accumulators plus the ring of in-flight loads,
+// in 32-bit registers per lane, at most 176.  Configurations beyond it are not compiled.
+constexpr int decode_ring_regs(int mb, int tn, int depth, bool xl) {
+  return 4 * mb * tn + depth * 4 * (tn + (xl ? 0 : 4 * mb));
+}
+constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
+  return decode_ring_regs(mb, tn, depth, xl) <= 176;
+}
+
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
                              int N, int tn, int depth, int waves, int split, hipStream_t stream);

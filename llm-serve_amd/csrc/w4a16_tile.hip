@@ -152,19 +152,18 @@ __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restri
     for (int tt = 0; tt < 4; ++tt) acc[mt][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // S-stage ring over the workgroup's groups: item i (group g_begin + i) lives in LDS stage
-  // and register slot i % S.  Step i waits for item i's loads (items i + 1 .. i + S - 2 may
-  // still be in flight), passes one barrier -- after which every wave has finished item
-  // i - 1, whose slot is refilled with item i + S - 1 -- and computes item i.  The first
-  // trip only issues loads.  Every load is issued unconditionally (invalid items fetch
-  // nothing), so the per-step wait count is exact.
+  // and register slot i % S.  Step i waits for every outstanding load (items i .. i + S - 2:
+  // direct-to-LDS loads may complete out of order with the register loads issued after
+  // them, so a partial count would not cover item i's stage), passes one barrier -- after
+  // which every wave has finished item i - 1, whose slot is refilled with item i + S - 1 --
+  // and computes item i while items i + 1 .. i + S - 1 are in flight.  The first trip only
+  // issues loads.
   const NibbleConsts nib = nibble_consts();
   const __amdgpu_buffer_rsrc_t rx = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
   const BSources bsrc{make_buffer(packed, static_cast<uint32_t>(K) * (N / 2)),
                       make_buffer(scales, static_cast<uint32_t>(G) * N * 2u),
                       make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u)};
-  constexpr int kStageLoads = WM + kBLoads;  // vector-memory instructions per item and wave
-  constexpr int kAhead = kStageLoads * (S - 2);
-  constexpr int kWaitAhead = (kAhead & 15) | (((kAhead >> 4) & 3) << 14) | (7 << 4) | (15 << 8);
+  constexpr int kWaitAll = 0x0F70;  // vmcnt(0); expcnt and lgkmcnt not waited for
   const int n_items = g_end - g_begin;
   BGroup ring[S];
   for (int base = -S; base < n_items; base += S) {
@@ -173,7 +172,7 @@ __global__ __launch_bounds__(256, OCC) void tile_kernel(const uint16_t* __restri
       const int i = base + d;
       const bool live = i >= 0 && i < n_items;
       if (live) {
-        __builtin_amdgcn_s_waitcnt(kWaitAhead);  // item i's LDS and register loads have landed
+        __builtin_amdgcn_s_waitcnt(kWaitAll);  // item i's LDS and register loads have landed
         __syncthreads();
       }
       const int ds = (d + S - 1) % S;  // a constant once the loop is unrolled

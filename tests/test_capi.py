@@ -120,8 +120,12 @@ def test_forced_config_validation(pkg):
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 33, None, 0, None) == 1  # split > K/128
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 3, 1, None, 0, None) == 1  # bad depth
     assert "depth" in L.last_error()
-    assert f(p, p, p, p, p, 64, 4096, 4096, 128, 1, 4, 16, 2, 1, None, 0, None) == 1  # 256 KiB of LDS
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 16, 2, 1, None, 0, None) == 1  # 16 waves
+    assert "waves" in L.last_error()
+    assert f(p, p, p, p, p, 64, 4096, 6144, 128, 1, 6, 8, 1, 1, None, 0, None) == 1  # 192 KiB of LDS
     assert "LDS" in L.last_error()
+    assert f(p, p, p, p, p, 64, 4096, 6144, 128, 1, 3, 4, 4, 1, None, 0, None) == 1  # ring registers
+    assert "registers" in L.last_error()
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 1, 2, 1, None, 0, None) == 1  # bad wm
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 3, 2, 1, None, 0, None) == 1  # bad occupancy
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 16, 2, 2, 1, None, 0, None) == 1  # wm 16 needs occupancy 1

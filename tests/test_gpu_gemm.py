@@ -62,22 +62,35 @@ def test_single_token_wide_gemv_reference_recipe(gpu_lib):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.01, atol=0.02)
 
 
-DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4) for w in (4, 8, 16) for d in (1, 2, 4) for s in (1, 3, 8)]
+DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4, 6) for w in (4, 8) for d in (1, 2, 4) for s in (1, 3, 8)]
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 33, 64])
+def decode_config_accepted(m, k, tn, depth, waves, split):
+    """The library's admission rules (LDS and ring registers), restated: staged activations
+    for M <= 4 within 32 KiB, LDS <= 64 KiB, accumulator + ring registers <= 176."""
+    mb = (m + 15) // 16
+    n_gmax = -(-(k // 128) // split)
+    xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
+    up = lambda v, a: -(-v // a) * a
+    staged = up(n_gmax * tn * 32, 256) + up(n_gmax * tn * 8, 256) + (up(n_gmax * m * 256, 1024) if xl else 0)
+    lds = max(staged, waves * mb * tn * 1024)
+    regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
+    return lds <= 64 * 1024 and regs <= 176
+
+
+@pytest.mark.parametrize("m", [1, 3, 5, 16, 33, 64])
 def test_every_decode_configuration(gpu_lib, m):
     """All column-tile / wave / depth / split combinations of the decode kernel, incl. uneven
     splits, waves with no group and prefetch rings that wrap (K = 2048: 16 groups; N = 768:
-    48 column tiles, divisible by every tile count)."""
+    48 column tiles, divisible by every tile count); M <= 4 runs with staged activations."""
     k, n = 2048, 768
     p = ora.make_problem(seed=100 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
     for tn, waves, depth, split in DECODE_CONFIGS:
-        if waves * ((m + 15) // 16) * tn * 1024 > 64 * 1024:
-            continue  # rejected by the library (LDS limit), see test_capi
+        if not decode_config_accepted(m, k, tn, depth, waves, split):
+            continue  # rejected by the library, see test_capi
         ws_bytes = gpu_lib.workspace_bytes_config(m, n, 1, tn, split)
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
@@ -86,6 +99,17 @@ def test_every_decode_configuration(gpu_lib, m):
         assert err <= GEMM_REL_TOL, (tn, waves, depth, split, err)
         if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
             assert int(torch.count_nonzero(ws[:65536])) == 0
+
+
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_decode_long_k_stays_within_lds(gpu_lib, m):
+    """K = 65536 (512 groups): the per-wave staged scales and zeros of one workgroup would
+    exceed LDS without a K split; the planner splits K until they fit."""
+    k, n = 65536, 64
+    p = ora.make_problem(seed=300 + m, m=m, k=k, n=n)
+    t = to_gpu(p)
+    y = hip_linear(t)
+    assert rel_err(y, ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)) <= GEMM_REL_TOL
 
 
 TILE_CONFIGS = [(wm, occ, split) for wm in (4, 8) for occ in (1, 2) for split in (1, 2, 3)] + [(16, 1, 1), (16, 1, 2)]
