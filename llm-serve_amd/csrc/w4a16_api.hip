@@ -41,11 +41,18 @@ struct GemmPlan {
   int regime;  // w4a16_regime_id
   int p0;      // decode: column tiles per workgroup; tile: wm (16-row tiles per wave)
   int p1;      // decode: waves per workgroup; tile: waves per SIMD the registers allow
-  int p2;      // decode: groups in flight per wave; tile: unused
+  int p2;      // decode: groups in flight per wave; tile: tile shape code (w4a16::tile_shape)
   int split;   // K splits (1 = none)
 };
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Tile regime: rows and columns of the workgroup tile.
+int tile_bm(const GemmPlan& p) { return 16 * p.p0 * w4a16::tile_shape(p.p2).nwm; }
+int tile_bn(const GemmPlan& p) {
+  const w4a16::TileShape t = w4a16::tile_shape(p.p2);
+  return 16 * t.tw * t.nwn;
+}
 
 // Decode regime, chosen from a sweep of every configuration on MI355X over the Qwen3-8B
 // projection shapes (tn 16-column tiles per workgroup, waves, depth = groups in flight per
@@ -96,17 +103,25 @@ GemmPlan plan_decode(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
-// Tile regime: 64-row tiles (wm = 4) with registers for two waves per SIMD everywhere
-// (measured best from M = 128 to 2048 on all four shapes).  K is split by the largest power
-// of two (at most 8, keeping >= 4 groups per split) that brings the grid up to about one
-// workgroup per CU; the fp32 partials are reduced by the last workgroup of each tile.
+// Tile regime, chosen from sweeps on MI355X over the Qwen3-8B shapes at M = 128, 512 and
+// 2048.  Workgroups of 8 waves side by side along N (32 columns each, 256 per workgroup).
+// Tall problems (M >= 1024) use 128-row tiles (wm = 8: every dequantized weight serves 128
+// rows, one workgroup per CU), except where that grid fills the CUs in uneven rounds and
+// 64-row tiles do not (N = 6144: 384 vs 768 tiles at M = 2048).  Otherwise 64-row tiles
+// (two workgroups per CU) with K split in powers of two while the grid stays within about
+// 1.5 workgroups per CU (2 for long K) and every split keeps >= 8 groups; the fp32
+// partials are reduced by the last workgroup of each tile.
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  const int wm = 4;
-  const int tiles = ceil_div(M, 16 * wm) * ceil_div(N, 256);
+  constexpr int kShape = 3;  // w4a16::tile_shape: 8 waves along N, 32 columns each
+  auto tiles = [&](int wm) { return ceil_div(M, 16 * wm) * ceil_div(N, 256); };
+  if (M >= 1024 && tiles(8) >= 256 && (tiles(8) % 256 == 0 || tiles(8) >= 1024))
+    return GemmPlan{W4A16_REGIME_TILE, 8, 2, kShape, 1};
+  const int t = tiles(4);
+  const int cap = G >= 64 ? 512 : 384;
   int split = 1;
-  while (split < 8 && tiles * split * 2 <= 256 && split * 2 * 4 <= G) split *= 2;
-  return GemmPlan{W4A16_REGIME_TILE, wm, 2, 0, split};
+  while (split < 8 && t * split * 2 <= cap && 8 * split * 2 <= G) split *= 2;
+  return GemmPlan{W4A16_REGIME_TILE, 4, 2, kShape, split};
 }
 
 GemmPlan plan(int M, int K, int N) {
@@ -122,7 +137,7 @@ constexpr size_t kMaxCounters = kCounterBytes / sizeof(int);
 
 size_t counters_needed(const GemmPlan& p, int M, int N) {
   if (p.regime == W4A16_REGIME_DECODE) return static_cast<size_t>(N / 16);
-  return static_cast<size_t>(ceil_div(M, 16 * p.p0)) * ceil_div(N, 256);
+  return static_cast<size_t>(ceil_div(M, tile_bm(p))) * ceil_div(N, tile_bn(p));
 }
 
 // fp32 partial tiles: split x (M padded to the kernel's row block) x (N padded to its
@@ -130,8 +145,8 @@ size_t counters_needed(const GemmPlan& p, int M, int N) {
 size_t partial_bytes(const GemmPlan& p, int M, int N) {
   if (p.regime == W4A16_REGIME_DECODE)
     return static_cast<size_t>(p.split) * (16 * ceil_div(M, 16)) * N * sizeof(float);
-  const int bm = 16 * p.p0;
-  return static_cast<size_t>(p.split) * (bm * ceil_div(M, bm)) * (256 * ceil_div(N, 256)) * sizeof(float);
+  const int bm = tile_bm(p), bn = tile_bn(p);
+  return static_cast<size_t>(p.split) * (bm * ceil_div(M, bm)) * (bn * ceil_div(N, bn)) * sizeof(float);
 }
 
 size_t workspace_for(const GemmPlan& p, int M, int N) {
@@ -183,7 +198,7 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
   // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
   // one launch each, in order on the stream (each launch re-arms the counters it used).
-  const int bm = 16 * p.p0;
+  const int bm = tile_bm(p);
   const size_t fit = (kMaxTensorBytes - 1) / (2 * static_cast<size_t>(K));
   const int chunk = fit >= static_cast<size_t>(M) ? M : static_cast<int>(fit / bm) * bm;
   if (chunk <= 0) return fail(W4A16_ERR_SHAPE, "K=%d is too long for one %d-row tile below 2 GiB", K, bm);
@@ -191,7 +206,7 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
     const int mc = M - r0 < chunk ? M - r0 : chunk;
     const int rc = check_launch(w4a16::launch_tile_cfg(x + static_cast<size_t>(r0) * K, pk, qz, scales,
                                                        y + static_cast<size_t>(r0) * N, partials, counters, mc, K,
-                                                       N, p.p0, p.p1, p.split, stream),
+                                                       N, p.p0, p.p2, p.p1, p.split, stream),
                                 "tile");
     if (rc != W4A16_OK) return rc;
   }
@@ -302,9 +317,11 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
       return fail(W4A16_ERR_ARG, "decode configuration needs %d ring and accumulator registers per lane (limit 176)",
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
-    if (p0 != 4 && p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 4, 8 or 16");
+    if (p0 != 4 && p0 != 6 && p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 4, 6, 8 or 16");
+    if (p2 < 0 || p2 > 3) return fail(W4A16_ERR_ARG, "tile shape code must be 0..3");
     if (p1 != 1 && p1 != 2) return fail(W4A16_ERR_ARG, "tile occupancy must be 1 or 2");
-    if (p0 == 16 && p1 != 1) return fail(W4A16_ERR_ARG, "tile wm 16 supports occupancy 1 only");
+    if (!w4a16::tile_config_compiled(p0, p2, p1))
+      return fail(W4A16_ERR_ARG, "tile configuration wm %d, shape %d, occupancy %d is not compiled", p0, p2, p1);
   } else {
     return fail(W4A16_ERR_ARG, "unknown regime %d", regime);
   }
@@ -314,7 +331,14 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
 
 size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split) {
   if (M <= 0 || N <= 0) return 0;
-  return workspace_for(GemmPlan{regime, p0, 0, 0, split}, M, N);
+  // Tile regime: enough for every tile shape (taller or wider tiles pad more).
+  size_t most = workspace_for(GemmPlan{regime, p0, 0, 1, split}, M, N);
+  if (regime != W4A16_REGIME_TILE) return most;
+  for (int shape = 2; shape <= 3; ++shape) {
+    const size_t b = workspace_for(GemmPlan{regime, p0, 0, shape, split}, M, N);
+    most = b > most ? b : most;
+  }
+  return most;
 }
 
 }  // extern "C"

@@ -43,11 +43,21 @@ hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const ui
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
                              int N, int tn, int depth, int waves, int split, hipStream_t stream);
 
-// LDS-tiled MFMA GEMM: workgroup tile (16 wm) x 256, wm in {4, 8, 16}; occ in {1, 2} waves
-// per SIMD the register allocation targets (wm 16: 1 only).  `partials` holds the split-K
-// fp32 fragments and `counters` one int per output tile (both unused when split == 1).
+// LDS-tiled MFMA GEMM.  A tile shape code selects the wave grid: nwm waves along M x nwn
+// along N, each owning tw 16-column layout tiles and 16 wm rows, so the workgroup tile is
+// (16 wm nwm) x (16 tw nwn).  Codes: 1 (or 0) = {tw 4, 1 x 4}, 2 = {tw 4, 2 x 4},
+// 3 = {tw 2, 1 x 8}.
+struct TileShape {
+  int tw, nwm, nwn;
+};
+TileShape tile_shape(int shape);
+// Whether (wm, shape, occ) is compiled; occ = waves per SIMD the register allocation targets.
+// Compiled: (4,1,1), (4,1,2), (8,1,1), (4,2,2), (6,2,2), (4,3,2), (8,3,2).
+bool tile_config_compiled(int wm, int shape, int occ);
+// `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
+// unused when split == 1).
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                            const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int occ, int split, hipStream_t stream);
+                           int N, int wm, int shape, int occ, int split, hipStream_t stream);
 
 }  // namespace w4a16

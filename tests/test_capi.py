@@ -128,7 +128,10 @@ def test_forced_config_validation(pkg):
     assert "registers" in L.last_error()
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 1, 2, 1, None, 0, None) == 1  # bad wm
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 3, 2, 1, None, 0, None) == 1  # bad occupancy
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 16, 2, 2, 1, None, 0, None) == 1  # wm 16 needs occupancy 1
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 16, 2, 2, 1, None, 0, None) == 1  # wm 16 is not compiled
+    assert "not compiled" in L.last_error()
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 7, 1, None, 0, None) == 1  # bad tile shape code
+    assert "shape" in L.last_error()
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 2, 1, None, 0, None) == 1  # bad regime
     # split > 1 without workspace
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 4, None, 0, None) == 4

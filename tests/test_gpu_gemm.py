@@ -112,23 +112,27 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
     assert rel_err(y, ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)) <= GEMM_REL_TOL
 
 
-TILE_CONFIGS = [(wm, occ, split) for wm in (4, 8) for occ in (1, 2) for split in (1, 2, 3)] + [(16, 1, 1), (16, 1, 2)]
+# (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
+TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (6, 2, 2), (4, 3, 2), (8, 3, 2)]
+TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3)]
 
 
 @pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256)])
 def test_every_tile_configuration(gpu_lib, m, n):
+    """Every compiled tile kernel and split: partial m-blocks (rows clamped and dropped),
+    n-blocks partly past N (waves with no columns), uneven K splits."""
     k = 1024
     p = ora.make_problem(seed=200 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
-    for wm, occ, split in TILE_CONFIGS:
+    for wm, shape, occ, split in TILE_CONFIGS:
         ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, occ, split, ws)
+        gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, occ, split, ws, p2=shape)
         err = rel_err(y, want)
-        assert err <= GEMM_REL_TOL, (wm, occ, split, err)
+        assert err <= GEMM_REL_TOL, (wm, shape, occ, split, err)
         if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
