@@ -103,25 +103,30 @@ GemmPlan plan_decode(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
-// Tile regime, chosen from sweeps on MI355X over the Qwen3-8B shapes at M = 128, 512 and
-// 2048.  Workgroups of 8 waves side by side along N (32 columns each, 256 per workgroup).
-// Tall problems (M >= 1024) use 128-row tiles (wm = 8: every dequantized weight serves 128
-// rows, one workgroup per CU), except where that grid fills the CUs in uneven rounds and
-// 64-row tiles do not (N = 6144: 384 vs 768 tiles at M = 2048).  Otherwise 64-row tiles
-// (two workgroups per CU) with K split in powers of two while the grid stays within about
-// 1.5 workgroups per CU (2 for long K) and every split keeps >= 8 groups; the fp32
-// partials are reduced by the last workgroup of each tile.
+// Tile regime, chosen from sweeps on MI355X over the Qwen3-8B shapes at M = 512 and 2048.
+// Two wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by side along N (32 columns
+// each), one workgroup per CU; shape 1 = 4 waves (64 columns each), two workgroups per CU.
+//  * Tall problems (M >= 1024): 128-row tiles in shape 3 (wm = 8: every dequantized weight
+//    serves 128 rows) when that grid fills the CUs in even rounds (gate_up, O and down at
+//    M = 2048); otherwise 64-row tiles in shape 1 (N = 6144: 384 vs 768 tiles).
+//  * Shorter problems: 64-row tiles; shape 1 when the grid is large (>= 512 tiles), else
+//    shape 3.  K is split in powers of two while the grid stays within one round (shape 3:
+//    256 workgroups; shape 1: 512) and every split keeps >= 8 groups; the fp32 partials
+//    are reduced by the last workgroup of each tile.
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  constexpr int kShape = 3;  // w4a16::tile_shape: 8 waves along N, 32 columns each
   auto tiles = [&](int wm) { return ceil_div(M, 16 * wm) * ceil_div(N, 256); };
-  if (M >= 1024 && tiles(8) >= 256 && (tiles(8) % 256 == 0 || tiles(8) >= 1024))
-    return GemmPlan{W4A16_REGIME_TILE, 8, 2, kShape, 1};
+  if (M >= 1024) {
+    const int t8 = tiles(8);
+    if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+    return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
+  }
   const int t = tiles(4);
-  const int cap = G >= 64 ? 512 : 384;
+  const int shape = t >= 512 ? 1 : 3;
+  const int cap = shape == 1 ? 512 : 256;
   int split = 1;
   while (split < 8 && t * split * 2 <= cap && 8 * split * 2 <= G) split *= 2;
-  return GemmPlan{W4A16_REGIME_TILE, 4, 2, kShape, split};
+  return GemmPlan{W4A16_REGIME_TILE, 4, 2, shape, split};
 }
 
 GemmPlan plan(int M, int K, int N) {

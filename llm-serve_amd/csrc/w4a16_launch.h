@@ -52,7 +52,7 @@ struct TileShape {
 };
 TileShape tile_shape(int shape);
 // Whether (wm, shape, occ) is compiled; occ = waves per SIMD the register allocation targets.
-// Compiled: (4,1,1), (4,1,2), (8,1,1), (4,2,2), (6,2,2), (4,3,2), (8,3,2).
+// Compiled: (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
 // unused when split == 1).

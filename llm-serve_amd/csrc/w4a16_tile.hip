@@ -86,7 +86,11 @@ __device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src,
 
 // One 128-deep group: per 32-row step, the matrix-core dequant of the wave's TW weight
 // tiles (2 TW scaling MFMAs), then WM x TW main MFMAs against the wave's 16 WM rows of the
-// LDS activation tile (`stage` points at the first of them).
+// LDS activation tile (`stage` points at the first of them).  Software-pipelined: step
+// j + 1's fragments are read and its weights dequantized while step j's main MFMAs run,
+// and scheduling groups interleave the two streams (one main MFMA, then a few VALU or
+// LDS instructions), so the VALU dequant of one step hides under the matrix work of the
+// previous one instead of alternating with it.
 template <int WM, int TW>
 __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const BGroup<TW>& b,
                                           const NibbleConsts& nib, int lane) {
@@ -95,19 +99,56 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
   TileScale ts[TW];
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt) ts[tt] = make_tile_scale(b.s[tt], (b.zw[tt] >> zshift) & 0xFu, lane);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    bf16x8_t bf[TW];
-#pragma unroll
-    for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
+  auto read_a = [&](bf16x8_t (&a)[WM], int j) {
     const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 15);  // row & 15 == lane & 15
     const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt) {
-      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
+    for (int mt = 0; mt < WM; ++mt) a[mt] = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
+  };
+  auto dequant = [&](bf16x8_t (&bf)[TW], int j) {
 #pragma unroll
-      for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a, bf[tt], acc[mt][tt]);
+    for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
+  };
+  if constexpr (WM * TW > 16) {
+    // Large wave tiles: no register double-buffering (the accumulators fill the AGPRs);
+    // the WM x TW independent MFMAs of a step leave the scheduler enough work to overlap.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8_t a[WM];
+      bf16x8_t bf[TW];
+      read_a(a, j);
+      dequant(bf, j);
+#pragma unroll
+      for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[mt], bf[tt], acc[mt][tt]);
     }
+    return;
+  }
+  bf16x8_t a[2][WM];
+  bf16x8_t bf[2][TW];
+  read_a(a[0], 0);
+  dequant(bf[0], 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = j & 1;
+    if (j < 3) {
+      read_a(a[c ^ 1], j + 1);
+      dequant(bf[c ^ 1], j + 1);
+    }
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[c][mt], bf[c][tt], acc[mt][tt]);
+    // Interleave: each main MFMA followed by up to two VALU and one LDS read of the next
+    // step (masks: 0x008 MFMA, 0x002 VALU, 0x100 LDS read).
+#pragma unroll
+    for (int k = 0; k < WM * TW; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -334,8 +375,7 @@ TileShape tile_shape(int shape) {
 // The compiled (wm, tile shape, occupancy) combinations, in one list for the launcher and
 // for tile_config_compiled.
 #define W4A16_TILE_CONFIGS(X)                                                                 \
-  X(4, 4, 1, 4, 1) X(4, 4, 1, 4, 2) X(8, 4, 1, 4, 1) X(4, 4, 2, 4, 2) X(6, 4, 2, 4, 2) X(4, 2, 1, 8, 2) \
-  X(8, 2, 1, 8, 2)
+  X(4, 4, 1, 4, 1) X(4, 4, 1, 4, 2) X(8, 4, 1, 4, 1) X(4, 4, 2, 4, 2) X(4, 2, 1, 8, 2) X(8, 2, 1, 8, 2)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);
