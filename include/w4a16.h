@@ -109,10 +109,13 @@ int w4a16_regime(int M, int K, int N);
 int w4a16_split_k(int M, int K, int N);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
- * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,3,4} dividing N/16, p1 = waves per
- * workgroup in {4,8,16}, p2 = 128-row groups in flight per wave in {1,2,4}, M <= 64) or
- * W4A16_REGIME_TILE (p0 = 16-row tiles per wave in {4,8,16}, p1 = waves per SIMD the
- * register allocation targets in {1,2} (1 for p0 = 16); p2 ignored);
+ * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,3,4,6} dividing N/16,
+ * p1 = waves per workgroup in {4,8}, p2 = 128-row groups in flight per wave in {1,2,4},
+ * M <= 64; configurations whose LDS exceeds 64 KiB or whose accumulators and load ring
+ * exceed 176 registers per lane are rejected) or W4A16_REGIME_TILE (p0 = 16-row tiles per
+ * wave, p1 = waves per SIMD the register allocation targets, p2 = wave layout: 0 or 1 =
+ * 4 waves of 64 columns, 2 = 2 x 4 waves of 64 columns, 3 = 8 waves of 32 columns; the
+ * compiled (p0, p2, p1) are (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2));
  * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises
  * every split-K reduction path at small sizes). */
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
@@ -120,7 +123,8 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
                       int regime, int p0, int p1, int p2, int split, void* workspace,
                       size_t workspace_bytes, void* stream);
 
-/* Workspace bytes w4a16_gemm_config needs for that configuration.  No reference counterpart. */
+/* Workspace bytes w4a16_gemm_config needs for that configuration (for the tile regime,
+ * enough for every wave layout).  No reference counterpart. */
 size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split);
 
 #ifdef __cplusplus
