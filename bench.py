@@ -34,6 +34,11 @@ Also reported (not part of `value`):
   * measured_ceilings: a 1 GiB device copy (read + write GB/s) and torch.matmul
     (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks.
 
+Checkpoint mode: `--checkpoint DIR [--layer-id I]` adds `checkpoint_layer`, the four
+projections of layer I of a local Qwen3 AutoAWQ checkpoint (read through its
+model.safetensors.index.json, q|k|v and gate|up merged along N) timed at M in {1, 4, 8, 16}
+on their real weights; `value` stays the synthetic sweep.
+
 Profiling mode: `--profile-point SHAPE:M` runs one point without graphs (a 256 MiB copy
 for counter calibration, then --steps launches over rotating weights) so that
 rocprofv3 --kernel-trace / --pmc see exactly that launch.
@@ -299,6 +304,28 @@ def measured_ceilings(dev, stream) -> dict:
             "hipblaslt_bf16_gate_up_m2048_TFLOP/s": round(2 * PREFILL_M * n * k / (ms * 1e-3) / 1e12, 1)}
 
 
+def checkpoint_layer(lib, dev, stream, path: str, layer_id: int, reps: int) -> dict:
+    """The four projections of one checkpoint layer, repacked on the GPU, each timed as one
+    graph-replayed launch (weights stay in cache across replays: a kernel-time figure, not
+    an HBM one) at M in {1, 4, 8, 16}."""
+    ckpt = importlib.import_module("llm-serve_amd.utils.checkpoint")
+    awq = importlib.import_module("llm-serve_amd.layers.quantization.awq")
+    out = {}
+    for proj in ckpt.load_layer_projections(path, layer_id=layer_id):
+        proj = proj.to(dev)
+        k, n = proj.input_size, proj.output_size
+        weights = [(awq.repack_awq_qweight(proj.qweight), proj.qzeros.contiguous(), proj.scales.contiguous())]
+        row = {"K": k, "N": n}
+        for m in DECODE_M:
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            p = Point(lib, proj.name, m, k, n, weights, x)
+            ms = time_graph(lambda: p.launch_all(torch.cuda.current_stream(dev).cuda_stream), stream, reps)
+            row[f"M={m}"] = {"us": round(ms * 1e3, 2),
+                             "GB/s": round(algorithmic_bytes(m, k, n) / (ms * 1e-3) / 1e9, 1)}
+        out[proj.name] = row
+    return {"path": os.path.abspath(path), "layer_id": layer_id, "projections": out}
+
+
 def read_traffic(path: str = TRAFFIC_FILE):
     """HBM bytes per launch recorded in the committed counter summary, or None."""
     try:
@@ -360,6 +387,8 @@ def main(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="skip the mixed-batch, layer-stack and ceiling legs")
     ap.add_argument("--details", action="store_true", help="print one line per point to stderr")
     ap.add_argument("--profile-point", metavar="SHAPE:M", help="profiling workload for one point (see doc)")
+    ap.add_argument("--checkpoint", metavar="DIR", help="also time one layer of a local Qwen3 AutoAWQ checkpoint")
+    ap.add_argument("--layer-id", type=int, default=0)
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no multi-GPU "
@@ -427,6 +456,12 @@ def main(argv=None):
             print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
             print(f"ceilings: {json.dumps(ceilings)}", file=sys.stderr)
 
+    ckpt_layer = None
+    if args.checkpoint:
+        ckpt_layer = checkpoint_layer(lib, dev, stream, args.checkpoint, args.layer_id, max(3, args.steps))
+        if args.details:
+            print(f"checkpoint layer: {json.dumps(ckpt_layer)}", file=sys.stderr)
+
     cpu = None if args.no_cpu else cpu_baseline()
     result = {
         "metric": METRIC,
@@ -454,6 +489,7 @@ def main(argv=None):
         "mixed_m512": mixed,
         "stack36": stack,
         "measured_ceilings": ceilings,
+        "checkpoint_layer": ckpt_layer,
         "points": points_out,
     }
     print(json.dumps(result))
