@@ -32,7 +32,13 @@ Also reported (not part of `value`):
     M in {1, 8, 64, 128}: 144 GEMMs per step captured in one graph; aggregate weight
     GB/s and linear-layer time per decoded token;
   * measured_ceilings: a 1 GiB device copy (read + write GB/s) and torch.matmul
-    (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks.
+    (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
+  * fused_gate_up: the gate_up GEMM with SiLU(gate) * up in its epilogue
+    (w4a16_gemm_silu_mul, [M, 12288] out) against the plain GEMM ([M, 24576] out) and
+    against the reference's two steps (the plain GEMM, then torch's SiLU * up on its
+    output), at M in {1, 16, 64, 512, 2048};
+  * quantize: the GPU AWQ quantizer over a [24576, 4096] bf16 weight (GB/s of weight
+    read + packed output written).
 
 Checkpoint mode: `--checkpoint DIR [--layer-id I]` adds `checkpoint_layer`, the four
 projections of layer I of a local Qwen3 AutoAWQ checkpoint (read through its
@@ -326,6 +332,67 @@ def checkpoint_layer(lib, dev, stream, path: str, layer_id: int, reps: int) -> d
     return {"path": os.path.abspath(path), "layer_id": layer_id, "projections": out}
 
 
+FUSED_M = (1, 16, 64, 512, 2048)
+
+
+def fused_gate_up(lib, dev, stream, reps: int) -> dict:
+    """Fused SiLU * up epilogue vs the plain gate_up GEMM and the two-step path, each
+    graph-replayed over rotating weight copies (decode bytes come from HBM)."""
+    k, n = SHAPES["gate_up"]
+    copies = max(2, -(-2 * CACHE_BYTES // weight_bytes(k, n)))
+    weights = make_weights(k, n, copies, dev, 4242)
+    out = {}
+    for m in FUSED_M:
+        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        yf = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
+        ws_len = lib.workspace_bytes(m, k, n)
+        ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
+        wsp = ws.data_ptr() if ws_len else None
+
+        def run(fn_name, dst, act=False):
+            def step():
+                sp = torch.cuda.current_stream(dev).cuda_stream
+                for packed, qzeros, scales in weights:
+                    rc = getattr(lib.dll, fn_name)(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                   scales.data_ptr(), dst.data_ptr(), m, k, n, 128, wsp, ws_len, sp)
+                    if rc != 0:
+                        raise RuntimeError(lib.last_error())
+                    if act:
+                        torch.mul(torch.nn.functional.silu(dst[:, : n // 2]), dst[:, n // 2:], out=yf)
+            return time_graph(step, stream, reps) / len(weights)
+
+        fused_ms = run("w4a16_gemm_silu_mul", yf)
+        plain_ms = run("w4a16_gemm", y)
+        two_ms = run("w4a16_gemm", y, act=True)
+        out[f"M={m}"] = {"fused_us": round(fused_ms * 1e3, 2), "gemm_us": round(plain_ms * 1e3, 2),
+                         "two_step_us": round(two_ms * 1e3, 2),
+                         "saved_vs_two_step": round(1 - fused_ms / two_ms, 4),
+                         "fused_TFLOP/s": round(2 * m * n * k / (fused_ms * 1e-3) / 1e12, 1)}
+    del weights
+    return out
+
+
+def quantize_throughput(lib, dev, stream, reps: int) -> dict:
+    """w4a16_quantize over a [24576, 4096] bf16 weight (the gate_up projection's float
+    weight): bytes = 2 per weight read + 0.5 written + scales and zeros."""
+    out_f, in_f = 24576, 4096
+    w = (torch.randn((out_f, in_f), device=dev) * 0.02).to(torch.bfloat16)
+    qw = torch.empty((in_f, out_f // 8), dtype=torch.int32, device=dev)
+    qz = torch.empty((in_f // 128, out_f // 8), dtype=torch.int32, device=dev)
+    sc = torch.empty((in_f // 128, out_f), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        rc = lib.dll.w4a16_quantize(w.data_ptr(), 0, qw.data_ptr(), qz.data_ptr(), sc.data_ptr(), out_f, in_f, 128,
+                                    torch.cuda.current_stream(dev).cuda_stream)
+        if rc != 0:
+            raise RuntimeError(lib.last_error())
+
+    ms = time_graph(step, stream, reps)
+    nbytes = out_f * in_f * 2 + out_f * in_f // 2 + (in_f // 128) * out_f * (2 + 0.5)
+    return {"shape": [out_f, in_f], "us": round(ms * 1e3, 1), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def read_traffic(path: str = TRAFFIC_FILE):
     """HBM bytes per launch recorded in the committed counter summary, or None."""
     try:
@@ -446,15 +513,19 @@ def main(argv=None):
                 print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
         del pts
 
-    mixed = stack = ceilings = None
+    mixed = stack = ceilings = fused = quant = None
     if not args.no_extra:
         mixed = mixed_batch(lib, dev, stream, max(3, args.steps // 4))
         stack = layer_stack(lib, dev, stream, max(2, args.steps // 10))
         ceilings = measured_ceilings(dev, stream)
+        fused = fused_gate_up(lib, dev, stream, max(3, args.steps // 4))
+        quant = quantize_throughput(lib, dev, stream, max(3, args.steps // 4))
         if args.details:
             print(f"mixed M={MIXED_M}: {json.dumps(mixed)}", file=sys.stderr)
             print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
             print(f"ceilings: {json.dumps(ceilings)}", file=sys.stderr)
+            print(f"fused gate_up: {json.dumps(fused)}", file=sys.stderr)
+            print(f"quantize: {json.dumps(quant)}", file=sys.stderr)
 
     ckpt_layer = None
     if args.checkpoint:
@@ -489,6 +560,8 @@ def main(argv=None):
         "mixed_m512": mixed,
         "stack36": stack,
         "measured_ceilings": ceilings,
+        "fused_gate_up": fused,
+        "quantize": quant,
         "checkpoint_layer": ckpt_layer,
         "points": points_out,
     }

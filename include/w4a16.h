@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 1
+#define W4A16_ABI_VERSION 2
 
 enum w4a16_status {
   W4A16_OK = 0,
@@ -44,6 +44,13 @@ enum w4a16_status {
 };
 
 /* Kernel families reported by w4a16_regime(). */
+/* Element type of a float weight given to w4a16_quantize (its scales get the same type). */
+enum w4a16_dtype {
+  W4A16_DTYPE_BF16 = 0,
+  W4A16_DTYPE_F16 = 1,
+  W4A16_DTYPE_F32 = 2
+};
+
 enum w4a16_regime_id {
   W4A16_REGIME_NONE = 0,   /* M == 0: nothing to launch */
   W4A16_REGIME_DECODE = 1, /* M <= 64: split-K, HBM-bound kernel */
@@ -83,7 +90,26 @@ int w4a16_repack_qweight(const int32_t* qweight, int32_t* packed, int K, int N, 
 int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
                          uint16_t* w_out, int K, int N, int group_size, void* stream);
 
-/* Bytes of workspace w4a16_gemm needs for this problem (0 = none).  The workspace must be
+/* Group-wise asymmetric int4 quantization of weight [out_features, in_features] (row-major,
+ * element type dtype) into the AutoAWQ GEMM layout: qweight [in_features, out_features/8],
+ * qzeros [in_features/group_size, out_features/8] (int32), scales
+ * [in_features/group_size, out_features] of type dtype.  Per (output row, group):
+ * s = max(max - min, 1e-5) / 15, z = clamp(-round(min / s), 0, 15),
+ * q = clamp(round(w / s) + z, 0, 15) in fp32, round half to even -- bit-exact with the
+ * reference for finite weights.  out_features % 8 == 0, 1 <= group_size <= 128 dividing
+ * in_features, in_features / group_size <= 65535; weight 2- or 4-byte aligned by type.
+ * Replaces quantize_awq_weight (awq_calibration.py:35-62). */
+int w4a16_quantize(const void* weight, int dtype, int32_t* qweight, int32_t* qzeros, void* scales,
+                   int out_features, int in_features, int group_size, void* stream);
+
+/* Pack int32 values [rows, cols] (cols % 8 == 0; each value's low 4 bits) into AutoAWQ words
+ * [rows, cols/8]: nibble i of word [r, j] holds column 8j + (0,2,4,6,1,3,5,7)[i].  values
+ * 16-byte aligned.  Range checks on the values stay with the caller.
+ * Replaces _pack_int4 (awq_calibration.py:19-32). */
+int w4a16_pack_int4(const int32_t* values, int32_t* packed, int rows, int cols, void* stream);
+
+/* Bytes of workspace w4a16_gemm needs for this problem (0 = none), and, when N % 128 == 0,
+ * w4a16_gemm_silu_mul too (the larger of the two).  The workspace must be
  * zero-filled once when first allocated; the kernels leave its counter words at zero.
  * Two GEMMs in flight at the same time must not share one workspace.
  * Replaces the workspace sizing of awq.py:168-180 and awq_cuda.py:157-176. */
@@ -98,6 +124,17 @@ size_t w4a16_workspace_bytes(int M, int K, int N, int group_size);
 int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
                const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/* y[M, N/2] = SiLU(g) * u with [g | u] = x[M, K] @ W for a gate|up weight W [K, N] whose
+ * first N/2 columns are the gate projection and last N/2 the up projection (the layout of
+ * MergedColumnParallelLinear's gate_up_proj); g and u stay in fp32 and the product is rounded
+ * once to bf16.  Same arguments and limits as w4a16_gemm, plus N % 128 == 0; y is
+ * [M, N/2], 16-byte aligned; workspace from w4a16_workspace_bytes(M, K, N, 128).
+ * Replaces gate_up_proj followed by SiluAndMul (qwen3.py:126-130, activation.py:8-11):
+ * the [M, N] gate|up intermediate is never written. */
+int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                        const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* Kernel family w4a16_gemm launches for (M, K, N): a w4a16_regime_id.
  * Replaces the dispatch rule of select_awq_cuda_split_k (awq_cuda.py:17-26) and
@@ -122,6 +159,13 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
                       const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
                       int regime, int p0, int p1, int p2, int split, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* w4a16_gemm_silu_mul with the kernel configuration forced, as w4a16_gemm_config (decode
+ * p0 must be even).  No reference counterpart: a testing hook. */
+int w4a16_gemm_silu_mul_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                               const uint16_t* scales, uint16_t* y, int M, int K, int N,
+                               int group_size, int regime, int p0, int p1, int p2, int split,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes w4a16_gemm_config needs for that configuration (for the tile regime,
  * enough for every wave layout).  No reference counterpart. */

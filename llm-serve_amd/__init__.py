@@ -10,6 +10,7 @@ from .layers.quantization.awq import (
     AWQLinearMethod,
     AWQRuntimeConfig,
     awq_linear,
+    awq_linear_silu_mul,
     awq_regime,
     dequantize_awq_gemm,
     repack_awq_qweight,
@@ -25,6 +26,7 @@ __all__ = (
     "W4A16Error",
     "W4A16Library",
     "awq_linear",
+    "awq_linear_silu_mul",
     "awq_regime",
     "dequantize_awq_gemm",
     "lib",

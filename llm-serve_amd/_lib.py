@@ -38,8 +38,15 @@ _SIGNATURES = {
     "w4a16_gemm_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
     "w4a16_workspace_bytes_config": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "w4a16_quantize": (_c_int, [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr]),
+    "w4a16_pack_int4": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_gemm_silu_mul": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+                                     _c_ptr, _c_size, _c_ptr]),
+    "w4a16_gemm_silu_mul_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
+                                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size,
+                                            _c_ptr]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class W4A16Error(RuntimeError):
@@ -115,6 +122,33 @@ class W4A16Library:
                        "w4a16_dequant")
         return out
 
+    _DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+    def quantize(self, weight: torch.Tensor, group_size: int):
+        """weight [out, in] (bf16 / fp16 / fp32, contiguous) -> (qweight [in, out/8],
+        qzeros [in/g, out/8], scales [in/g, out] of weight's dtype)."""
+        self._require_gpu(weight)
+        out_f, in_f = weight.shape
+        dev = weight.device
+        qweight = torch.empty((in_f, out_f // 8), dtype=torch.int32, device=dev)
+        qzeros = torch.empty((in_f // group_size, out_f // 8), dtype=torch.int32, device=dev)
+        scales = torch.empty((in_f // group_size, out_f), dtype=weight.dtype, device=dev)
+        with torch.cuda.device(dev):
+            self.check(self.dll.w4a16_quantize(weight.data_ptr(), self._DTYPES[weight.dtype], qweight.data_ptr(),
+                                               qzeros.data_ptr(), scales.data_ptr(), out_f, in_f, group_size,
+                                               self._stream(weight)), "w4a16_quantize")
+        return qweight, qzeros, scales
+
+    def pack_int4(self, values: torch.Tensor) -> torch.Tensor:
+        """int32 [rows, cols] -> AutoAWQ words [rows, cols/8] (low 4 bits of each value)."""
+        self._require_gpu(values)
+        rows, cols = values.shape
+        out = torch.empty((rows, cols // 8), dtype=torch.int32, device=values.device)
+        with torch.cuda.device(values.device):
+            self.check(self.dll.w4a16_pack_int4(values.data_ptr(), out.data_ptr(), rows, cols,
+                                                self._stream(values)), "w4a16_pack_int4")
+        return out
+
     def repack_qweight(self, qweight: torch.Tensor) -> torch.Tensor:
         self._require_gpu(qweight)
         k, n = qweight.shape[0], qweight.shape[1] * 8
@@ -145,17 +179,30 @@ class W4A16Library:
                        "w4a16_gemm")
         return y
 
-    def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,
-                    split: int, workspace: torch.Tensor | None, group_size: int = 128,
-                    p2: int = 0) -> torch.Tensor:
+    def gemm_silu_mul(self, x, packed, qzeros, scales, y, k: int, n: int, workspace: torch.Tensor | None,
+                      group_size: int = 128) -> torch.Tensor:
+        """y[M, N/2] = SiLU(g) * u, [g | u] = x[M, K] @ W for a gate|up weight of width N."""
         m = x.shape[0]
         ws_ptr = workspace.data_ptr() if workspace is not None else None
         ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
         with torch.cuda.device(x.device):
-            self.check(self.dll.w4a16_gemm_config(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
-                                                  scales.data_ptr(), y.data_ptr(), m, k, n, group_size, regime,
-                                                  p0, p1, p2, split, ws_ptr, ws_len, self._stream(x)),
-                       "w4a16_gemm_config")
+            self.check(self.dll.w4a16_gemm_silu_mul(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                    scales.data_ptr(), y.data_ptr(), m, k, n, group_size, ws_ptr,
+                                                    ws_len, self._stream(x)),
+                       "w4a16_gemm_silu_mul")
+        return y
+
+    def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,
+                    split: int, workspace: torch.Tensor | None, group_size: int = 128,
+                    p2: int = 0, silu_mul: bool = False) -> torch.Tensor:
+        m = x.shape[0]
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        fn = self.dll.w4a16_gemm_silu_mul_config if silu_mul else self.dll.w4a16_gemm_config
+        with torch.cuda.device(x.device):
+            self.check(fn(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(), m, k,
+                          n, group_size, regime, p0, p1, p2, split, ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm_silu_mul_config" if silu_mul else "w4a16_gemm_config")
         return y
 
 

@@ -134,6 +134,26 @@ GemmPlan plan(int M, int K, int N) {
   return M <= kDecodeMaxM ? plan_decode(M, K, N) : plan_tile(M, K, N);
 }
 
+// The fused SiLU(gate) * up product of a gate|up weight [K, N] runs the plain GEMM's plan,
+// except that a decode workgroup must hold whole gate/up tile pairs: an odd tile count
+// becomes the next even one that divides N / 16 and fits the registers (the LDS check may
+// then split K further).
+GemmPlan plan_silu_mul(int M, int K, int N) {
+  GemmPlan p = plan(M, K, N);
+  if (p.regime != W4A16_REGIME_DECODE || p.p0 % 2 == 0) return p;
+  const int G = K / w4a16::kGroup;
+  const int MB = (M + 15) / 16;
+  const int T = N / 16;
+  const bool xl = w4a16::decode_stages_x(M, K, p.split);
+  int tn = p.p0 == 1 ? 2 : 4;
+  while (tn > 2 && (T % tn != 0 || !w4a16::decode_config_fits(MB, tn, 1, xl))) tn -= 2;
+  while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
+  p.p0 = tn;
+  while (w4a16::decode_lds_bytes(M, K, tn, p.p1, p.split) > w4a16::kDecodeMaxLds && p.split < G)
+    p.split = p.split * 2 > G ? G : p.split * 2;
+  return p;
+}
+
 // Workspace layout: [arrival counters: kCounterBytes][fp32 partials: split * M * N].
 // The counters sit at a fixed offset so that a workspace shared by calls of different
 // shapes always presents zeroed counters (every kernel re-arms the ones it used).
@@ -160,12 +180,14 @@ size_t workspace_for(const GemmPlan& p, int M, int N) {
 }
 
 int validate_gemm(const void* x, const void* packed, const void* qzeros, const void* scales, const void* y, int M,
-                  int K, int N, int group_size) {
+                  int K, int N, int group_size, bool silu_mul = false) {
   if (M < 0 || K <= 0 || N <= 0) return fail(W4A16_ERR_ARG, "M must be >= 0 and K, N positive (got M=%d K=%d N=%d)", M, K, N);
   if (group_size != w4a16::kGroup)
     return fail(W4A16_ERR_SHAPE, "group_size must be 128 (got %d)", group_size);
   if (K % w4a16::kGroup) return fail(W4A16_ERR_SHAPE, "K must be divisible by 128 (got %d)", K);
   if (N % 64) return fail(W4A16_ERR_SHAPE, "N must be divisible by 64 (got %d)", N);
+  if (silu_mul && N % 128)
+    return fail(W4A16_ERR_SHAPE, "the gate|up width N must be divisible by 128 (got %d)", N);
   if (static_cast<size_t>(K) * N / 2 >= kMaxTensorBytes)
     return fail(W4A16_ERR_SHAPE, "packed weights of K=%d N=%d exceed 2 GiB", K, N);
   if (static_cast<size_t>(M) * K * 2 >= kMaxTensorBytes && M <= kDecodeMaxM)
@@ -179,9 +201,10 @@ int validate_gemm(const void* x, const void* packed, const void* qzeros, const v
   return ok();
 }
 
+// up_tiles: 0 for the plain GEMM, N / 32 for the fused SiLU(gate) * up (y is [M, N / 2]).
 int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
              const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
-             hipStream_t stream) {
+             hipStream_t stream, int up_tiles = 0) {
   if (p.regime == W4A16_REGIME_NONE) return ok();
   const size_t need = workspace_for(p, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -198,20 +221,21 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
   if (p.regime == W4A16_REGIME_DECODE)
     return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p2,
-                                                 p.p1, p.split, stream),
+                                                 p.p1, p.split, up_tiles, stream),
                         "decode");
   // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
   // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
   // one launch each, in order on the stream (each launch re-arms the counters it used).
   const int bm = tile_bm(p);
+  const size_t n_out = up_tiles ? N / 2 : N;
   const size_t fit = (kMaxTensorBytes - 1) / (2 * static_cast<size_t>(K));
   const int chunk = fit >= static_cast<size_t>(M) ? M : static_cast<int>(fit / bm) * bm;
   if (chunk <= 0) return fail(W4A16_ERR_SHAPE, "K=%d is too long for one %d-row tile below 2 GiB", K, bm);
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int mc = M - r0 < chunk ? M - r0 : chunk;
     const int rc = check_launch(w4a16::launch_tile_cfg(x + static_cast<size_t>(r0) * K, pk, qz, scales,
-                                                       y + static_cast<size_t>(r0) * N, partials, counters, mc, K,
-                                                       N, p.p0, p.p2, p.p1, p.split, stream),
+                                                       y + static_cast<size_t>(r0) * n_out, partials, counters, mc,
+                                                       K, N, p.p0, p.p2, p.p1, p.split, up_tiles, stream),
                                 "tile");
     if (rc != W4A16_OK) return rc;
   }
@@ -277,9 +301,45 @@ int w4a16_dequant_packed(const int32_t* packed, const int32_t* qzeros, const uin
                       "dequant_packed");
 }
 
+int w4a16_quantize(const void* weight, int dtype, int32_t* qweight, int32_t* qzeros, void* scales,
+                   int out_features, int in_features, int group_size, void* stream) {
+  static_assert(W4A16_DTYPE_BF16 == w4a16::kDtypeBF16 && W4A16_DTYPE_F16 == w4a16::kDtypeF16 &&
+                    W4A16_DTYPE_F32 == w4a16::kDtypeF32,
+                "dtype codes");
+  if (out_features <= 0 || in_features <= 0) return fail(W4A16_ERR_ARG, "out_features and in_features must be positive");
+  if (dtype != W4A16_DTYPE_BF16 && dtype != W4A16_DTYPE_F16 && dtype != W4A16_DTYPE_F32)
+    return fail(W4A16_ERR_ARG, "unknown weight dtype %d", dtype);
+  if (group_size < 1 || group_size > 128)
+    return fail(W4A16_ERR_SHAPE, "group_size must be in [1, 128] (got %d)", group_size);
+  if (in_features % group_size) return fail(W4A16_ERR_SHAPE, "input size must be divisible by group_size");
+  if (out_features % 8) return fail(W4A16_ERR_SHAPE, "output size must be divisible by 8");
+  if (in_features / group_size > 65535) return fail(W4A16_ERR_SHAPE, "more than 65535 groups per row");
+  if (!weight || !qweight || !qzeros || !scales) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  const size_t elem = dtype == W4A16_DTYPE_F32 ? 4 : 2;
+  if (!aligned(weight, elem) || !aligned(scales, elem) || !aligned(qweight, 4) || !aligned(qzeros, 4))
+    return fail(W4A16_ERR_ALIGN, "weight and scales must be aligned to their element size");
+  return check_launch(w4a16::launch_quantize(weight, dtype, reinterpret_cast<uint32_t*>(qweight),
+                                             reinterpret_cast<uint32_t*>(qzeros), scales, out_features,
+                                             in_features, group_size, static_cast<hipStream_t>(stream)),
+                      "quantize");
+}
+
+int w4a16_pack_int4(const int32_t* values, int32_t* packed, int rows, int cols, void* stream) {
+  if (rows <= 0 || cols <= 0) return fail(W4A16_ERR_ARG, "rows and cols must be positive");
+  if (cols % 8) return fail(W4A16_ERR_SHAPE, "INT4 packing requires the output dimension to be divisible by 8");
+  if (!values || !packed) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if (!aligned(values, 16) || !aligned(packed, 4)) return fail(W4A16_ERR_ALIGN, "values must be 16-byte aligned");
+  return check_launch(w4a16::launch_pack_int4(values, reinterpret_cast<uint32_t*>(packed), rows, cols,
+                                              static_cast<hipStream_t>(stream)),
+                      "pack_int4");
+}
+
 size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
   if (M <= 0 || K <= 0 || N <= 0 || group_size != w4a16::kGroup || K % w4a16::kGroup || N % 64) return 0;
-  return workspace_for(plan(M, K, N), M, N);
+  const size_t plain = workspace_for(plan(M, K, N), M, N);
+  if (N % 128) return plain;
+  const size_t fused = workspace_for(plan_silu_mul(M, K, N), M, N);
+  return fused > plain ? fused : plain;
 }
 
 int w4a16_regime(int M, int K, int N) {
@@ -300,10 +360,23 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, 
                   static_cast<hipStream_t>(stream));
 }
 
-int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
-                      uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int p2,
-                      int split, void* workspace, size_t workspace_bytes, void* stream) {
-  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
+int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                        uint16_t* y, int M, int K, int N, int group_size, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size, true);
+  if (v != W4A16_OK) return v;
+  return run_plan(plan_silu_mul(M, K, N), x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream), N / 32);
+}
+
+}  // extern "C"
+
+namespace {
+
+int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                     uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int p2, int split,
+                     void* workspace, size_t workspace_bytes, void* stream, bool silu_mul) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size, silu_mul);
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
   const int G = K / w4a16::kGroup;
@@ -313,6 +386,8 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
     if (M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
     if (p0 < 1 || p0 > 6 || p0 == 5) return fail(W4A16_ERR_ARG, "decode column tiles must be 1, 2, 3, 4 or 6");
     if ((N / 16) % p0) return fail(W4A16_ERR_SHAPE, "N / 16 = %d is not a multiple of %d column tiles", N / 16, p0);
+    if (silu_mul && p0 % 2)
+      return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs an even decode column tile count");
     if (p1 != 4 && p1 != 8) return fail(W4A16_ERR_ARG, "decode waves must be 4 or 8");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
     if (w4a16::decode_lds_bytes(M, K, p0, p1, split) > w4a16::kDecodeMaxLds)
@@ -331,7 +406,26 @@ int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* q
     return fail(W4A16_ERR_ARG, "unknown regime %d", regime);
   }
   return run_plan(p, x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
-                  static_cast<hipStream_t>(stream));
+                  static_cast<hipStream_t>(stream), silu_mul ? N / 32 : 0);
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                      uint16_t* y, int M, int K, int N, int group_size, int regime, int p0, int p1, int p2,
+                      int split, void* workspace, size_t workspace_bytes, void* stream) {
+  return gemm_config_impl(x, packed, qzeros, scales, y, M, K, N, group_size, regime, p0, p1, p2, split, workspace,
+                          workspace_bytes, stream, false);
+}
+
+int w4a16_gemm_silu_mul_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                               const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size, int regime,
+                               int p0, int p1, int p2, int split, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return gemm_config_impl(x, packed, qzeros, scales, y, M, K, N, group_size, regime, p0, p1, p2, split, workspace,
+                          workspace_bytes, stream, true);
 }
 
 size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split) {

@@ -31,6 +31,10 @@
 namespace w4a16 {
 
 constexpr int kGroup = 128;      // quantization group (rows of K per scale / zero)
+// Element types of a float weight given to the quantizer (W4A16_DTYPE_* in w4a16.h).
+constexpr int kDtypeBF16 = 0;
+constexpr int kDtypeF16 = 1;
+constexpr int kDtypeF32 = 2;
 constexpr int kTileCols = 16;    // columns of one layout tile
 constexpr int kTileWords = 256;  // words of one (group, 16-column) tile = 1 KiB
 
@@ -58,6 +62,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
   return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+}
+
+// SiLU(g) * u = g / (1 + e^-g) * u in fp32 for the fused gate/up epilogue, e^-g as
+// 2^(-g log2 e) on the hardware exp2 and the quotient by the hardware reciprocal (about
+// 1 ulp each, far below the bf16 rounding of the result).  g -> -inf gives -0 (e^-g = inf,
+// reciprocal 0), g -> +inf gives g u; NaN propagates.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 // The two constants of the nibble unpack, held in registers: mask 0x000F000F in an SGPR,

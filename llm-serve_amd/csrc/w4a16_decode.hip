@@ -38,6 +38,7 @@ struct DecodeArgs {
   float* partials;
   int* counters;
   int M, K, N, split;
+  int up_tiles;  // 0: plain GEMM; else fused SiLU(gate) * up with up tiles this far past gate
 };
 
 // LDS layout of the staged operands.  A wave owns at most `items` groups (its groups
@@ -67,6 +68,14 @@ __host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int
   return l;
 }
 
+// Column tiles of a workgroup.  Plain: tiles tb + tt, tt < TN.  Fused gate/up (TN even,
+// H = TN / 2): gate tiles tb + tt for tt < H and their up tiles tb + up_tiles + tt - H, i.e.
+// tile tb + tt + dt for tt >= H with dt = up_tiles - H (dt = 0 plain).
+template <int TN>
+__device__ __forceinline__ int decode_tile(int tb, int dt, int tt) {
+  return tb + tt + (tt >= TN / 2 ? dt : 0);
+}
+
 // Everything one wave loads from global memory for one 128-row group: one 16-byte weight
 // load per tile and, when the activations are not staged, the MB x 4 activation fragments.
 // Loaded DEPTH groups ahead of use; decoded only when consumed.
@@ -87,13 +96,13 @@ struct DecodeSources {
 
 template <int MB, int TN, bool XL>
 __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, const DecodeSources& src,
-                                                  const uint32_t (&x_row)[MB], int g, bool valid, int N, int cb,
-                                                  int lane) {
+                                                  const uint32_t (&x_row)[MB], int g, bool valid, int N, int tb,
+                                                  int dt, int lane) {
   const int NT = N / kTileCols;
   const uint32_t oob = valid ? 0u : kOutOfRange;
 #pragma unroll
   for (int tt = 0; tt < TN; ++tt) {
-    const int t = cb * TN + tt;
+    const int t = decode_tile<TN>(tb, dt, tt);
     const uint32_t wo = (valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : 0u) | oob;
     st.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
   }
@@ -152,16 +161,17 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 // end fetch nothing).
 template <int TN, bool XL, int W>
 __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay, const DecodeSources& src, int M,
-                                               int K, int N, int cb, int g_first, int n_items, int lane) {
-  constexpr int kSW = TN * 8;  // scale-pair words per group
-  constexpr int kZW = TN * 2;  // zero words per group
+                                               int K, int N, int tb, int dt, int g_first, int n_items, int lane) {
+  constexpr int kSW = TN * 8;  // scale-pair words per group (8 per tile)
+  constexpr int kZW = TN * 2;  // zero words per group (2 per tile)
   const int s_words = n_items * kSW;
   for (int b = 0; b < s_words; b += 64) {
     const int w = b + lane;
     const int i = w / kSW;
     const int j = w - i * kSW;
+    const int sj = tb * 8 + j + (j >= (TN / 2) * 8 ? dt * 8 : 0);
     const uint32_t off =
-        w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + cb * kSW + j) * 4u : kOutOfRange;
+        w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + sj) * 4u : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)(wl + lay.s_off + b * 4), 4, off, 0, 0, 0);
   }
   const int z_words = n_items * kZW;
@@ -169,8 +179,9 @@ __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay
     const int w = b + lane;
     const int i = w / kZW;
     const int j = w - i * kZW;
+    const int zj = tb * 2 + j + (j >= (TN / 2) * 2 ? dt * 2 : 0);
     const uint32_t off =
-        w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + cb * kZW + j) * 4u : kOutOfRange;
+        w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(wl + lay.z_off + b * 4), 4, off, 0, 0, 0);
   }
   if constexpr (XL) {
@@ -198,7 +209,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ scales,
                                                             uint16_t* __restrict__ y, float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
-                                                            int split) {
+                                                            int split, int up_tiles) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
   const int lane = threadIdx.x & 63;
@@ -210,7 +221,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const int g_begin = (G * sidx) / split;
   const int g_end = (G * (sidx + 1)) / split;
   const int nG = g_end - g_begin;
-  const int col0 = cb * (16 * TN) + (lane & 15);  // this lane's column in tile 0
+  // Fused SiLU(gate) * up (TN even): the workgroup's H gate tiles are output tiles
+  // cb H .. cb H + H - 1 of the [M, N / 2] result.
+  constexpr int H = TN / 2;
+  const bool act = TN % 2 == 0 && up_tiles != 0;
+  const int tb = act ? cb * H : cb * TN;
+  const int dt = act ? up_tiles - H : 0;
   const DecodeLds lay = decode_lds_layout(M, K, TN, W, split, XL);
 
   DecodeSources src;
@@ -234,7 +250,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // The wave's groups: gi = wave + i W of the K range, i < n_items.
   const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
   uint8_t* wl = lds + wave * lay.wave_bytes;
-  stage_operands<TN, XL, W>(wl, lay, src, M, K, N, cb, g_begin + wave, n_items, lane);
+  stage_operands<TN, XL, W>(wl, lay, src, M, K, N, tb, dt, g_begin + wave, n_items, lane);
   __builtin_amdgcn_sched_barrier(0);  // the staging loads stay ahead of the ring's
 
   // Depth-DEPTH ring over the wave's items: item i is loaded while item i - DEPTH is being
@@ -244,7 +260,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   DecodeStage<MB, TN, XL> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d)
-    load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, cb, lane);
+    load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
   // Direct-to-LDS loads may complete out of order with the register loads issued after
   // them (they do when those hit in cache), so a partial vmcnt wait does not cover them:
   // wait for everything, the ring included, before the first group reads the slice.
@@ -258,7 +274,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
       if (i < n_items) compute_decode_stage<MB, TN, XL>(acc, ring[d], wl, lay, i, M, nib, lane);
       const int in = i + DEPTH;
       __builtin_amdgcn_sched_barrier(0);
-      load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, cb, lane);
+      load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -274,68 +290,80 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   __syncthreads();
 
   // Output (mb, tt) pairs are spread over the waves; p is a compile-time index so the
-  // register arrays stay in registers.
+  // register arrays stay in registers.  Fused, a gate pair and its up pair (tt and tt + H)
+  // belong to the same wave.
   constexpr int kPairs = MB * TN;
+  auto owner = [&](int p) {
+    return (act ? (p / TN) * H + (p % TN) % (H > 0 ? H : 1) : p) % W;
+  };
   f32x4_t out[kPairs];
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
-    if (p % W != wave) continue;
+    if (owner(p) != wave) continue;
     f32x4_t v = red[p * 64 + lane];
 #pragma unroll
     for (int w = 1; w < W; ++w) v += red[(w * kPairs + p) * 64 + lane];
     out[p] = v;
   }
 
-  if (split == 1) {
+  if (split > 1) {
+    // Split K: every workgroup stores its fp32 fragments (lane-major, 1 KiB per output
+    // pair) into partials[sidx][cb]; the last to arrive sums all splits in split order.
+    const int nwg = gridDim.x;
+    const __amdgpu_buffer_rsrc_t rp = make_buffer(partials, static_cast<uint32_t>(split) * nwg * kPairs * 1024u);
+    const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
     for (int p = 0; p < kPairs; ++p) {
-      if (p % W != wave) continue;
-      const int n = col0 + 16 * (p % TN);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * (p / TN) + 4 * (lane >> 4) + i;
-        if (row < M) y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(out[p][i]);
-      }
+      if (owner(p) != wave) continue;
+      store_fragment(rp, ((static_cast<uint32_t>(sidx) * nwg + cb) * kPairs + p) * 1024u + lane_off, out[p]);
     }
-    return;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = (arrive(&counters[cb]) == split - 1);
+    __syncthreads();
+    if (!is_last) return;
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+      if (owner(p) != wave) continue;
+      f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < split; s0 += 4) {
+        f32x4_t part[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)  // splits past `split` lie past the buffer: zeros, no access
+          part[u] = load_fragment(rp, ((static_cast<uint32_t>(s0 + u) * nwg + cb) * kPairs + p) * 1024u + lane_off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (s0 + u < split) v += (s0 + u == sidx) ? out[p] : part[u];
+      }
+      out[p] = v;
+    }
+    if (threadIdx.x == 0) rearm(&counters[cb]);
   }
 
-  // Split K: every workgroup stores its fp32 fragments (lane-major, 1 KiB per output pair)
-  // into partials[sidx][cb]; the last to arrive sums all splits in split order.
-  const int nwg = gridDim.x;
-  const __amdgpu_buffer_rsrc_t rp = make_buffer(partials, static_cast<uint32_t>(split) * nwg * kPairs * 1024u);
-  const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
+  const int c = lane & 15;
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
-    if (p % W != wave) continue;
-    store_fragment(rp, ((static_cast<uint32_t>(sidx) * nwg + cb) * kPairs + p) * 1024u + lane_off, out[p]);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) is_last = (arrive(&counters[cb]) == split - 1);
-  __syncthreads();
-  if (!is_last) return;
+    if (owner(p) != wave) continue;
+    const int mb = p / TN, tt = p % TN;
+    if (!act) {
+      const int n = 16 * (tb + tt) + c;
 #pragma unroll
-  for (int p = 0; p < kPairs; ++p) {
-    if (p % W != wave) continue;
-    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < split; s0 += 4) {
-      f32x4_t part[4];
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * mb + 4 * (lane >> 4) + i;
+        if (row < M) y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(out[p][i]);
+      }
+    } else if constexpr (H > 0) {
+      if (tt < H) {
+        const int n = 16 * (tb + tt) + c;  // output column of the [M, N / 2] result
+        const f32x4_t u = out[p + H < kPairs ? p + H : p];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)  // splits past `split` lie past the buffer: zeros, no access
-        part[u] = load_fragment(rp, ((static_cast<uint32_t>(s0 + u) * nwg + cb) * kPairs + p) * 1024u + lane_off);
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (s0 + u < split) v += (s0 + u == sidx) ? out[p] : part[u];
-    }
-    const int n = col0 + 16 * (p % TN);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 16 * (p / TN) + 4 * (lane >> 4) + i;
-      if (row < M) y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(v[i]);
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * mb + 4 * (lane >> 4) + i;
+          if (row < M) y[static_cast<size_t>(row) * (N >> 1) + n] = f32_to_bf16_bits(silu_mul(out[p][i], u[i]));
+        }
+      }
     }
   }
-  if (threadIdx.x == 0) rearm(&counters[cb]);
 }
 
 bool decode_stages_x(int M, int K, int split) {
@@ -356,7 +384,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL).total;
   decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
-      a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split);
+      a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles);
   return hipGetLastError();
   }
 }
@@ -399,8 +427,8 @@ static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int wa
 
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                             int N, int tn, int depth, int waves, int split, hipStream_t stream) {
-  const DecodeArgs a{x, packed, qzeros, scales, y, partials, counters, M, K, N, split};
+                             int N, int tn, int depth, int waves, int split, int up_tiles, hipStream_t stream) {
+  const DecodeArgs a{x, packed, qzeros, scales, y, partials, counters, M, K, N, split, up_tiles};
   switch ((M + 15) / 16) {
     case 1: return launch_decode_m<1>(a, tn, depth, waves, stream);
     case 2: return launch_decode_m<2>(a, tn, depth, waves, stream);

@@ -15,6 +15,15 @@ hipError_t launch_repack(const uint32_t* qweight, uint32_t* packed, int K, int N
 hipError_t launch_dequant_packed(const uint32_t* packed, const uint32_t* qzeros, const uint16_t* scales,
                                  uint16_t* w_out, int K, int N, hipStream_t stream);
 
+// Quantizer and packer (producer side of the format).  quantize: W [out_f, in_f] of element
+// type dtype (kDtype*) -> qweight [in_f, out_f / 8], qzeros [in_f / group_size, out_f / 8],
+// scales [in_f / group_size, out_f] of type dtype; out_f % 8 == 0, 1 <= group_size <= 128
+// dividing in_f.  pack: int32 [rows, cols] (cols % 8 == 0, values masked to 4 bits) ->
+// [rows, cols / 8] AutoAWQ words.
+hipError_t launch_quantize(const void* weight, int dtype, uint32_t* qweight, uint32_t* qzeros, void* scales,
+                           int out_f, int in_f, int group_size, hipStream_t stream);
+hipError_t launch_pack_int4(const int32_t* values, uint32_t* packed, int rows, int cols, hipStream_t stream);
+
 // Split-K decode kernel, M <= 64.  tn in {1, 2, 3, 4, 6} 16-column tiles per workgroup (tn
 // divides N / 16), depth in {1, 2, 4} groups in flight per wave, waves in {4, 8},
 // 1 <= split <= K / 128, decode_config_fits() and decode_lds_bytes() <= kDecodeMaxLds.
@@ -39,9 +48,11 @@ constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
   return decode_ring_regs(mb, tn, depth, xl) <= 176;
 }
 
+// up_tiles: 0 for the plain GEMM (y is [M, N]); N / 32 for the fused SiLU(gate) * up of a
+// gate|up weight (tn even, N % 128 == 0, y is [M, N / 2]).
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                             int N, int tn, int depth, int waves, int split, hipStream_t stream);
+                             int N, int tn, int depth, int waves, int split, int up_tiles, hipStream_t stream);
 
 // LDS-tiled MFMA GEMM.  A tile shape code selects the wave grid: nwm waves along M x nwn
 // along N, each owning tw 16-column layout tiles and 16 wm rows, so the workgroup tile is
@@ -55,9 +66,9 @@ TileShape tile_shape(int shape);
 // Compiled: (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
-// unused when split == 1).
+// unused when split == 1).  up_tiles as for the decode kernel (N % 128 == 0 when fused).
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                            const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int shape, int occ, int split, hipStream_t stream);
+                           int N, int wm, int shape, int occ, int split, int up_tiles, hipStream_t stream);
 
 }  // namespace w4a16

@@ -21,6 +21,8 @@
 // operands in that XCD's L2.  With split > 1 the workgroups write fp32 partials and the
 // last to arrive at a tile (atomic counter) sums them in split order; the counter is
 // re-armed to zero.
+#include <type_traits>
+
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
 
@@ -66,15 +68,17 @@ struct BSources {
   __amdgpu_buffer_rsrc_t w, s, z;
 };
 
+// The wave's tiles are t0 + tt, plus dt for tt >= TW / 2 (dt = 0 for the plain GEMM; for
+// the fused gate/up product the second half are the up tiles of the first half's gate tiles).
 template <int TW>
 __device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src, int g, bool valid, int N, int t0,
-                                             int lane) {
+                                             int dt, int lane) {
   const int NT = N / kTileCols;
   const int c = lane & 15;
   const uint32_t oob = valid ? 0u : kOutOfRange;
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt) {
-    const int t = t0 + tt;
+    const int t = t0 + tt + (tt >= TW / 2 ? dt : 0);
     const uint32_t wo = valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : kOutOfRange;
     b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
     const int col = kTileCols * t + c;
@@ -168,7 +172,8 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
                                                                    uint16_t* __restrict__ y,
                                                                    float* __restrict__ partials,
                                                                    int* __restrict__ counters, int M, int K, int N,
-                                                                   int split, int m_blocks, int n_blocks) {
+                                                                   int split, int m_blocks, int n_blocks,
+                                                                   int up_tiles) {
   constexpr int NW = NWM * NWN;  // waves per workgroup
   constexpr int BM = 16 * WM * NWM;
   constexpr int BN = 16 * TW * NWN;
@@ -214,9 +219,16 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
   const int g_begin = (G * sidx) / split;
   const int g_end = (G * (sidx + 1)) / split;
   const int row0 = mbk * BM;
-  const int col_w = nbk * BN + 16 * TW * wn;  // first column of this wave
+  // Plain: the wave computes output columns [col_w, col_w + 16 TW) = layout tiles t0 + tt.
+  // Fused SiLU(gate) * up (up_tiles = N / 32): output columns [col_w, col_w + 8 TW) of the
+  // [M, N / 2] result, from gate tiles t0 + tt and up tiles t0 + up_tiles + tt, tt < TW / 2.
+  static_assert(TW % 2 == 0, "the fused product pairs the two halves of a wave's tiles");
+  const bool act = up_tiles != 0;
+  const int n_out = act ? N / 2 : N;
+  const int col_w = act ? nbk * (BN / 2) + 8 * TW * wn : nbk * BN + 16 * TW * wn;  // first output column
   const int t0 = col_w / kTileCols;
-  const bool active = col_w < N;  // wave-uniform (N % 64 == 0): the last n-block may be partly past N
+  const int dt = act ? up_tiles - TW / 2 : 0;
+  const bool active = col_w < n_out;  // wave-uniform (n_out % 64 == 0): the last n-block may be partly past it
 
   f32x4_t acc[WM][TW];
 #pragma unroll
@@ -243,7 +255,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
   auto issue = [&](int slot, int item) {
     const bool valid = item < n_items;
     issue_a_stage<NI, NW>(rx, stage(slot), row0, M, K, g_begin + item, valid, wave, lane);
-    load_b_group<TW>(ring[slot], bsrc, g_begin + item, valid && active, N, t0, lane);
+    load_b_group<TW>(ring[slot], bsrc, g_begin + item, valid && active, N, t0, dt, lane);
   };
 #pragma unroll
   for (int q = 0; q < P; ++q) issue(q, q);
@@ -317,50 +329,73 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
   }
 
   if (!active) return;
-  // Epilogue: bf16 through LDS (row-major 16 WM x 16 TW per wave: rows of CPR 16-byte
-  // chunks swizzled by row), then 16-byte coalesced stores.  The stages are free after the
-  // last barrier.
-  constexpr int WR = 16 * WM;      // rows of a wave
-  constexpr int CPR = 2 * TW;      // 16-byte chunks per row
-  constexpr int PITCH = 16 * CPR;  // bytes per row
-  constexpr int kWavesPerStage = kStage / (WR * PITCH);
-  static_assert(kWavesPerStage >= 1 && kWavesPerStage * S >= NW, "epilogue staging exceeds the stages");
-  uint8_t* ep = stage(wave / kWavesPerStage) + (wave % kWavesPerStage) * (WR * PITCH);
-#pragma unroll
-  for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-    for (int tt = 0; tt < TW; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * mt + 4 * (lane >> 4) + i;
-        const int c = 16 * tt + (lane & 15);
-        const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
-        *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][tt][i]);
-      }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  constexpr int kRowsPerRound = 64 / CPR;
+  // Epilogue: bf16 through LDS (row-major 16 WM rows x the wave's output columns: rows of
+  // CPR 16-byte chunks swizzled by row), then 16-byte coalesced stores.  The stages are free
+  // after the last barrier.
+  constexpr int WR = 16 * WM;  // rows of a wave
+  constexpr int kStageRows = kStage / (WR * 32 * TW);
+  static_assert(kStageRows >= 1 && kStageRows * S >= NW, "epilogue staging exceeds the stages");
+  uint8_t* ep = stage(wave / kStageRows) + (wave % kStageRows) * (WR * 32 * TW);
+  auto store_rows = [&](auto cpr_tag) {
+    constexpr int CPR = decltype(cpr_tag)::value;
+    constexpr int PITCH = 16 * CPR;
+    constexpr int kRowsPerRound = 64 / CPR;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll 4
-  for (int round = 0; round < WR / kRowsPerRound; ++round) {
-    const int r = kRowsPerRound * round + lane / CPR;
-    const int q = lane % CPR;
-    const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + ((q ^ (r % CPR)) << 4));
-    const int row = row0 + wm * WR + r;
-    if (row < M) *reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * N + col_w + 8 * q) = v;
+    for (int round = 0; round < WR / kRowsPerRound; ++round) {
+      const int r = kRowsPerRound * round + lane / CPR;
+      const int q = lane % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + ((q ^ (r % CPR)) << 4));
+      const int row = row0 + wm * WR + r;
+      if (row < M) *reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * n_out + col_w + 8 * q) = v;
+    }
+  };
+  if (!act) {
+    constexpr int CPR = 2 * TW;  // 16-byte chunks per row
+    constexpr int PITCH = 16 * CPR;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * mt + 4 * (lane >> 4) + i;
+          const int c = 16 * tt + (lane & 15);
+          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][tt][i]);
+        }
+    store_rows(std::integral_constant<int, CPR>{});
+  } else {
+    constexpr int H = TW / 2;
+    constexpr int CPR = TW;  // half the columns
+    constexpr int PITCH = 16 * CPR;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < H; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * mt + 4 * (lane >> 4) + i;
+          const int c = 16 * tt + (lane & 15);
+          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul(acc[mt][tt][i], acc[mt][tt + H][i]));
+        }
+    store_rows(std::integral_constant<int, CPR>{});
   }
 }
 
 template <int WM, int TW, int NWM, int NWN, int OCC>
 static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                                 const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                                int N, int split, hipStream_t stream) {
+                                int N, int split, int up_tiles, hipStream_t stream) {
   constexpr int BM = 16 * WM * NWM;
   constexpr int BN = 16 * TW * NWN;
   const int m_blocks = (M + BM - 1) / BM;
   const int n_blocks = (N + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
   tile_kernel<WM, TW, NWM, NWN, OCC><<<grid, 64 * NWM * NWN, 0, stream>>>(
-      x, packed, qzeros, scales, y, partials, counters, M, K, N, split, m_blocks, n_blocks);
+      x, packed, qzeros, scales, y, partials, counters, M, K, N, split, m_blocks, n_blocks, up_tiles);
   return hipGetLastError();
 }
 
@@ -388,12 +423,12 @@ bool tile_config_compiled(int wm, int shape, int occ) {
 
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                            const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int shape, int occ, int split, hipStream_t stream) {
+                           int N, int wm, int shape, int occ, int split, int up_tiles, hipStream_t stream) {
   const TileShape ts = tile_shape(shape);
 #define W4A16_TILE_LAUNCH(WM_, TW_, NWM_, NWN_, OCC_)                                                           \
   if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_)                            \
     return launch_tile_t<WM_, TW_, NWM_, NWN_, OCC_>(x, packed, qzeros, scales, y, partials, counters, M, K, N, \
-                                                     split, stream);
+                                                     split, up_tiles, stream);
   W4A16_TILE_CONFIGS(W4A16_TILE_LAUNCH)
 #undef W4A16_TILE_LAUNCH
   return hipErrorInvalidValue;

@@ -131,6 +131,16 @@ class MergedColumnParallelLinear(ColumnParallelLinear):
         loaded_weight = loaded_weight.chunk(self.tp_size, output_dim)[self.tp_rank]
         param_data.copy_(loaded_weight)
 
+    def forward_silu_and_mul(self, x: torch.Tensor) -> torch.Tensor:
+        """``SiluAndMul()(self(x))`` for a [gate, up] layer of two equal shards
+        (qwen3.py:126-130 with activation.py:8-11), fused into the AWQ GEMM epilogue: the
+        [M, 2 I] intermediate is never written."""
+        if len(self.output_sizes) != 2 or self.output_sizes[0] != self.output_sizes[1]:
+            raise ValueError("fused SiLU * up needs exactly two equal output shards (gate, up)")
+        if self.quant_method is None or not hasattr(self.quant_method, "apply_silu_and_mul"):
+            raise ValueError("fused SiLU * up is implemented for the AWQ HIP backend only")
+        return self.quant_method.apply_silu_and_mul(self, x)
+
 
 class QKVParallelLinear(ColumnParallelLinear):
 

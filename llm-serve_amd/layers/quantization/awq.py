@@ -11,6 +11,9 @@ Same names, argument meaning and error behaviour as the reference:
 * ``dequantize_awq_gemm``                          awq.py:235-248
 * ``awq_linear`` (the reference's ``awq_cuda_linear`` / ``awq_reference_linear`` role,
   awq_cuda.py:141-185, awq.py:251-276)
+* ``awq_linear_silu_mul`` / ``AWQLinearMethod.apply_silu_and_mul``: the gate|up GEMM with
+  the reference's ``SiluAndMul`` (activation.py:8-11, applied at qwen3.py:126-130) fused
+  into its epilogue; no reference counterpart as one call
 
 There is one execution backend, the HIP library (libw4a16.so): every tensor operation
 runs there and raises when the library or a GPU is missing -- nothing falls back to a CPU
@@ -156,6 +159,14 @@ class AWQLinearMethod:
         layer.scales.output_dim = 1
         layer.scales.input_dim = 0
 
+    def apply_silu_and_mul(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
+        """``SiluAndMul()(self.apply(layer, inputs))`` as one kernel, for a layer whose output
+        is [gate | up] of equal widths (qwen3.py:126-130)."""
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear_silu_mul(inputs, layer.awq_qweight, layer.awq_qzeros, layer.scales,
+                                   group_size=self.config.group_size)
+
     def apply(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
         if not hasattr(layer, "awq_qweight"):
             raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
@@ -239,14 +250,8 @@ def _aligned16(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0
 
 
-def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
-               *, group_size: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """y[..., N] = inputs[..., K] @ W on the HIP kernels (bf16 in/out, fp32 accumulation).
-
-    ``packed_qweight`` comes from ``repack_awq_qweight``; ``qzeros`` [K/128, N/8] and
-    ``scales`` [K/128, N] are the AutoAWQ tensors.  Leading dimensions of ``inputs`` are
-    flattened into M.  ``workspace`` (uint8, zero-filled when allocated) overrides the
-    per-stream shared one."""
+def _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size):
+    """Shared argument checks of the GEMM entry points; returns (x [M, K], lead dims, K, N)."""
     if not inputs.is_floating_point():
         raise ValueError("AWQ activations must use a floating dtype")
     if inputs.dtype != scales.dtype:
@@ -275,6 +280,18 @@ def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch
         x = x.contiguous()
         if not _aligned16(x):
             x = x.clone()
+    return x, lead, k, n
+
+
+def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+               *, group_size: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y[..., N] = inputs[..., K] @ W on the HIP kernels (bf16 in/out, fp32 accumulation).
+
+    ``packed_qweight`` comes from ``repack_awq_qweight``; ``qzeros`` [K/128, N/8] and
+    ``scales`` [K/128, N] are the AutoAWQ tensors.  Leading dimensions of ``inputs`` are
+    flattened into M.  ``workspace`` (uint8, zero-filled when allocated) overrides the
+    per-stream shared one."""
+    x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
     m = x.shape[0]
     y = torch.empty((m, n), dtype=inputs.dtype, device=inputs.device)
     if m == 0:
@@ -284,6 +301,28 @@ def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch
         workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
     library.gemm(x, packed_qweight, qzeros, scales.contiguous(), y, k, n, workspace, group_size)
     return y.reshape(*lead, n)
+
+
+def awq_linear_silu_mul(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor,
+                        scales: torch.Tensor, *, group_size: int,
+                        workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """SiLU(g) * u over [g | u] = inputs @ W for a gate|up weight of width N (first N/2
+    columns gate, last N/2 up, as MergedColumnParallelLinear loads them): the reference's
+    ``SiluAndMul`` (activation.py:8-11) applied to ``awq_linear``'s output, computed in the
+    GEMM epilogue from the fp32 accumulators and rounded once to bf16.  Returns
+    [..., N/2]; N must be divisible by 128."""
+    x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
+    if n % 128:
+        raise ValueError("AWQ fused SiLU * up requires the gate|up output size to be divisible by 128")
+    m = x.shape[0]
+    y = torch.empty((m, n // 2), dtype=inputs.dtype, device=inputs.device)
+    if m == 0:
+        return y.reshape(*lead, n // 2)
+    library = lib()
+    if workspace is None:
+        workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
+    library.gemm_silu_mul(x, packed_qweight, qzeros, scales.contiguous(), y, k, n, workspace, group_size)
+    return y.reshape(*lead, n // 2)
 
 
 def awq_regime(m: int, k: int, n: int) -> str:

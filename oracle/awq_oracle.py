@@ -21,6 +21,12 @@ What it restates (reference = HGinkgo/LLM-Serve):
 * ``awq_linear_ref``                          llmserve/layers/quantization/awq.py:251-276
     y = matmul(x, W) with W from the dequant above, accumulated in fp32 (the
     reference's BLAS) or fp64 (a tighter reference for tolerance checks).
+* ``silu_and_mul_ref``                        llmserve/layers/activation.py:8-11
+    x, y = chunk(2, -1); silu(x) * y, evaluated in fp64 on the bf16 inputs (the
+    reference's compiled kernel computes in fp32 and rounds once to bf16).
+* ``awq_gate_up_silu_mul_ref``                llmserve/models/qwen3.py:126-130
+    SiluAndMul(gate_up_proj(x)): the GEMM (fp64 accumulation) rounded to bf16 as the
+    reference's layer returns it (or, optionally, unrounded), then ``silu_and_mul_ref``.
 * ``quantize_awq_weight``                     llmserve/quantization/awq_calibration.py:35-62
     the producer side of the format, used for known-answer tests and synthetic data.
 
@@ -182,11 +188,39 @@ def awq_linear_bf16_bits(x_bits, qweight, qzeros, scales_bits, group_size: int) 
     return f32_to_bf16_bits(y)
 
 
+# ------------------------------------------------------------------ activation
+def silu_and_mul_ref(gate_up) -> np.ndarray:
+    """SiluAndMul (activation.py:8-11): the last axis splits into halves x | y (first half
+    x), result silu(x) * y = x / (1 + exp(-x)) * y, in float64."""
+    a = np.asarray(gate_up, dtype=np.float64)
+    if a.shape[-1] % 2:
+        raise ValueError("SiluAndMul needs an even last dimension")
+    half = a.shape[-1] // 2
+    x, y = a[..., :half], a[..., half:]
+    with np.errstate(over="ignore"):
+        sig = 1.0 / (1.0 + np.exp(-x))
+    return x * sig * y
+
+
+def awq_gate_up_silu_mul_ref(x_bits, qweight, qzeros, scales_bits, group_size: int,
+                             round_intermediate: bool = True) -> np.ndarray:
+    """SiluAndMul(gate_up_proj(x)) (qwen3.py:126-130), float64 [..., N / 2].
+
+    round_intermediate=True: the gate|up GEMM rounded to bf16 as the reference's layer
+    returns it, then ``silu_and_mul_ref`` (the reference's two steps).  False: the same
+    composition without that rounding (the exact value a fused kernel approximates)."""
+    y = awq_linear_ref(x_bits, qweight, qzeros, scales_bits, group_size, accum="f64")
+    if round_intermediate:
+        y = bf16_bits_to_f32(f32_to_bf16_bits(y.astype(np.float32)))
+    return silu_and_mul_ref(y)
+
+
 # ------------------------------------------------------------------- producer
 def quantize_awq_weight(weight, group_size: int = 128, out_dtype: str = "bf16"):
     """[out_features, in_features] float -> (qweight, qzeros, scales) in AutoAWQ GEMM
     layout (awq_calibration.py:35-62).  Scales are returned as bf16 bits when
-    out_dtype == 'bf16', else as float32."""
+    out_dtype == 'bf16', as float16 when 'f16' (RNE, as torch's .to(float16)), else as
+    float32."""
     w = np.asarray(weight)
     if w.ndim != 2:
         raise ValueError("AWQ quantization expects a two-dimensional weight tensor")
@@ -211,6 +245,8 @@ def quantize_awq_weight(weight, group_size: int = 128, out_dtype: str = "bf16"):
     s_t = np.ascontiguousarray(scales.T)
     if out_dtype == "bf16":
         return qweight, qzeros, f32_to_bf16_bits(s_t)
+    if out_dtype == "f16":
+        return qweight, qzeros, s_t.astype(np.float16)
     return qweight, qzeros, s_t
 
 

@@ -38,7 +38,7 @@ def test_binding_signatures_cover_the_header(pkg):
 
 def test_abi_version_and_empty_error(pkg):
     L = pkg.lib()
-    assert L.dll.w4a16_abi_version() == 1
+    assert L.dll.w4a16_abi_version() == 2
     assert isinstance(L.last_error(), str)
 
 
@@ -136,3 +136,41 @@ def test_forced_config_validation(pkg):
     # split > 1 without workspace
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 4, None, 0, None) == 4
     assert "workspace" in L.last_error()
+
+
+def test_silu_mul_entry_points_validate_without_launching(pkg):
+    """The fused gate|up entry points: N % 128, even decode tile counts, and the workspace
+    query covering both the plain and the fused plan (no kernel launches)."""
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    g = L.dll.w4a16_gemm_silu_mul
+    assert g(p, p, p, p, p, 16, 4096, 192, 128, None, 0, None) == 2  # 192 % 128
+    assert "divisible by 128" in L.last_error()
+    assert g(None, None, None, None, None, 0, 4096, 24576, 128, None, 0, None) == 0  # M == 0
+    assert g(None, None, None, None, None, 4, 4096, 24576, 128, None, 0, None) == 1  # null pointers
+    f = L.dll.w4a16_gemm_silu_mul_config
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 1, 4, 2, 1, None, 0, None) == 1  # odd tile count
+    assert "even" in L.last_error()
+    assert f(p, p, p, p, p, 16, 4096, 4160, 128, 1, 2, 4, 2, 1, None, 0, None) == 2  # 4160 % 128
+    for k, n in QWEN3.values():
+        for m in (1, 4, 16, 64, 512, 2048):
+            assert L.workspace_bytes(m, k, n) >= (L.split_k(m, k, n) > 1) * m * n * 4
+
+
+def test_quantize_and_pack_validate_without_launching(pkg):
+    L = pkg.lib()
+    q = L.dll.w4a16_quantize
+    assert q(None, 0, None, None, None, 0, 128, 128, None) == 1                  # sizes
+    assert q(None, 5, None, None, None, 8, 128, 128, None) == 1                  # dtype
+    assert "dtype" in L.last_error()
+    assert q(None, 0, None, None, None, 8, 256, 256, None) == 2                  # group > 128
+    assert q(None, 0, None, None, None, 8, 100, 64, None) == 2                   # in % group
+    assert q(None, 0, None, None, None, 12, 128, 128, None) == 2                 # out % 8
+    assert "output size" in L.last_error()
+    assert q(None, 0, None, None, None, 8, 131072, 1, None) == 2                 # grid rows
+    assert q(None, 2, None, None, None, 8, 128, 128, None) == 1                  # null pointers
+    pk = L.dll.w4a16_pack_int4
+    assert pk(None, None, 2, 12, None) == 2
+    assert pk(None, None, 0, 8, None) == 1
+    assert pk(None, None, 2, 8, None) == 1

@@ -1,0 +1,117 @@
+"""GPU parity of the AutoAWQ producer kernels (w4a16_quantize, w4a16_pack_int4) with the
+reference's quantize_awq_weight / _pack_int4 (llmserve/quantization/awq_calibration.py:19-62):
+bit-exact qweight, qzeros and scales against the oracle, the reference's known-answer tests
+(tests/test_awq_quantizer.py:8-72), and round-trip properties at full Qwen3-8B size."""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from awq_helpers import bits_of
+from oracle import awq_oracle as ora
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cal(gpu_lib):
+    return importlib.import_module("llm-serve_amd.quantization.awq_calibration")
+
+
+def scale_array(t: torch.Tensor) -> np.ndarray:
+    return bits_of(t) if t.dtype == torch.bfloat16 else t.cpu().numpy()
+
+
+ORACLE_DTYPE = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def test_reference_roundtrip_kat(cal, gpu_lib):
+    """tests/test_awq_quantizer.py:8-41: [[-7, 8, -14, 16]] x 8, group 2 -> scales [1, 2],
+    exact bf16 round trip through the dequant kernel."""
+    w = torch.tensor([[-7.0, 8.0, -14.0, 16.0]] * 8, dtype=torch.bfloat16, device="cuda")
+    p = cal.quantize_awq_weight(w, group_size=2)
+    assert p.qweight.shape == (4, 1) and p.qzeros.shape == (2, 1) and p.scales.shape == (2, 8)
+    assert p.qweight.dtype == torch.int32 and p.qzeros.dtype == torch.int32 and p.scales.dtype == torch.bfloat16
+    assert torch.equal(p.scales.cpu(), torch.tensor([[1.0] * 8, [2.0] * 8], dtype=torch.bfloat16))
+    restored = gpu_lib.dequant(p.qweight, p.qzeros, p.scales, 2).t()
+    assert torch.equal(restored, w)
+
+
+def test_ties_round_half_to_even(cal):
+    row = torch.tensor([0.0, 15.0, 2.5, 3.5, 4.5, 13.5, 7.0, 8.0])
+    w = row.repeat(8, 1).cuda()
+    p = cal.quantize_awq_weight(w, group_size=8)
+    assert torch.all(p.scales == 1.0) and torch.all(p.qzeros == 0)
+    q = ora.unpack_awq_int4(p.qweight.cpu().numpy())[:, 0]
+    np.testing.assert_array_equal(q, [0, 15, 2, 4, 4, 14, 7, 8])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("out_f,in_f,gs", [(136, 256, 128), (64, 64, 2), (8, 384, 128), (1000, 512, 64),
+                                           (200, 96, 32)])
+def test_bit_exact_against_oracle(cal, dtype, out_f, in_f, gs):
+    """Partial 64-row workgroups (136, 200, 1000 rows), small and large groups, every
+    weight dtype; weights with outlier rows and a constant row (max - min = 0 -> 1e-5)."""
+    gen = torch.Generator().manual_seed(out_f + in_f + gs)
+    w = torch.randn((out_f, in_f), generator=gen) * 0.05
+    w[3] *= 40.0
+    w[5] = 0.25
+    w = w.to(dtype)
+    print(f"quantize {dtype} {out_f}x{in_f} g{gs}", flush=True)
+    p = cal.quantize_awq_weight(w.cuda(), group_size=gs)
+    qw, qz, sc = ora.quantize_awq_weight(w.float().numpy(), group_size=gs, out_dtype=ORACLE_DTYPE[dtype])
+    np.testing.assert_array_equal(p.qweight.cpu().numpy(), qw)
+    np.testing.assert_array_equal(p.qzeros.cpu().numpy(), qz)
+    assert p.scales.dtype == dtype
+    np.testing.assert_array_equal(scale_array(p.scales), sc)
+
+
+def test_explicit_asymmetric_reference(cal, gpu_lib):
+    """tests/test_awq_quantizer.py:43-72 (torch seed 7, randn(16, 128) fp32): the dequant of
+    the quantized weight matches the explicit formula within rtol = atol = 0.01."""
+    torch.manual_seed(7)
+    weight = torch.randn(16, 128, dtype=torch.float32)
+    mn, mx = weight.amin(dim=1, keepdim=True), weight.amax(dim=1, keepdim=True)
+    s = (mx - mn).clamp(min=1e-5) / 15
+    z = (-torch.round(mn / s)).clamp(0, 15)
+    expected = (torch.clamp(torch.round(weight / s) + z, 0, 15) - z) * s
+    p = cal.quantize_awq_weight(weight.cuda(), group_size=128)
+    actual = gpu_lib.dequant(p.qweight, p.qzeros, p.scales.to(torch.bfloat16), 128).t()
+    torch.testing.assert_close(actual.float().cpu(), expected, rtol=0.01, atol=0.01)
+
+
+def test_full_size_roundtrip_and_oracle_rows(cal, gpu_lib):
+    """Qwen3-8B down projection as a [4096, 12288] bf16 weight: dequantized values lie within
+    half a scale step of the weights they came from, plus the bf16 roundings of s (up to
+    15 s 2^-9) and of the result -- all but the rare exact ties of round(max / s) that the
+    reference's clamp to 15 moves by one more step -- and the first 256 output rows match
+    the oracle bit for bit."""
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    w = (torch.randn((4096, 12288), device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    p = cal.quantize_awq_weight(w, group_size=128)
+    deq = gpu_lib.dequant(p.qweight, p.qzeros, p.scales, 128).t().float()
+    s = p.scales.float().t().repeat_interleave(128, dim=1)
+    err = (deq - w.float()).abs()
+    rounding = 2 ** -4 * s + 2 ** -8 * deq.abs()
+    assert float((err <= 0.5 * s + rounding).float().mean()) >= 1 - 1e-6
+    assert bool(torch.all(err <= 1.5 * s + rounding))
+    rows = w[:256].float().cpu().numpy()
+    qw, qz, sc = ora.quantize_awq_weight(rows, group_size=128, out_dtype="bf16")
+    np.testing.assert_array_equal(p.qweight[:, :32].cpu().numpy(), qw)
+    np.testing.assert_array_equal(p.qzeros[:, :32].cpu().numpy(), qz)
+    np.testing.assert_array_equal(bits_of(p.scales[:, :256]), sc)
+
+
+def test_pack_int4_matches_oracle_and_reference_errors(cal):
+    rng = np.random.default_rng(4)
+    v = rng.integers(0, 16, size=(37, 64))
+    packed = cal.pack_int4(torch.from_numpy(v).cuda())
+    np.testing.assert_array_equal(packed.cpu().numpy(), ora.pack_awq_int4(v))
+    # the round-trip KAT of tests/test_awq_reference.py:103-116
+    kat = torch.tensor([list(range(16)), list(range(15, -1, -1))], dtype=torch.int32, device="cuda")
+    np.testing.assert_array_equal(ora.unpack_awq_int4(cal.pack_int4(kat).cpu().numpy()), kat.cpu().numpy())
+    with pytest.raises(ValueError, match=r"\[0, 15\]"):
+        cal.pack_int4(torch.full((1, 8), 16, dtype=torch.int32, device="cuda"))
+    with pytest.raises(TypeError, match="integer"):
+        cal.pack_int4(torch.zeros((1, 8), device="cuda"))

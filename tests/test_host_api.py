@@ -191,3 +191,38 @@ def test_unpack_rejects_bad_input(awq):
         awq.unpack_awq_int4(torch.zeros(8, dtype=torch.int32))
     with pytest.raises(ValueError, match="int32"):
         awq.unpack_awq_int4(torch.zeros((1, 8), dtype=torch.int64))
+
+
+# ---------------------------------------------------------------- quantizer contract
+@pytest.fixture(scope="module")
+def cal(pkg):
+    import importlib
+
+    return importlib.import_module("llm-serve_amd.quantization.awq_calibration")
+
+
+def test_quantizer_rejects_unsupported_shapes(cal):
+    """tests/test_awq_quantizer.py:74-87 (same messages), checked before any device work."""
+    with pytest.raises(ValueError, match="two-dimensional"):
+        cal.quantize_awq_weight(torch.zeros(8), group_size=2)
+    with pytest.raises(ValueError, match="floating"):
+        cal.quantize_awq_weight(torch.zeros((8, 4), dtype=torch.int32), group_size=2)
+    with pytest.raises(ValueError, match="input size"):
+        cal.quantize_awq_weight(torch.zeros((8, 5)), group_size=2)
+    with pytest.raises(ValueError, match="output size"):
+        cal.quantize_awq_weight(torch.zeros((7, 4)), group_size=2)
+    with pytest.raises(ValueError, match="positive"):
+        cal.quantize_awq_weight(torch.zeros((8, 4)), group_size=0)
+
+
+def test_quantizer_and_packer_have_no_cpu_path(cal):
+    with pytest.raises(ValueError, match="GPU"):
+        cal.quantize_awq_weight(torch.zeros((8, 4)), group_size=2)
+    with pytest.raises(ValueError, match="GPU"):
+        cal.pack_int4(torch.zeros((2, 8), dtype=torch.int32))
+    with pytest.raises(ValueError, match="2D"):
+        cal.pack_int4(torch.zeros(8, dtype=torch.int32))
+    with pytest.raises(ValueError, match="divisible by 8"):
+        cal.pack_int4(torch.zeros((2, 6), dtype=torch.int32))
+    with pytest.raises(TypeError, match="integer"):
+        cal.pack_int4(torch.zeros((2, 8)))

@@ -299,3 +299,81 @@ def test_metric_floor_behaviour():
     assert ora.gemm_rel_err(r, r) == 0.0
     # rms(r) = sqrt(0.5): the two small entries are judged against that floor
     assert ora.gemm_rel_err(r + 0.01, r) == pytest.approx(0.01 / np.sqrt(0.5), rel=1e-9)
+
+
+# ------------------------------------------------------------------ SiluAndMul
+def test_silu_and_mul_closed_forms_and_half_order():
+    """activation.py:8-11.  silu(0) = 0; silu(ln 3) = (3/4) ln 3; silu(x) - silu(-x) = x;
+    the first half is the gated input (a swapped split fails the asymmetric rows)."""
+    ln3 = float(np.log(3.0))
+    gate_up = np.array([[0.0, ln3, 2.0, 1.0, 1.0, 5.0]])
+    out = ora.silu_and_mul_ref(gate_up)
+    sig2 = 1.0 / (1.0 + np.exp(-2.0))
+    np.testing.assert_allclose(out, [[0.0, 0.75 * ln3, 2.0 * sig2 * 5.0]], rtol=1e-15, atol=0)
+    xs = np.linspace(-8.0, 8.0, 33)
+    pos = ora.silu_and_mul_ref(np.concatenate([xs, np.ones_like(xs)])[None])[0]
+    neg = ora.silu_and_mul_ref(np.concatenate([-xs, np.ones_like(xs)])[None])[0]
+    np.testing.assert_allclose(pos - neg, xs, rtol=1e-14, atol=1e-14)
+    # saturation: silu(-inf) * u = -0, silu(+large) = x; NaN propagates
+    big = ora.silu_and_mul_ref(np.array([[-1e4, 1e4, np.nan, 3.0, 2.0, 1.0]]))
+    assert big[0, 0] == 0.0 and big[0, 1] == 2e4 and np.isnan(big[0, 2])
+    with pytest.raises(ValueError, match="even"):
+        ora.silu_and_mul_ref(np.zeros((2, 3)))
+
+
+def test_silu_and_mul_matches_torch_cpu():
+    """Against torch's own silu on the CPU in float64 (the library routine the reference
+    calls, activation.py:11)."""
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((7, 64)) * 4
+    t = torch.from_numpy(a)
+    want = (torch.nn.functional.silu(t[:, :32]) * t[:, 32:]).numpy()
+    np.testing.assert_allclose(ora.silu_and_mul_ref(a), want, rtol=1e-13, atol=1e-13)
+
+
+def test_gate_up_silu_mul_composes_the_rounded_gemm():
+    """qwen3.py:126-130: SiluAndMul over the gate|up GEMM output, rounded to bf16 by torch's
+    own conversion (the reference's layer output dtype) or left unrounded."""
+    p = ora.make_problem(seed=8, m=3, k=256, n=128)
+    y = torch.from_numpy(ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128))
+    for rounded in (True, False):
+        t = y.float().to(torch.bfloat16).double() if rounded else y
+        want = (torch.nn.functional.silu(t[:, :64]) * t[:, 64:]).numpy()
+        got = ora.awq_gate_up_silu_mul_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128,
+                                           round_intermediate=rounded)
+        assert got.shape == (3, 64)
+        np.testing.assert_allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+def test_quantizer_ties_round_half_to_even():
+    """A row with min 0 and max 15 has s = 1 exactly and z = 0, so q = round(w): the ties
+    2.5, 3.5, 4.5, 13.5 go to 2, 4, 4, 14 under torch.round's half-to-even (half-up would
+    give 3, 4, 5, 14)."""
+    row = np.array([0.0, 15.0, 2.5, 3.5, 4.5, 13.5, 7.0, 8.0], dtype=np.float32)
+    w = np.tile(row, (8, 1))  # 8 output rows, one group of 8 inputs
+    qw, qz, sb = ora.quantize_awq_weight(w, group_size=8, out_dtype="f32")
+    assert np.all(sb == 1.0)
+    assert np.all(ora.unpack_awq_int4(qz) == 0)
+    np.testing.assert_array_equal(ora.unpack_awq_int4(qw)[:, 0], [0, 15, 2, 4, 4, 14, 7, 8])
+
+
+def test_quantizer_matches_torch_cpu_arithmetic():
+    """The reference's steps (awq_calibration.py:50-62) evaluated by torch on the CPU -- its
+    amin/amax, clamp, division and round -- bit for bit against the oracle, for fp32, bf16
+    and fp16 weights (scales cast back to the weight dtype)."""
+    gen = torch.Generator().manual_seed(5)
+    for dtype, out in ((torch.float32, "f32"), (torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        w = (torch.randn((24, 256), generator=gen) * 0.05).to(dtype)
+        grouped = w.to(torch.float32).reshape(24, 2, 128)
+        mn, mx = grouped.amin(dim=-1), grouped.amax(dim=-1)
+        s = (mx - mn).clamp(min=1e-5) / 15.0
+        z = (-torch.round(mn / s)).clamp(0, 15)
+        q = (torch.round(grouped / s.unsqueeze(-1)) + z.unsqueeze(-1)).clamp(0, 15).to(torch.int32).reshape(24, 256)
+        qw, qz, sc = ora.quantize_awq_weight(w.float().numpy(), group_size=128, out_dtype=out)
+        np.testing.assert_array_equal(ora.unpack_awq_int4(qw), q.t().numpy())
+        np.testing.assert_array_equal(ora.unpack_awq_int4(qz), z.to(torch.int32).t().numpy())
+        want_s = s.t().contiguous().to(dtype)
+        if out == "bf16":
+            np.testing.assert_array_equal(sc, want_s.view(torch.int16).numpy().view(np.uint16))
+        else:
+            np.testing.assert_array_equal(sc, want_s.numpy())
