@@ -407,9 +407,18 @@ def read_traffic(path: str = TRAFFIC_FILE):
 
 def profile_point(lib, spec: str, steps: int, dev) -> int:
     """Counter/trace workload: one 256 MiB bf16 copy (3x) for calibration, then `steps`
-    direct launches of one decode or prefill point over rotating weights."""
+    direct launches of one decode or prefill point over rotating weights.  SHAPE+silu:M
+    launches the fused SiLU * up GEMM of that (gate|up) shape; quantize:0 launches the
+    quantizer over a [24576, 4096] bf16 weight."""
     name, m = spec.split(":")
     m = int(m)
+    if name == "quantize":
+        q = quantize_throughput(lib, dev, torch.cuda.Stream(dev), steps)
+        print(json.dumps({"profile_point": spec, "launches": steps + 2, **q}))
+        return 0
+    fused = name.endswith("+silu")
+    name = name.removesuffix("+silu")
+    entry = lib.dll.w4a16_gemm_silu_mul if fused else lib.dll.w4a16_gemm
     k, n = SHAPES[name]
     src = torch.ones(CALIBRATION_BYTES // 2, dtype=torch.bfloat16, device=dev)
     dst = torch.empty_like(src)
@@ -422,16 +431,18 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
     x = torch.randn((m, k), device=dev).to(torch.bfloat16)
     p = Point(lib, name, m, k, n, weights, x)
     stream = torch.cuda.current_stream(dev)
-    p.launch_all(stream.cuda_stream)  # warm-up
+    for packed, qzeros, scales in weights:  # warm-up
+        if entry(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), p.y.data_ptr(), m, k, n,
+                 128, p.ws.data_ptr() if p.ws_len else None, p.ws_len, stream.cuda_stream) != 0:
+            raise RuntimeError(lib.last_error())
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     done = 0
     while done < steps:
         for packed, qzeros, scales in weights[: steps - done]:
-            rc = lib.dll.w4a16_gemm(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
-                                    p.y.data_ptr(), m, k, n, 128, p.ws.data_ptr() if p.ws_len else None,
-                                    p.ws_len, stream.cuda_stream)
+            rc = entry(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), p.y.data_ptr(), m,
+                       k, n, 128, p.ws.data_ptr() if p.ws_len else None, p.ws_len, stream.cuda_stream)
             if rc != 0:
                 raise RuntimeError(lib.last_error())
             done += 1

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_kernel(const void* __r
                                                                  uint32_t* __restrict__ qweight,
                                                                  uint32_t* __restrict__ qzeros,
                                                                  void* __restrict__ scales, int out_f, int in_f,
-                                                                 int gs) {
+                                                                 int gs, bool vec) {
   extern __shared__ float tile[];  // [kQuantRows][gs + 1]
   __shared__ float row_s[kQuantRows];
   __shared__ float row_z[kQuantRows];
@@ -40,12 +40,38 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_kernel(const void* __r
   const int rows = out_f - o0 < kQuantRows ? out_f - o0 : kQuantRows;  // a multiple of 8
   const int tid = threadIdx.x;
 
-  for (int e = tid; e < rows * gs; e += kQuantThreads) {
-    const int r = e / gs;
-    const int c = e - r * gs;
-    const size_t i = static_cast<size_t>(o0 + r) * in_f + static_cast<size_t>(g) * gs + c;
-    tile[r * pitch + c] = dtype == kDtypeF32 ? static_cast<const float*>(weight)[i]
-                                             : load_weight(static_cast<const uint16_t*>(weight), dtype, i);
+  if (vec) {
+    // 16-byte loads: 8 values of a 16-bit type or 4 floats per load (gs a multiple of
+    // either, weight 16-byte aligned; checked on the host).
+    const int per = dtype == kDtypeF32 ? 4 : 8;
+    const int cpr = gs / per;  // chunks per row
+    for (int e = tid; e < rows * cpr; e += kQuantThreads) {
+      const int r = e / cpr;
+      const int c = (e - r * cpr) * per;
+      const size_t i = static_cast<size_t>(o0 + r) * in_f + static_cast<size_t>(g) * gs + c;
+      float* dst = tile + r * pitch + c;
+      if (dtype == kDtypeF32) {
+        const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(weight) + i);
+        dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(weight) + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint16_t lo = static_cast<uint16_t>(w[h] & 0xFFFFu), hi = static_cast<uint16_t>(w[h] >> 16);
+          dst[2 * h] = dtype == kDtypeF16 ? static_cast<float>(__builtin_bit_cast(_Float16, lo)) : bf16_bits_to_f32(lo);
+          dst[2 * h + 1] = dtype == kDtypeF16 ? static_cast<float>(__builtin_bit_cast(_Float16, hi)) : bf16_bits_to_f32(hi);
+        }
+      }
+    }
+  } else {
+    for (int e = tid; e < rows * gs; e += kQuantThreads) {
+      const int r = e / gs;
+      const int c = e - r * gs;
+      const size_t i = static_cast<size_t>(o0 + r) * in_f + static_cast<size_t>(g) * gs + c;
+      tile[r * pitch + c] = dtype == kDtypeF32 ? static_cast<const float*>(weight)[i]
+                                               : load_weight(static_cast<const uint16_t*>(weight), dtype, i);
+    }
   }
   __syncthreads();
 
@@ -132,8 +158,9 @@ size_t quantize_lds_bytes(int group_size) {
 hipError_t launch_quantize(const void* weight, int dtype, uint32_t* qweight, uint32_t* qzeros, void* scales,
                            int out_f, int in_f, int group_size, hipStream_t stream) {
   const dim3 grid((out_f + kQuantRows - 1) / kQuantRows, in_f / group_size);
+  const bool vec = reinterpret_cast<uintptr_t>(weight) % 16 == 0 && group_size % (dtype == kDtypeF32 ? 4 : 8) == 0;
   quantize_kernel<<<grid, kQuantThreads, quantize_lds_bytes(group_size), stream>>>(
-      weight, dtype, qweight, qzeros, scales, out_f, in_f, group_size);
+      weight, dtype, qweight, qzeros, scales, out_f, in_f, group_size, vec);
   return hipGetLastError();
 }
 

@@ -94,11 +94,14 @@ class _WorkspacePool:
     """Split-K workspace shared by all layers issuing on one (device, stream).
 
     Kernels on one stream run in order, so one buffer per stream serves every layer; it
-    is zero-filled when (re)allocated and the kernels re-arm their counters to zero."""
+    is zero-filled when (re)allocated and the kernels re-arm their counters to zero.  A
+    buffer that is outgrown stays referenced for the life of the pool: a HIP graph captured
+    earlier may still address it, so its memory must not return to the allocator."""
 
     def __init__(self):
         self._lock = threading.Lock()
         self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
         if nbytes <= 0:
@@ -108,6 +111,8 @@ class _WorkspacePool:
         with self._lock:
             buf = self._buffers.get(key)
             if buf is None or buf.numel() < nbytes:
+                if buf is not None:
+                    self._retired.append(buf)
                 size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._buffers[key] = buf
