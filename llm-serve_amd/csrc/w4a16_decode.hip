@@ -136,7 +136,7 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
     const uint8_t* lx = wl + lay.x_off + (i * M + r) * 256;
 #pragma unroll
     for (int js = 0; js < 4; ++js)
-      a[0][js] = *reinterpret_cast<const u32x4_t*>(lx + ((((js << 2) | (lane >> 4)) ^ ((r & 3) << 2)) << 4));
+      a[0][js] = *reinterpret_cast<const u32x4_t*>(lx + ((((js << 2) | (lane >> 4)) ^ (r & 15)) << 4));
   } else {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -185,15 +185,16 @@ __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(wl + lay.z_off + b * 4), 4, off, 0, 0, 0);
   }
   if constexpr (XL) {
-    // LDS chunk C = (i M + r) 16 + cc holds global chunk cc ^ ((r & 3) << 2) of row r of
-    // item i's group (the XOR spreads the rows of one fragment read over the banks).
+    // LDS chunk C = (i M + r) 16 + cc holds global chunk cc ^ (r & 15) of row r of item i's
+    // group: the 16 rows of one fragment read then sit in 16 different chunk positions,
+    // i.e. on all 64 banks once.
     const int chunks = n_items * M * 16;
     for (int b = 0; b < chunks; b += 64) {
       const int C = b + lane;
       const int im = C >> 4;
       const int i = im / M;
       const int r = im - i * M;
-      const int cc = (C & 15) ^ ((r & 3) << 2);
+      const int cc = (C & 15) ^ (r & 15);
       const uint32_t off =
           C < chunks ? (static_cast<uint32_t>(r) * K + static_cast<uint32_t>(g_first + i * W) * kGroup) * 2u + cc * 16u
                      : kOutOfRange;
@@ -369,12 +370,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 bool decode_stages_x(int M, int K, int split) {
   const int G = K / kGroup;
   const size_t n_gmax = static_cast<size_t>((G + split - 1) / split);
+  // Staging the activations pays for M <= 4 only: measured on MI355X over the Qwen3-8B
+  // shapes, staging them for M = 5..16 (up to 128 KiB per workgroup) gave no gain.
   return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
 }
 
 size_t decode_lds_bytes(int M, int K, int tn, int waves, int split) {
   return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split)).total;
 }
+
+constexpr int kMaxDevices = 64;
 
 template <int MB, int TN, int DEPTH, int WAVES, bool XL>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
@@ -383,6 +388,19 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL).total;
+  if (lds > 64 * 1024) {
+    // Dynamic LDS beyond 64 KiB must be allowed per kernel (once per device).
+    static bool raised[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!raised[dev]) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(kDecodeMaxLds));
+      if (e != hipSuccess) return e;
+      raised[dev] = true;
+    }
+  }
   decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles);
   return hipGetLastError();

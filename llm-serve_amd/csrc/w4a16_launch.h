@@ -29,7 +29,9 @@ hipError_t launch_pack_int4(const int32_t* values, uint32_t* packed, int rows, i
 // 1 <= split <= K / 128, decode_config_fits() and decode_lds_bytes() <= kDecodeMaxLds.
 // `partials` holds the split-K fp32 fragments and `counters` N / (16 tn) ints (both unused
 // when split == 1).
-constexpr size_t kDecodeMaxLds = 64 * 1024;      // LDS of one decode workgroup
+// LDS of one decode workgroup: a gfx950 CU has 160 KiB; the kernel's static LDS must fit
+// beside the dynamic part (a launch past the total is not rejected by the runtime: it faults).
+constexpr size_t kDecodeMaxLds = 156 * 1024;
 constexpr size_t kDecodeMaxStagedX = 32 * 1024;  // activations staged in LDS (M <= 4 only)
 
 // Whether the activations of an (M, K, split) problem are staged in LDS.

@@ -67,7 +67,7 @@ DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4, 6) for w in (4, 8) for d 
 
 def decode_config_accepted(m, k, tn, depth, waves, split):
     """The library's admission rules (LDS and ring registers), restated: staged activations
-    for M <= 4 within 32 KiB, LDS <= 64 KiB, accumulator + ring registers <= 176."""
+    for M <= 4 within 32 KiB, LDS <= 156 KiB, accumulator + ring registers <= 176."""
     mb = (m + 15) // 16
     n_gmax = -(-(k // 128) // split)
     xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
@@ -75,7 +75,7 @@ def decode_config_accepted(m, k, tn, depth, waves, split):
     staged = up(n_gmax * tn * 32, 256) + up(n_gmax * tn * 8, 256) + (up(n_gmax * m * 256, 1024) if xl else 0)
     lds = max(staged, waves * mb * tn * 1024)
     regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
-    return lds <= 64 * 1024 and regs <= 176
+    return lds <= 156 * 1024 and regs <= 176
 
 
 @pytest.mark.parametrize("m", [1, 3, 5, 16, 33, 64])
@@ -174,7 +174,7 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
     qw, qz, s = random_awq_gpu(k, n, seed=11)
     packed = awq_mod().repack_awq_qweight(qw)
     for m in (1, 4, 8, 16, 32, 64):
-        assert pkg().awq_regime(m, k, n) == "decode"
+        assert pkg().awq_regime(m, k, n) == ("tile" if m >= 48 and n >= 16384 else "decode")
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
         err = rel_err(y, full_reference(x, qw, qz, s))

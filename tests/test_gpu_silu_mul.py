@@ -59,7 +59,7 @@ def decode_config_accepted(m, k, tn, depth, waves, split):
     staged = up(n_gmax * tn * 32, 256) + up(n_gmax * tn * 8, 256) + (up(n_gmax * m * 256, 1024) if xl else 0)
     lds = max(staged, waves * mb * tn * 1024)
     regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
-    return lds <= 64 * 1024 and regs <= 176
+    return lds <= 156 * 1024 and regs <= 176
 
 
 @pytest.mark.parametrize("m", [1, 5, 33])
