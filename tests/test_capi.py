@@ -175,3 +175,16 @@ def test_quantize_and_pack_validate_without_launching(pkg):
     assert pk(None, None, 2, 12, None) == 2
     assert pk(None, None, 0, 8, None) == 1
     assert pk(None, None, 2, 8, None) == 1
+
+
+def test_two_gib_limits_are_rejected_before_launch(pkg):
+    """The kernels address tensors through 32-bit buffer offsets: packed weights of 2 GiB or
+    more, and decode-regime activations of 2 GiB or more, are refused (tile-regime
+    activations are split into row chunks instead)."""
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    assert L.dll.w4a16_gemm(p, p, p, p, p, 16, 65536, 65536, 128, None, 0, None) == 2
+    assert "2 GiB" in L.last_error()
+    assert L.dll.w4a16_gemm(p, p, p, p, p, 64, 1 << 24, 64, 128, None, 0, None) == 2
+    assert "2 GiB" in L.last_error()

@@ -326,3 +326,24 @@ def test_hip_graph_capture_replays_match_eager(gpu_lib):
         assert torch.equal(static_y.view(torch.int16), eager.view(torch.int16)), i
         _ = awq.awq_linear(random_x_gpu(m, k, seed=50 + i), packed, qz, s, group_size=128)
         torch.cuda.synchronize()
+
+
+def test_activations_beyond_2gib_run_in_row_chunks(gpu_lib):
+    """M x K bf16 activations of more than 2 GiB (K = 4096, M = 263000: 2.15 GB): the tile
+    regime launches row chunks below 2 GiB in order; rows on both sides of the chunk
+    boundary and at both ends match the reference."""
+    k, n, m = 4096, 64, 263000
+    fit = (2 ** 31 - 1) // (2 * k)
+    assert m * k * 2 >= 2 ** 31 and m > fit
+    qw, qz, s = random_awq_gpu(k, n, seed=77)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    x = torch.randn((m, k), device="cuda", dtype=torch.bfloat16, generator=g)
+    print(f"2 GiB activations: m={m} k={k} n={n}", flush=True)
+    y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
+    assert y.shape == (m, n)
+    for lo, hi in ((0, 512), (fit - 1024, fit + 1024), (m - 512, m)):
+        err = rel_err(y[lo:hi], full_reference(x[lo:hi], qw, qz, s))
+        assert err <= GEMM_REL_TOL, (lo, hi, err)
+    del x, y
+    torch.cuda.empty_cache()
