@@ -23,6 +23,8 @@
 // vector-memory instructions are then the TN weight loads per group (plus the activation
 // fragments when they are not staged).  The slices are private, so no barrier delays the
 // start of the stream: a wave waits only for its own loads.
+#include <atomic>
+
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
 
@@ -390,16 +392,18 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL).total;
   if (lds > 64 * 1024) {
-    // Dynamic LDS beyond 64 KiB must be allowed per kernel (once per device).
-    static bool raised[kMaxDevices] = {};
+    // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
+    // call from a racing thread is harmless).  A failed call returns before the launch: a
+    // launch that asks for more LDS than allowed is not rejected by the runtime.
+    static std::atomic<bool> raised[kMaxDevices];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!raised[dev]) {
+    if (!raised[dev].load(std::memory_order_acquire)) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                static_cast<int>(kDecodeMaxLds));
       if (e != hipSuccess) return e;
-      raised[dev] = true;
+      raised[dev].store(true, std::memory_order_release);
     }
   }
   decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
