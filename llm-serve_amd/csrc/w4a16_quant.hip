@@ -137,6 +137,118 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_kernel(const void* __r
   }
 }
 
+// Fast path for GS in {32, 64, 128} (the same arithmetic, bit for bit): each of the four
+// threads of a row holds its GS / 4 consecutive values in registers (16-byte loads), the
+// row's min and max come from two lane shuffles, and only the 4-bit codes go through LDS
+// (one byte each, rows padded to GS + 4 bytes so that the eight rows one packed word
+// gathers sit in different banks) for the transposed packing.
+template <int GS, int DTYPE>
+__global__ __launch_bounds__(kQuantThreads) void quantize_rows_kernel(const void* __restrict__ weight,
+                                                                      uint32_t* __restrict__ qweight,
+                                                                      uint32_t* __restrict__ qzeros,
+                                                                      void* __restrict__ scales, int out_f, int in_f) {
+  constexpr int PART = GS / 4;       // values per thread
+  constexpr int QP = GS + 4;         // LDS row pitch of the codes, bytes
+  constexpr int PER = DTYPE == kDtypeF32 ? 4 : 8;  // values per 16-byte load
+  static_assert(PART % PER == 0, "a thread's values must split into 16-byte loads");
+  __shared__ __attribute__((aligned(16))) uint8_t codes[kQuantRows * QP];
+  __shared__ float row_z[kQuantRows];
+  const int o0 = blockIdx.x * kQuantRows;
+  const int g = blockIdx.y;
+  const int rows = out_f - o0 < kQuantRows ? out_f - o0 : kQuantRows;  // a multiple of 8
+  const int tid = threadIdx.x;
+  const int r = tid >> 2;  // the four threads of row r are adjacent lanes of one wave
+  const int h = tid & 3;
+  const bool live = r < rows;
+
+  float v[PART];
+  const size_t base = static_cast<size_t>(o0 + (live ? r : 0)) * in_f + static_cast<size_t>(g) * GS + h * PART;
+#pragma unroll
+  for (int c = 0; c < PART; c += PER) {
+    if constexpr (DTYPE == kDtypeF32) {
+      const float4 w = live ? *reinterpret_cast<const float4*>(static_cast<const float*>(weight) + base + c)
+                            : float4{0.f, 0.f, 0.f, 0.f};
+      v[c] = w.x; v[c + 1] = w.y; v[c + 2] = w.z; v[c + 3] = w.w;
+    } else {
+      const uint4 w = live ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(weight) + base + c)
+                           : uint4{0u, 0u, 0u, 0u};
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t lo = static_cast<uint16_t>(ww[e] & 0xFFFFu), hi = static_cast<uint16_t>(ww[e] >> 16);
+        if constexpr (DTYPE == kDtypeF16) {
+          v[c + 2 * e] = static_cast<float>(__builtin_bit_cast(_Float16, lo));
+          v[c + 2 * e + 1] = static_cast<float>(__builtin_bit_cast(_Float16, hi));
+        } else {
+          v[c + 2 * e] = bf16_bits_to_f32(lo);
+          v[c + 2 * e + 1] = bf16_bits_to_f32(hi);
+        }
+      }
+    }
+  }
+  // Row min and max (NaN propagates as in torch's amin / amax).
+  float mn = v[0], mx = v[0];
+#pragma unroll
+  for (int c = 1; c < PART; ++c) {
+    mn = (v[c] < mn || v[c] != v[c]) ? v[c] : mn;
+    mx = (v[c] > mx || v[c] != v[c]) ? v[c] : mx;
+  }
+#pragma unroll
+  for (int d = 1; d <= 2; d <<= 1) {
+    const float mn2 = __shfl_xor(mn, d);
+    const float mx2 = __shfl_xor(mx, d);
+    mn = (mn2 < mn || mn2 != mn2) ? mn2 : mn;
+    mx = (mx2 > mx || mx2 != mx2) ? mx2 : mx;
+  }
+  float dd = mx - mn;
+  dd = dd < 1e-5f ? 1e-5f : dd;  // torch clamp(min=): NaN stays NaN
+  const float s = dd / 15.0f;
+  float z = -__builtin_rintf(mn / s);
+  z = z < 0.f ? 0.f : (z > 15.f ? 15.f : z);
+  if (live) {
+    uint32_t packed[PART / 4];
+#pragma unroll
+    for (int c = 0; c < PART; c += 4) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float q = __builtin_rintf(v[c + e] / s) + z;
+        q = q < 0.f ? 0.f : (q > 15.f ? 15.f : q);
+        word |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * e);
+      }
+      packed[c / 4] = word;
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(codes + r * QP + h * PART);
+#pragma unroll
+    for (int c = 0; c < PART / 4; ++c) dst[c] = packed[c];
+    if (h == 0) {
+      row_z[r] = z;
+      const size_t si = static_cast<size_t>(g) * out_f + o0 + r;
+      if constexpr (DTYPE == kDtypeF32) static_cast<float*>(scales)[si] = s;
+      else if constexpr (DTYPE == kDtypeF16) static_cast<_Float16*>(scales)[si] = static_cast<_Float16>(s);
+      else static_cast<uint16_t*>(scales)[si] = f32_to_bf16_bits(s);
+    }
+  }
+  __syncthreads();
+
+  const int W = rows / 8;    // packed words per input row in this workgroup
+  const int C8 = out_f / 8;  // packed words per input row
+  if (tid < W) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) word |= (static_cast<uint32_t>(row_z[8 * tid + c]) & 0xFu) << awq_shift(c);
+    qzeros[static_cast<size_t>(g) * C8 + o0 / 8 + tid] = word;
+  }
+  for (int e = tid; e < GS * W; e += kQuantThreads) {
+    const int k = e / W;
+    const int j = e - k * W;
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) word |= (static_cast<uint32_t>(codes[(8 * j + c) * QP + k]) & 0xFu) << awq_shift(c);
+    qweight[(static_cast<size_t>(g) * GS + k) * C8 + o0 / 8 + j] = word;
+  }
+}
+
 // One thread per packed word: out[r, c8] = sum_c (v[r, 8 c8 + c] & 15) << awq_shift(c).
 __global__ __launch_bounds__(256) void pack_int4_kernel(const int32_t* __restrict__ values,
                                                         uint32_t* __restrict__ packed, int rows, int c8) {
@@ -155,9 +267,34 @@ size_t quantize_lds_bytes(int group_size) {
   return static_cast<size_t>(kQuantRows) * (group_size + 1) * sizeof(float);
 }
 
+template <int GS>
+static hipError_t launch_quantize_rows(const void* weight, int dtype, uint32_t* qweight, uint32_t* qzeros,
+                                       void* scales, int out_f, int in_f, dim3 grid, hipStream_t stream) {
+  switch (dtype) {
+    case kDtypeF32:
+      quantize_rows_kernel<GS, kDtypeF32><<<grid, kQuantThreads, 0, stream>>>(weight, qweight, qzeros, scales, out_f, in_f);
+      break;
+    case kDtypeF16:
+      quantize_rows_kernel<GS, kDtypeF16><<<grid, kQuantThreads, 0, stream>>>(weight, qweight, qzeros, scales, out_f, in_f);
+      break;
+    default:
+      quantize_rows_kernel<GS, kDtypeBF16><<<grid, kQuantThreads, 0, stream>>>(weight, qweight, qzeros, scales, out_f, in_f);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_quantize(const void* weight, int dtype, uint32_t* qweight, uint32_t* qzeros, void* scales,
                            int out_f, int in_f, int group_size, hipStream_t stream) {
   const dim3 grid((out_f + kQuantRows - 1) / kQuantRows, in_f / group_size);
+  // Fast path: 16-byte aligned weight (every row segment a thread loads is then aligned).
+  if (reinterpret_cast<uintptr_t>(weight) % 16 == 0) {
+    switch (group_size) {
+      case 128: return launch_quantize_rows<128>(weight, dtype, qweight, qzeros, scales, out_f, in_f, grid, stream);
+      case 64: return launch_quantize_rows<64>(weight, dtype, qweight, qzeros, scales, out_f, in_f, grid, stream);
+      case 32: return launch_quantize_rows<32>(weight, dtype, qweight, qzeros, scales, out_f, in_f, grid, stream);
+      default: break;
+    }
+  }
   const bool vec = reinterpret_cast<uintptr_t>(weight) % 16 == 0 && group_size % (dtype == kDtypeF32 ? 4 : 8) == 0;
   quantize_kernel<<<grid, kQuantThreads, quantize_lds_bytes(group_size), stream>>>(
       weight, dtype, qweight, qzeros, scales, out_f, in_f, group_size, vec);
