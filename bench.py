@@ -31,6 +31,10 @@ Also reported (not part of `value`):
   * stack36: a 36-layer Qwen3-8B-shaped stack (independent weights, 3.6 GB) stepped at
     M in {1, 8, 64, 128}: 144 GEMMs per step captured in one graph; aggregate weight
     GB/s and linear-layer time per decoded token;
+  * stack36_chained: the same weights with the layer's dataflow: QKV, O on the first 4096
+    QKV columns (the attention output's shape) with the residual add in its epilogue, the
+    fused gate|up GEMM with SiLU * up, down with the residual add -- 144 GEMM launches and
+    36 copies per step, one graph;
   * measured_ceilings: a 1 GiB device copy (read + write GB/s) and torch.matmul
     (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
   * fused_gate_up: the gate_up GEMM with SiLU(gate) * up in its epilogue
@@ -260,9 +264,10 @@ def mixed_batch(lib, dev, stream, reps: int) -> dict:
     return out
 
 
-def layer_stack(lib, dev, stream, reps: int) -> dict:
+def layer_stack(lib, dev, stream, reps: int) -> tuple[dict, dict]:
     """36 layers x (QKV, O, gate_up, down) with independent weights; one step = the 144
-    GEMMs back to back on one stream at packed M."""
+    GEMMs back to back on one stream at packed M.  Also returns the chained variant over
+    the same weights (layer_stack_chained)."""
     layers = [{name: make_weights(k, n, 1, dev, 1000 + 4 * li + si)[0]
                for si, (name, (k, n)) in enumerate(SHAPES.items())} for li in range(STACK_LAYERS)]
     out = {}
@@ -289,7 +294,50 @@ def layer_stack(lib, dev, stream, reps: int) -> dict:
                          "us_per_token": round(ms * 1e3 / m, 2),
                          "regimes": sorted({"decode" if lib.regime(m, k, n) == 1 else "tile"
                                             for k, n in SHAPES.values()})}
+    chained = layer_stack_chained(lib, dev, stream, reps, layers)
     del layers
+    return out, chained
+
+
+def layer_stack_chained(lib, dev, stream, reps: int, layers) -> dict:
+    """36 layers stepped with the layer's dataflow (attention itself left out: O reads the
+    first 4096 QKV columns), O and down through w4a16_gemm_residual (in place on the hidden
+    state), gate|up through w4a16_gemm_silu_mul; one graph per M."""
+    out = {}
+    kq, nq = SHAPES["qkv"]
+    ki, ni = SHAPES["gate_up"]
+    for m in STACK_M:
+        h = torch.randn((m, kq), device=dev).to(torch.bfloat16)
+        qkv = torch.empty((m, nq), dtype=torch.bfloat16, device=dev)
+        attn = torch.empty((m, kq), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((m, ni // 2), dtype=torch.bfloat16, device=dev)
+        ws_len = max(lib.workspace_bytes(m, k, n) for k, n in SHAPES.values())
+        ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
+        wsp = ws.data_ptr() if ws_len else None
+
+        def call(fn, x, w, y, k, n, sp):
+            packed, qzeros, scales = w
+            if fn(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(), m, k, n, 128,
+                  wsp, ws_len, sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def call_res(x, w, k, n, sp):
+            packed, qzeros, scales = w
+            if lib.dll.w4a16_gemm_residual(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                           h.data_ptr(), h.data_ptr(), m, k, n, 128, wsp, ws_len, sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def step():
+            sp = torch.cuda.current_stream(dev).cuda_stream
+            for layer in layers:
+                call(lib.dll.w4a16_gemm, h, layer["qkv"], qkv, kq, nq, sp)
+                attn.copy_(qkv[:, :kq])
+                call_res(attn, layer["o"], *SHAPES["o"], sp)  # h = bf16(o_proj(attn) + h), in place
+                call(lib.dll.w4a16_gemm_silu_mul, h, layer["gate_up"], act, ki, ni, sp)
+                call_res(act, layer["down"], *SHAPES["down"], sp)
+
+        ms = time_graph(step, stream, reps)
+        out[f"M={m}"] = {"step_us": round(ms * 1e3, 1), "us_per_token": round(ms * 1e3 / m, 2)}
     return out
 
 
@@ -523,16 +571,17 @@ def main(argv=None):
                 print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
         del pts
 
-    mixed = stack = ceilings = fused = quant = None
+    mixed = stack = stack_chained = ceilings = fused = quant = None
     if not args.no_extra:
         mixed = mixed_batch(lib, dev, stream, max(3, args.steps // 4))
-        stack = layer_stack(lib, dev, stream, max(2, args.steps // 10))
+        stack, stack_chained = layer_stack(lib, dev, stream, max(2, args.steps // 10))
         ceilings = measured_ceilings(dev, stream)
         fused = fused_gate_up(lib, dev, stream, max(3, args.steps // 4))
         quant = quantize_throughput(lib, dev, stream, max(3, args.steps // 4))
         if args.details:
             print(f"mixed M={MIXED_M}: {json.dumps(mixed)}", file=sys.stderr)
             print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
+            print(f"stack36_chained: {json.dumps(stack_chained)}", file=sys.stderr)
             print(f"ceilings: {json.dumps(ceilings)}", file=sys.stderr)
             print(f"fused gate_up: {json.dumps(fused)}", file=sys.stderr)
             print(f"quantize: {json.dumps(quant)}", file=sys.stderr)
@@ -569,6 +618,7 @@ def main(argv=None):
         "prefill_m2048": prefill,
         "mixed_m512": mixed,
         "stack36": stack,
+        "stack36_chained": stack_chained,
         "measured_ceilings": ceilings,
         "fused_gate_up": fused,
         "quantize": quant,

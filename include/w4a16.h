@@ -125,6 +125,15 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
                const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* y[M, N] = bf16(bf16(x[M, K] @ W) + residual[M, N]): the GEMM with the residual add that
+ * follows the O and down projections (the reference's add_rms_forward: x.float() +
+ * residual.float() then bf16, layernorm.py:35-36) done in the epilogue.  residual may be y itself
+ * (in place); 16-byte aligned.  Otherwise as w4a16_gemm; same workspace.  Replaces
+ * o_proj / down_proj followed by that add (qwen3.py:170-174). */
+int w4a16_gemm_residual(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                        const uint16_t* scales, const uint16_t* residual, uint16_t* y, int M, int K,
+                        int N, int group_size, void* workspace, size_t workspace_bytes, void* stream);
+
 /* y[M, N/2] = SiLU(g) * u with [g | u] = x[M, K] @ W for a gate|up weight W [K, N] whose
  * first N/2 columns are the gate projection and last N/2 the up projection (the layout of
  * MergedColumnParallelLinear's gate_up_proj); g and u stay in fp32 and the product is rounded

@@ -10,6 +10,7 @@ from .layers.quantization.awq import (
     AWQLinearMethod,
     AWQRuntimeConfig,
     awq_linear,
+    awq_linear_residual,
     awq_linear_silu_mul,
     awq_regime,
     dequantize_awq_gemm,
@@ -26,6 +27,7 @@ __all__ = (
     "W4A16Error",
     "W4A16Library",
     "awq_linear",
+    "awq_linear_residual",
     "awq_linear_silu_mul",
     "awq_regime",
     "dequantize_awq_gemm",

@@ -40,6 +40,8 @@ _SIGNATURES = {
     "w4a16_workspace_bytes_config": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "w4a16_quantize": (_c_int, [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr]),
     "w4a16_pack_int4": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_gemm_residual": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
+                                     _c_int, _c_ptr, _c_size, _c_ptr]),
     "w4a16_gemm_silu_mul": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
                                      _c_ptr, _c_size, _c_ptr]),
     "w4a16_gemm_silu_mul_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
@@ -177,6 +179,19 @@ class W4A16Library:
             self.check(self.dll.w4a16_gemm(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
                                            y.data_ptr(), m, k, n, group_size, ws_ptr, ws_len, self._stream(x)),
                        "w4a16_gemm")
+        return y
+
+    def gemm_residual(self, x, packed, qzeros, scales, residual, y, k: int, n: int,
+                      workspace: torch.Tensor | None, group_size: int = 128) -> torch.Tensor:
+        """y[M, N] = bf16(bf16(x @ W) + residual); residual may be y."""
+        m = x.shape[0]
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_gemm_residual(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                    scales.data_ptr(), residual.data_ptr(), y.data_ptr(), m, k, n,
+                                                    group_size, ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm_residual")
         return y
 
     def gemm_silu_mul(self, x, packed, qzeros, scales, y, k: int, n: int, workspace: torch.Tensor | None,

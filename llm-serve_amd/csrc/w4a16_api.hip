@@ -208,9 +208,10 @@ int validate_gemm(const void* x, const void* packed, const void* qzeros, const v
 }
 
 // up_tiles: 0 for the plain GEMM, N / 32 for the fused SiLU(gate) * up (y is [M, N / 2]).
+// res: null, or a bf16 [M, N] residual added in the epilogue (plain GEMM; may be y).
 int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
              const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
-             hipStream_t stream, int up_tiles = 0) {
+             hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr) {
   if (p.regime == W4A16_REGIME_NONE) return ok();
   const size_t need = workspace_for(p, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -226,8 +227,8 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const uint32_t* pk = reinterpret_cast<const uint32_t*>(packed);
   const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
   if (p.regime == W4A16_REGIME_DECODE)
-    return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, partials, counters, M, K, N, p.p0, p.p2,
-                                                 p.p1, p.split, up_tiles, stream),
+    return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, res, partials, counters, M, K, N, p.p0,
+                                                 p.p2, p.p1, p.split, up_tiles, stream),
                         "decode");
   // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
   // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
@@ -240,8 +241,9 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int mc = M - r0 < chunk ? M - r0 : chunk;
     const int rc = check_launch(w4a16::launch_tile_cfg(x + static_cast<size_t>(r0) * K, pk, qz, scales,
-                                                       y + static_cast<size_t>(r0) * n_out, partials, counters, mc,
-                                                       K, N, p.p0, p.p2, p.p1, p.split, up_tiles, stream),
+                                                       y + static_cast<size_t>(r0) * n_out,
+                                                       res ? res + static_cast<size_t>(r0) * N : nullptr, partials,
+                                                       counters, mc, K, N, p.p0, p.p2, p.p1, p.split, up_tiles, stream),
                                 "tile");
     if (rc != W4A16_OK) return rc;
   }
@@ -364,6 +366,18 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, 
   if (v != W4A16_OK) return v;
   return run_plan(plan(M, K, N), x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
                   static_cast<hipStream_t>(stream));
+}
+
+int w4a16_gemm_residual(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                        const uint16_t* residual, uint16_t* y, int M, int K, int N, int group_size, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  if (!residual) return fail(W4A16_ERR_ARG, "null residual pointer");
+  if (!aligned(residual, 16)) return fail(W4A16_ERR_ALIGN, "residual must be 16-byte aligned");
+  return run_plan(plan(M, K, N), x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream), 0, residual);
 }
 
 int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,

@@ -64,6 +64,23 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
   return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xFFFFu);
 }
 
+// Residual epilogue: eight bf16 GEMM outputs plus eight bf16 residuals, added in fp32 and
+// rounded once more -- the reference's order (the layer's bf16 output, then
+// x.float() + residual.float() rounded back to bf16).
+__device__ __forceinline__ uint4 add_bf16x8(uint4 v, uint4 r) {
+  const uint32_t vv[4] = {v.x, v.y, v.z, v.w}, rr[4] = {r.x, r.y, r.z, r.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(bf16_bits_to_f32(vv[e] & 0xFFFFu) + bf16_bits_to_f32(rr[e] & 0xFFFFu),
+                       bf16_bits_to_f32(vv[e] >> 16) + bf16_bits_to_f32(rr[e] >> 16));
+  return uint4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ uint16_t add_bf16(uint16_t v, uint16_t r) {
+  return f32_to_bf16_bits(bf16_bits_to_f32(v) + bf16_bits_to_f32(r));
+}
+
 // SiLU(g) * u = g / (1 + e^-g) * u in fp32 for the fused gate/up epilogue, e^-g as
 // 2^(-g log2 e) on the hardware exp2 and the quotient by the hardware reciprocal (about
 // 1 ulp each, far below the bf16 rounding of the result).  g -> -inf gives -0 (e^-g = inf,

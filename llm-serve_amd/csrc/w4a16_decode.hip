@@ -38,6 +38,7 @@ struct DecodeArgs {
   const uint32_t* qzeros;
   const uint16_t* scales;
   uint16_t* y;
+  const uint16_t* res;  // residual added to y (may be y itself), or null
   float* partials;
   int* counters;
   int M, K, N, split;
@@ -211,7 +212,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
                                                             const uint16_t* __restrict__ scales,
-                                                            uint16_t* __restrict__ y, float* __restrict__ partials,
+                                                            uint16_t* y, const uint16_t* res,
+                                                            float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
                                                             int split, int up_tiles) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -354,7 +356,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 16 * mb + 4 * (lane >> 4) + i;
-        if (row < M) y[static_cast<size_t>(row) * N + n] = f32_to_bf16_bits(out[p][i]);
+        if (row < M) {
+          const size_t idx = static_cast<size_t>(row) * N + n;
+          const uint16_t b = f32_to_bf16_bits(out[p][i]);
+          y[idx] = res ? add_bf16(b, res[idx]) : b;
+        }
       }
     } else if constexpr (H > 0) {
       if (tt < H) {
@@ -407,7 +413,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     }
   }
   decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
-      a.x, a.packed, a.qzeros, a.scales, a.y, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles);
+      a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles);
   return hipGetLastError();
   }
 }
@@ -449,9 +455,10 @@ static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int wa
 }
 
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                             const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                             int N, int tn, int depth, int waves, int split, int up_tiles, hipStream_t stream) {
-  const DecodeArgs a{x, packed, qzeros, scales, y, partials, counters, M, K, N, split, up_tiles};
+                             const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
+                             int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
+                             hipStream_t stream) {
+  const DecodeArgs a{x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, up_tiles};
   switch ((M + 15) / 16) {
     case 1: return launch_decode_m<1>(a, tn, depth, waves, stream);
     case 2: return launch_decode_m<2>(a, tn, depth, waves, stream);

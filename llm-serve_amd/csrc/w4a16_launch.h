@@ -51,10 +51,12 @@ constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
 }
 
 // up_tiles: 0 for the plain GEMM (y is [M, N]); N / 32 for the fused SiLU(gate) * up of a
-// gate|up weight (tn even, N % 128 == 0, y is [M, N / 2]).
+// gate|up weight (tn even, N % 128 == 0, y is [M, N / 2]).  res: null, or a bf16 [M, N]
+// residual added in the epilogue (plain GEMM only; may be y itself).
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                             const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                             int N, int tn, int depth, int waves, int split, int up_tiles, hipStream_t stream);
+                             const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
+                             int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
+                             hipStream_t stream);
 
 // LDS-tiled MFMA GEMM.  A tile shape code selects the wave grid: nwm waves along M x nwn
 // along N, each owning tw 16-column layout tiles and 16 wm rows, so the workgroup tile is
@@ -68,9 +70,11 @@ TileShape tile_shape(int shape);
 // Compiled: (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
-// unused when split == 1).  up_tiles as for the decode kernel (N % 128 == 0 when fused).
+// unused when split == 1).  up_tiles and res as for the decode kernel (N % 128 == 0 when
+// fused; res 16-byte aligned).
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                           const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int shape, int occ, int split, int up_tiles, hipStream_t stream);
+                           const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials, int* counters,
+                           int M, int K, int N, int wm, int shape, int occ, int split, int up_tiles,
+                           hipStream_t stream);
 
 }  // namespace w4a16

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
                                                                    const uint32_t* __restrict__ packed,
                                                                    const uint32_t* __restrict__ qzeros,
                                                                    const uint16_t* __restrict__ scales,
-                                                                   uint16_t* __restrict__ y,
+                                                                   uint16_t* y, const uint16_t* res,
                                                                    float* __restrict__ partials,
                                                                    int* __restrict__ counters, int M, int K, int N,
                                                                    int split, int m_blocks, int n_blocks,
@@ -339,7 +339,10 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
       const int q = lane % CPR;
       const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + ((q ^ (r % CPR)) << 4));
       const int row = row0 + wm * WR + r;
-      if (row < M) *reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * n_out + col_w + 8 * q) = v;
+      if (row < M) {
+        const size_t off = static_cast<size_t>(row) * n_out + col_w + 8 * q;
+        *reinterpret_cast<uint4*>(y + off) = res ? add_bf16x8(v, *reinterpret_cast<const uint4*>(res + off)) : v;
+      }
     }
   };
   if (!act) {
@@ -378,15 +381,15 @@ __global__ __launch_bounds__(64 * NWM * NWN, OCC) void tile_kernel(const uint16_
 
 template <int WM, int TW, int NWM, int NWN, int OCC>
 static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                                const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                                int N, int split, int up_tiles, hipStream_t stream) {
+                                const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
+                                int* counters, int M, int K, int N, int split, int up_tiles, hipStream_t stream) {
   constexpr int BM = 16 * WM * NWM;
   constexpr int BN = 16 * TW * NWN;
   const int m_blocks = (M + BM - 1) / BM;
   const int n_blocks = (N + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
   tile_kernel<WM, TW, NWM, NWN, OCC><<<grid, 64 * NWM * NWN, 0, stream>>>(
-      x, packed, qzeros, scales, y, partials, counters, M, K, N, split, m_blocks, n_blocks, up_tiles);
+      x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, m_blocks, n_blocks, up_tiles);
   return hipGetLastError();
 }
 
@@ -413,12 +416,13 @@ bool tile_config_compiled(int wm, int shape, int occ) {
 }
 
 hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
-                           const uint16_t* scales, uint16_t* y, float* partials, int* counters, int M, int K,
-                           int N, int wm, int shape, int occ, int split, int up_tiles, hipStream_t stream) {
+                           const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials, int* counters,
+                           int M, int K, int N, int wm, int shape, int occ, int split, int up_tiles,
+                           hipStream_t stream) {
   const TileShape ts = tile_shape(shape);
 #define W4A16_TILE_LAUNCH(WM_, TW_, NWM_, NWN_, OCC_)                                                           \
   if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_)                            \
-    return launch_tile_t<WM_, TW_, NWM_, NWN_, OCC_>(x, packed, qzeros, scales, y, partials, counters, M, K, N, \
+    return launch_tile_t<WM_, TW_, NWM_, NWN_, OCC_>(x, packed, qzeros, scales, y, res, partials, counters, M, K, N, \
                                                      split, up_tiles, stream);
   W4A16_TILE_CONFIGS(W4A16_TILE_LAUNCH)
 #undef W4A16_TILE_LAUNCH

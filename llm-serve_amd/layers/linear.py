@@ -202,3 +202,15 @@ class RowParallelLinear(LinearBase):
         if self.tp_size > 1:
             dist.all_reduce(y)
         return y
+
+    def forward_residual(self, x: torch.Tensor, residual: torch.Tensor,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+        """The new residual ``bf16(self(x).float() + residual.float())`` of the next
+        add_rms_forward (layernorm.py:35-36, after O and down in qwen3.py:170-174) with the
+        add in the AWQ GEMM epilogue; ``out`` may be ``residual`` for an in-place update.
+        The RMSNorm itself stays with the norm layer."""
+        if self.quant_method is None or not hasattr(self.quant_method, "apply_residual"):
+            raise ValueError("the fused residual add is implemented for the AWQ HIP backend only")
+        if self.tp_size > 1:
+            raise ValueError("the fused residual add needs a tensor-parallel world size of 1")
+        return self.quant_method.apply_residual(self, x, residual, out=out)

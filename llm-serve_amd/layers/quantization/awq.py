@@ -11,6 +11,8 @@ Same names, argument meaning and error behaviour as the reference:
 * ``dequantize_awq_gemm``                          awq.py:235-248
 * ``awq_linear`` (the reference's ``awq_cuda_linear`` / ``awq_reference_linear`` role,
   awq_cuda.py:141-185, awq.py:251-276)
+* ``awq_linear_residual`` / ``AWQLinearMethod.apply_residual``: the GEMM with the residual
+  add of the reference's ``add_rms_forward`` (layernorm.py:35-36) in its epilogue
 * ``awq_linear_silu_mul`` / ``AWQLinearMethod.apply_silu_and_mul``: the gate|up GEMM with
   the reference's ``SiluAndMul`` (activation.py:8-11, applied at qwen3.py:126-130) fused
   into its epilogue; no reference counterpart as one call
@@ -164,6 +166,15 @@ class AWQLinearMethod:
         layer.scales.output_dim = 1
         layer.scales.input_dim = 0
 
+    def apply_residual(self, layer: nn.Module, inputs: torch.Tensor, residual: torch.Tensor,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+        """``(self.apply(layer, inputs).float() + residual.float()).to(bf16)`` as one kernel:
+        the residual update after O and down (qwen3.py:170-174, layernorm.py:35-36)."""
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear_residual(inputs, layer.awq_qweight, layer.awq_qzeros, layer.scales, residual,
+                                   group_size=self.config.group_size, out=out)
+
     def apply_silu_and_mul(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
         """``SiluAndMul()(self.apply(layer, inputs))`` as one kernel, for a layer whose output
         is [gate | up] of equal widths (qwen3.py:126-130)."""
@@ -306,6 +317,36 @@ def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch
         workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
     library.gemm(x, packed_qweight, qzeros, scales.contiguous(), y, k, n, workspace, group_size)
     return y.reshape(*lead, n)
+
+
+def awq_linear_residual(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor,
+                        scales: torch.Tensor, residual: torch.Tensor, *, group_size: int,
+                        out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(inputs @ W) + residual) -- the layer output rounded to bf16, then added to
+    the residual in fp32 and rounded again, as the reference's add_rms_forward does
+    (layernorm.py:35-36) -- in the GEMM epilogue.  ``residual`` is bf16 [..., N] on the same
+    GPU; ``out`` (default: a new tensor) may be ``residual`` itself for an in-place update."""
+    x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
+    m = x.shape[0]
+    if residual.dtype != torch.bfloat16 or residual.device != inputs.device:
+        raise ValueError("AWQ residual must be a bfloat16 tensor on the activations' GPU")
+    if residual.shape != (*lead, n):
+        raise ValueError("AWQ residual shape must be the layer output shape")
+    res = residual.reshape(m, n)
+    if not res.is_contiguous() or not _aligned16(res):
+        raise ValueError("AWQ residual must be contiguous and 16-byte aligned")
+    if out is None:
+        out = torch.empty_like(residual)
+    if out.shape != residual.shape or out.dtype != torch.bfloat16 or not out.is_contiguous() or not _aligned16(out):
+        raise ValueError("AWQ residual output must be a contiguous, 16-byte aligned bf16 tensor of the output shape")
+    if m == 0:
+        return out
+    library = lib()
+    if workspace is None:
+        workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
+    library.gemm_residual(x, packed_qweight, qzeros, scales.contiguous(), res, out.reshape(m, n), k, n, workspace,
+                          group_size)
+    return out
 
 
 def awq_linear_silu_mul(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor,

@@ -188,3 +188,15 @@ def test_two_gib_limits_are_rejected_before_launch(pkg):
     assert "2 GiB" in L.last_error()
     assert L.dll.w4a16_gemm(p, p, p, p, p, 64, 1 << 24, 64, 128, None, 0, None) == 2
     assert "2 GiB" in L.last_error()
+
+
+def test_residual_entry_point_validates_without_launching(pkg):
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    f = L.dll.w4a16_gemm_residual
+    assert f(p, p, p, p, None, p, 16, 4096, 4096, 128, None, 0, None) == 1
+    assert "residual" in L.last_error()
+    assert f(p, p, p, p, p + 2, p, 16, 4096, 4096, 128, None, 0, None) == 3
+    assert f(p, p, p, p, p, p, 16, 4096, 4100, 128, None, 0, None) == 2
+    assert f(None, None, None, None, None, None, 0, 4096, 4096, 128, None, 0, None) == 0

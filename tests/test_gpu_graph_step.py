@@ -1,5 +1,6 @@
 """A whole decode step of one Qwen3-8B decoder layer's projections captured as one HIP graph
-through the layer API: QKV, O, gate|up with the fused SiLU * up, down -- the four AWQ GEMMs
+through the layer API: QKV, O with the residual add, gate|up with the fused SiLU * up, down
+with the residual add -- the four AWQ GEMMs
 the reference runs per layer (qwen3.py:126-130, 168-173) and cannot capture with AWQ
 (config.py:58-59, model_runner.py:342).  Replays with eager work in between must reproduce
 the eager outputs bit for bit; the split-K workspace is warmed on the capture stream first,
@@ -42,8 +43,8 @@ def test_decoder_layer_projections_capture_and_replay(gpu_lib, m):
 
     def step(x):
         q = qkv(x)[:, : HEADS * HEAD]
-        h = o(q.contiguous()) + x
-        return down(gate_up.forward_silu_and_mul(h))
+        h = o.forward_residual(q.contiguous(), x)  # residual update in the O epilogue
+        return down.forward_residual(gate_up.forward_silu_and_mul(h), h)
 
     x = random_x_gpu(m, HIDDEN, seed=m)
     eager = step(x).clone()
