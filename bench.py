@@ -15,7 +15,9 @@ Method
     Infinity Cache), i.e. decode bytes come from HBM.
   * Each point's launches are captured once in a HIP graph (torch.cuda.CUDAGraph) and
     replayed; HIP events recorded on the replay stream bracket each replay, giving the
-    average kernel duration with host launch overhead removed.
+    average kernel duration with host launch overhead removed.  Every timed region is
+    preceded by WARM_MS of untimed replays of the same graphs: after a host-side pause the
+    clocks take tens of milliseconds of work to come back up.
   * Algorithmic bytes per GEMM = K N / 2 + K N / 256 + K N / 64 + 2 M K + 2 M N
     (int4 weights, int32 zeros, bf16 scales, bf16 x and y); flops = 2 M N K.
   * `roofline` describes the dominant launch (the decode point with the longest
@@ -159,15 +161,36 @@ def build_points(lib, ms, dev, seed0=0, min_bytes=2 * CACHE_BYTES):
     return points
 
 
+# Untimed GPU work before each timed region.  After a host-side pause (building inputs) the
+# clocks ramp up over the first tens of milliseconds of work: the first replays of the
+# M=2048 gate_up GEMM take 440-540 us, later ones 390-400 us.
+WARM_MS = 60.0
+
+
+def warm_up(replay, min_ms: float = WARM_MS) -> None:
+    """Call replay() (which enqueues GPU work) until at least min_ms of wall time has passed."""
+    t0 = time.perf_counter()
+    while True:
+        replay()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= min_ms:
+            return
+
+
 def time_points(points, stream, steps, warmup):
-    """Replay every point's graph `warmup` times untimed, then `steps` times timed.
-    Returns (per-point mean launch ms, total timed ms)."""
+    """Replay every point's graph `warmup` times untimed, then for WARM_MS more, then `steps`
+    times timed.  Returns (per-point mean launch ms, total timed ms)."""
     for p in points:
         p.capture(stream)
     for _ in range(warmup):
         for p in points:
             p.graph.replay()
-    torch.cuda.synchronize()
+
+    def replay_all():
+        for p in points:
+            p.graph.replay()
+
+    warm_up(replay_all)
     per_point = {id(p): [] for p in points}
     events = []
     start_all = torch.cuda.Event(enable_timing=True)
@@ -225,8 +248,8 @@ STACK_M = (1, 8, 64, 128)
 
 
 def time_graph(fn, stream, reps: int) -> float:
-    """Capture fn() in a HIP graph on `stream`, replay it `reps` times between HIP events
-    on that stream; returns ms per replay."""
+    """Capture fn() in a HIP graph on `stream`, replay it for WARM_MS untimed, then `reps`
+    times between HIP events on that stream; returns ms per replay."""
     with torch.cuda.stream(stream):
         fn()
     stream.synchronize()
@@ -234,7 +257,7 @@ def time_graph(fn, stream, reps: int) -> float:
     with torch.cuda.graph(g, stream=stream):
         fn()
     with torch.cuda.stream(stream):
-        g.replay()
+        warm_up(g.replay)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
@@ -560,7 +583,7 @@ def main(argv=None):
             cols = torch.randperm(k, device=dev, generator=gen)[: round(0.01 * k)]
             x[:, cols] *= 20.0
             pts.append(Point(lib, name, PREFILL_M, k, n, make_weights(k, n, 2, dev, 500 + si), x.to(torch.bfloat16)))
-        pl, _ = time_points(pts, stream, max(3, args.steps // 4), 1)
+        pl, _ = time_points(pts, stream, max(5, args.steps // 2), 1)
         prefill = {}
         for p in pts:
             ms = pl[id(p)]
