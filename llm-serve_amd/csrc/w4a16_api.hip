@@ -98,7 +98,7 @@ GemmPlan plan_decode(int M, int K, int N) {
   while (depth > 1 && !w4a16::decode_config_fits(MB, tn, depth, xl)) depth /= 2;
   while (tn > 1 && (T % tn != 0 || tn == 5 || !w4a16::decode_config_fits(MB, tn, depth, xl))) --tn;
   // Very long K: split it until the staged operands of a workgroup fit in LDS.
-  while (w4a16::decode_lds_bytes(M, K, tn, waves, split) > w4a16::kDecodeMaxLds && split < G)
+  while (w4a16::decode_lds_bytes(M, K, tn, waves, depth, split) > w4a16::kDecodeMaxLds && split < G)
     split = split * 2 > G ? G : split * 2;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
@@ -155,7 +155,7 @@ GemmPlan plan_silu_mul(int M, int K, int N) {
   while (tn > 2 && (T % tn != 0 || !w4a16::decode_config_fits(MB, tn, 1, xl))) tn -= 2;
   while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
   p.p0 = tn;
-  while (w4a16::decode_lds_bytes(M, K, tn, p.p1, p.split) > w4a16::kDecodeMaxLds && p.split < G)
+  while (w4a16::decode_lds_bytes(M, K, tn, p.p1, p.p2, p.split) > w4a16::kDecodeMaxLds && p.split < G)
     p.split = p.split * 2 > G ? G : p.split * 2;
   return p;
 }
@@ -410,9 +410,9 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
       return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs an even decode column tile count");
     if (p1 != 4 && p1 != 8) return fail(W4A16_ERR_ARG, "decode waves must be 4 or 8");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
-    if (w4a16::decode_lds_bytes(M, K, p0, p1, split) > w4a16::kDecodeMaxLds)
+    if (w4a16::decode_lds_bytes(M, K, p0, p1, p2, split) > w4a16::kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
-                  w4a16::decode_lds_bytes(M, K, p0, p1, split), w4a16::kDecodeMaxLds);
+                  w4a16::decode_lds_bytes(M, K, p0, p1, p2, split), w4a16::kDecodeMaxLds);
     if (!w4a16::decode_config_fits((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)))
       return fail(W4A16_ERR_ARG, "decode configuration needs %d ring and accumulator registers per lane (limit 176)",
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));

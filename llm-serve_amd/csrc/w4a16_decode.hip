@@ -48,16 +48,19 @@ struct DecodeArgs {
 // LDS layout of the staged operands.  A wave owns at most `items` groups (its groups
 // gi = wave + i W of the workgroup's K range); its slice holds, per item i, scale pairs
 // [items][TN * 8] words, zero words [items][TN * 2], then (XL) activations [items][M][128]
-// bf16 with 16-byte chunks swizzled by row.  Region sizes are rounded so that the last
+// bf16 with 16-byte chunks swizzled by row, then (pre) the dequant operands built from
+// the scales and zeros (build_tile_scales): C inputs [items][TN][16 columns] x 16 bytes and
+// diagonals [items][TN][16] x 8 bytes.  Region sizes are rounded so that the last
 // direct-to-LDS load of a region (64 lanes x 4 or 16 bytes) stays in it.  The cross-wave
 // reduction reuses the same memory after the streaming loop.
 struct DecodeLds {
-  uint32_t s_off, z_off, x_off, wave_bytes, staged, reduce, total;
+  uint32_t s_off, z_off, x_off, c_off, d_off, wave_bytes, staged, reduce, total;
 };
 
 __host__ __device__ constexpr uint32_t round_up(uint32_t v, uint32_t a) { return (v + a - 1) / a * a; }
 
-__host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int waves, int split, bool xl) {
+__host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int waves, int split, bool xl,
+                                                      bool pre) {
   const int G = K / kGroup;
   const uint32_t n_gmax = static_cast<uint32_t>((G + split - 1) / split);
   const uint32_t items = (n_gmax + waves - 1) / waves;
@@ -65,7 +68,9 @@ __host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int
   l.s_off = 0;
   l.z_off = round_up(items * tn * 8u * 4u, 256u);
   l.x_off = l.z_off + round_up(items * tn * 2u * 4u, 256u);
-  l.wave_bytes = round_up(l.x_off + (xl ? round_up(items * static_cast<uint32_t>(M) * 256u, 1024u) : 0u), 1024u);
+  l.c_off = l.x_off + (xl ? round_up(items * static_cast<uint32_t>(M) * 256u, 1024u) : 0u);
+  l.d_off = l.c_off + (pre ? items * tn * 16u * 16u : 0u);
+  l.wave_bytes = round_up(l.d_off + (pre ? items * tn * 16u * 8u : 0u), 256u);
   l.staged = l.wave_bytes * static_cast<uint32_t>(waves);
   l.reduce = static_cast<uint32_t>(waves) * ((M + 15) / 16) * tn * 1024u;
   l.total = l.staged > l.reduce ? l.staged : l.reduce;
@@ -120,19 +125,30 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, c
   }
 }
 
-// Multiply-accumulate one group: scales and zeros (and, with XL, the activation fragments)
-// come from the wave's LDS slice `wl`; i is the group's item index within the wave.
-template <int MB, int TN, bool XL>
+// Multiply-accumulate one group: the dequant operands (built from the staged scales and
+// zeros, or with PRE read prebuilt) and, with XL, the activation fragments come from the
+// wave's LDS slice `wl`; i is the group's item index within the wave.
+template <int MB, int TN, bool XL, bool PRE>
 __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL>& st,
                                                      const uint8_t* wl, const DecodeLds& lay, int i, int M,
                                                      const NibbleConsts& nib, int lane) {
   const int c = lane & 15;
-  const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off) + i * (TN * 8) + (c >> 1);
-  const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off) + i * (TN * 2) + (c >> 3);
-  const int zshift = awq_shift(lane & 7);
   TileScale ts[TN];
+  if constexpr (PRE) {
+    const f32x4_t* lc = reinterpret_cast<const f32x4_t*>(wl + lay.c_off) + i * (TN * 16) + c;
+    const s16x4_t* ld = reinterpret_cast<const s16x4_t*>(wl + lay.d_off) + i * (TN * 16) + c;
 #pragma unroll
-  for (int tt = 0; tt < TN; ++tt) ts[tt] = make_tile_scale(ls[tt * 8], (lz[tt * 2] >> zshift) & 0xFu, lane);
+    for (int tt = 0; tt < TN; ++tt) {
+      ts[tt].cin = lc[tt * 16];
+      ts[tt].diag = ld[tt * 16];
+    }
+  } else {
+    const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off) + i * (TN * 8) + (c >> 1);
+    const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off) + i * (TN * 2) + (c >> 3);
+    const int zshift = awq_shift(lane & 7);
+#pragma unroll
+    for (int tt = 0; tt < TN; ++tt) ts[tt] = make_tile_scale(ls[tt * 8], (lz[tt * 2] >> zshift) & 0xFu, lane);
+  }
   u32x4_t a[MB][4];
   if constexpr (XL) {
     // Rows >= M read row M - 1: their outputs are never stored.
@@ -207,6 +223,30 @@ __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay
   }
 }
 
+// Dequant operands of every (item, tile, column) of the wave, built once from the staged
+// scale pairs and zero words: one lane per column instead of every lane per tile and group
+// (make_tile_scale depends on the lane only through lane % 4, which equals the column's
+// c % 4 for every lane that later reads entry c).  It saves about 12 VALU instructions per
+// tile and group but puts LDS round trips before the first group: measured on MI355X it
+// pays with 8 waves and a ring at least two groups deep (gate_up M=16 -4 %), and costs
+// 2-8 % with 4 waves or a one-group ring, where that latency is not hidden.
+template <int TN>
+__device__ __forceinline__ void build_tile_scales(uint8_t* wl, const DecodeLds& lay, int n_items, int lane) {
+  const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off);
+  const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off);
+  f32x4_t* lc = reinterpret_cast<f32x4_t*>(wl + lay.c_off);
+  s16x4_t* ld = reinterpret_cast<s16x4_t*>(wl + lay.d_off);
+  const int entries = n_items * TN * 16;
+  for (int e = lane; e < entries; e += 64) {
+    const int c = e & 15;
+    const int it = e >> 4;  // item * TN + tile
+    const uint32_t z = (lz[it * 2 + (c >> 3)] >> awq_shift(c & 7)) & 0xFu;
+    const TileScale t = make_tile_scale(ls[it * 8 + (c >> 1)], z, c);
+    lc[e] = t.cin;
+    ld[e] = t.diag;
+  }
+}
+
 template <int MB, int TN, int DEPTH, int WAVES, bool XL>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
@@ -233,7 +273,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const bool act = TN % 2 == 0 && up_tiles != 0;
   const int tb = act ? cb * H : cb * TN;
   const int dt = act ? up_tiles - H : 0;
-  const DecodeLds lay = decode_lds_layout(M, K, TN, W, split, XL);
+  constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
+  const DecodeLds lay = decode_lds_layout(M, K, TN, W, split, XL, kPre);
 
   DecodeSources src;
   src.x = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
@@ -271,13 +312,14 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // them (they do when those hit in cache), so a partial vmcnt wait does not cover them:
   // wait for everything, the ring included, before the first group reads the slice.
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);  // vmcnt(0), expcnt and lgkmcnt untouched
+  if constexpr (kPre) build_tile_scales<TN>(wl, lay, n_items, lane);
 
   const NibbleConsts nib = nibble_consts();
   for (int base = 0; base < n_items; base += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int i = base + d;
-      if (i < n_items) compute_decode_stage<MB, TN, XL>(acc, ring[d], wl, lay, i, M, nib, lane);
+      if (i < n_items) compute_decode_stage<MB, TN, XL, kPre>(acc, ring[d], wl, lay, i, M, nib, lane);
       const int in = i + DEPTH;
       __builtin_amdgcn_sched_barrier(0);
       load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
@@ -384,8 +426,9 @@ bool decode_stages_x(int M, int K, int split) {
   return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
 }
 
-size_t decode_lds_bytes(int M, int K, int tn, int waves, int split) {
-  return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split)).total;
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
+  return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split), decode_prebuilt_scales(waves, depth))
+      .total;
 }
 
 constexpr int kMaxDevices = 64;
@@ -396,7 +439,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
-  const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL).total;
+  const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, decode_prebuilt_scales(WAVES, DEPTH)).total;
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
     // call from a racing thread is harmless).  A failed call returns before the launch: a

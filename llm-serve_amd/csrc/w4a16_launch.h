@@ -36,9 +36,12 @@ constexpr size_t kDecodeMaxStagedX = 32 * 1024;  // activations staged in LDS (M
 
 // Whether the activations of an (M, K, split) problem are staged in LDS.
 bool decode_stages_x(int M, int K, int split);
-// LDS bytes of a decode workgroup: staged scales, zeros (and activations), or the
-// cross-wave reduction, whichever is larger.
-size_t decode_lds_bytes(int M, int K, int tn, int waves, int split);
+// Whether a decode configuration builds its dequant operands once per wave in LDS
+// (8 waves and a ring at least two groups deep) instead of per tile and group.
+constexpr bool decode_prebuilt_scales(int waves, int depth) { return waves == 8 && depth >= 2; }
+// LDS bytes of a decode workgroup: staged scales, zeros (and activations, and prebuilt
+// dequant operands), or the cross-wave reduction, whichever is larger.
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split);
 
 // Register budget of a decode configuration (16-row activation blocks mb, tiles tn, ring
 // depth, activations staged or not): fp32 accumulators plus the ring of in-flight loads,

@@ -94,3 +94,22 @@ def random_x_gpu(m: int, k: int, seed: int, outliers: bool = False) -> torch.Ten
         cols = torch.randperm(k, device="cuda", generator=g)[: round(0.01 * k)]
         x[:, cols] *= 20.0
     return x.to(torch.bfloat16)
+
+
+def decode_config_accepted(m: int, k: int, tn: int, depth: int, waves: int, split: int) -> bool:
+    """The library's admission rules for a decode configuration, restated: activations
+    staged for M <= 4 within 32 KiB; per wave, its share of the groups' scale pairs and zero
+    words, staged activations and (8 waves with a ring of >= 2 groups) the prebuilt dequant
+    operands, 384 bytes per tile and group; the workgroup's LDS (those slices or the
+    cross-wave reduction) <= 156 KiB; accumulator + ring registers <= 176."""
+    mb = (m + 15) // 16
+    n_gmax = -(-(k // 128) // split)
+    items = -(-n_gmax // waves)
+    xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
+    pre = waves == 8 and depth >= 2
+    up = lambda v, a: -(-v // a) * a
+    wave = up(up(items * tn * 32, 256) + up(items * tn * 8, 256) + (up(items * m * 256, 1024) if xl else 0)
+              + (items * tn * 384 if pre else 0), 256)
+    lds = max(waves * wave, waves * mb * tn * 1024)
+    regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
+    return lds <= 156 * 1024 and regs <= 176

@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 import torch
 
-from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, golden_cases, pkg,
-                         random_awq_gpu, random_x_gpu, rel_err, to_gpu)
+from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, decode_config_accepted, golden_cases,
+                         pkg, random_awq_gpu, random_x_gpu, rel_err, to_gpu)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -63,19 +63,6 @@ def test_single_token_wide_gemv_reference_recipe(gpu_lib):
 
 
 DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4, 6) for w in (4, 8) for d in (1, 2, 4) for s in (1, 3, 8)]
-
-
-def decode_config_accepted(m, k, tn, depth, waves, split):
-    """The library's admission rules (LDS and ring registers), restated: staged activations
-    for M <= 4 within 32 KiB, LDS <= 156 KiB, accumulator + ring registers <= 176."""
-    mb = (m + 15) // 16
-    n_gmax = -(-(k // 128) // split)
-    xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
-    up = lambda v, a: -(-v // a) * a
-    staged = up(n_gmax * tn * 32, 256) + up(n_gmax * tn * 8, 256) + (up(n_gmax * m * 256, 1024) if xl else 0)
-    lds = max(staged, waves * mb * tn * 1024)
-    regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
-    return lds <= 156 * 1024 and regs <= 176
 
 
 @pytest.mark.parametrize("m", [1, 3, 5, 16, 33, 64])

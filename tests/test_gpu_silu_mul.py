@@ -18,7 +18,8 @@ import numpy as np
 import pytest
 import torch
 
-from awq_helpers import GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, random_awq_gpu, random_x_gpu, rel_err, to_gpu
+from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, decode_config_accepted, random_awq_gpu, random_x_gpu,
+                         rel_err, to_gpu)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -48,18 +49,6 @@ def test_fused_matches_oracle(gpu_lib, m):
 
 
 FUSED_DECODE_CONFIGS = [(tn, w, d, s) for tn in (2, 4, 6) for w in (4, 8) for d in (1, 2, 4) for s in (1, 3, 8)]
-
-
-def decode_config_accepted(m, k, tn, depth, waves, split):
-    """The library's admission rules (restated as in test_gpu_gemm.py)."""
-    mb = (m + 15) // 16
-    n_gmax = -(-(k // 128) // split)
-    xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
-    up = lambda v, a: -(-v // a) * a
-    staged = up(n_gmax * tn * 32, 256) + up(n_gmax * tn * 8, 256) + (up(n_gmax * m * 256, 1024) if xl else 0)
-    lds = max(staged, waves * mb * tn * 1024)
-    regs = 4 * mb * tn + depth * 4 * (tn + (0 if xl else 4 * mb))
-    return lds <= 156 * 1024 and regs <= 176
 
 
 @pytest.mark.parametrize("m", [1, 5, 33])
