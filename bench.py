@@ -37,8 +37,15 @@ Also reported (not part of `value`):
     QKV columns (the attention output's shape) with the residual add in its epilogue, the
     fused gate|up GEMM with SiLU * up, down with the residual add -- 144 GEMM launches and
     36 copies per step, one graph;
-  * measured_ceilings: a 1 GiB device copy (read + write GB/s) and torch.matmul
-    (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
+  * measured_ceilings: a 1 GiB device copy (read + write GB/s), plain streaming reads
+    (llm-serve_amd/csrc/probe_read.hip, best of six grid sizes) of 1 GiB and of 52.3 MB
+    per launch (the gate_up weight bytes, rotating over more than 2 x 256 MB), and
+    torch.matmul (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
+    `roofline.measured_frac` is the dominant launch against the 52.3 MB read;
+  * points: every decode point's mean, median, min and max per-launch time over the
+    timed replays;
+  * cpu_baseline.parity_max_rel_err_vs_gpu: the oracle's output against the HIP GEMM's
+    on the same inputs (the baseline's own problem);
   * fused_gate_up: the gate_up GEMM with SiLU(gate) * up in its epilogue
     (w4a16_gemm_silu_mul, [M, 12288] out) against the plain GEMM ([M, 24576] out) and
     against the reference's two steps (the plain GEMM, then torch's SiLU * up on its
@@ -209,14 +216,17 @@ def time_points(points, stream, steps, warmup):
     torch.cuda.synchronize()
     for p, e0, e1 in events:
         per_point[id(p)].append(e0.elapsed_time(e1) / p.launches)
+    time_points.samples = per_point  # per-replay ms per launch, for the spread
     return {id(p): statistics.mean(v) for p, v in ((p, per_point[id(p)]) for p in points)}, \
         start_all.elapsed_time(end_all)
 
 
-def cpu_baseline(seconds_budget: float = 12.0) -> dict:
+def cpu_baseline(seconds_budget: float = 12.0, gpu_gemm=None) -> dict:
     """The oracle (numpy restatement of the reference backend: dequant to bf16, then an
     fp32 BLAS matmul, then bf16) on the host at M=16, K=N=4096 (the O projection), repeated
-    for about `seconds_budget` seconds; the median run is reported."""
+    for about `seconds_budget` seconds; the median run is reported.  With gpu_gemm (a
+    function of the problem's bit arrays returning the HIP GEMM's bf16 output bits), also
+    the parity of the two results: max |y_gpu - y_cpu| / max(|y_cpu|, rms(y_cpu))."""
     from oracle import awq_oracle as ora
 
     try:
@@ -227,7 +237,7 @@ def cpu_baseline(seconds_budget: float = 12.0) -> dict:
     m, k, n = 16, 4096, 4096
     p = ora.make_problem(seed=0, m=m, k=k, n=n)
     run = lambda: ora.awq_linear_bf16_bits(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)  # noqa: E731
-    run()
+    y_cpu = ora.bf16_bits_to_f32(run()).astype("float64")
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 or (time.perf_counter() - t_start < seconds_budget and len(times) < 1000):
@@ -235,11 +245,30 @@ def cpu_baseline(seconds_budget: float = 12.0) -> dict:
         run()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    parity = None
+    if gpu_gemm is not None:
+        y_gpu = ora.bf16_bits_to_f32(gpu_gemm(p)).astype("float64")
+        rms = float((y_cpu ** 2).mean() ** 0.5)
+        parity = round(float((abs(y_gpu - y_cpu) / (abs(y_cpu).clip(min=rms))).max()), 5)
     return {"value": round(algorithmic_bytes(m, k, n) / t / 1e9, 3), "unit": "GB/s", "cores": int(threads),
+            "parity_max_rel_err_vs_gpu": parity,
             "kind": "port",
             "sample": f"oracle dequant+fp32 matmul, M={m} K={k} N={n} (O proj), median of {len(times)} runs "
                       f"over {time.perf_counter() - t_start:.1f} s, {t * 1e3:.1f} ms/GEMM, host "
                       f"{platform.processor() or platform.machine()}, os.cpu_count()={os.cpu_count()}"}
+
+
+def gpu_gemm_bits(pkg, dev, prob) -> "numpy.ndarray":
+    """The HIP GEMM over one problem of bit arrays (AutoAWQ tensors, bf16 bits) -> bf16 bits."""
+    import numpy as np
+    qw = torch.from_numpy(prob["qweight"]).to(dev)
+    qz = torch.from_numpy(prob["qzeros"]).to(dev)
+    sc = torch.from_numpy(prob["scales_bits"].view(np.int16)).to(dev).view(torch.bfloat16)
+    x = torch.from_numpy(prob["x_bits"].view(np.int16)).to(dev).view(torch.bfloat16)
+    packed = pkg.repack_awq_qweight(qw)
+    y = pkg.awq_linear(x, packed, qz, sc, group_size=128)
+    torch.cuda.synchronize()
+    return y.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
 MIXED_M = 48 * 1 + 8 * 4 + 432
@@ -364,19 +393,70 @@ def layer_stack_chained(lib, dev, stream, reps: int, layers) -> dict:
     return out
 
 
+def read_ceiling(dev, stream, nbytes: int, copies: int):
+    """Best GB/s of a plain streaming read (csrc/probe_read.hip, libw4a16_probe.so) over
+    `copies` rotating buffers of `nbytes` each, one launch per buffer, all captured in one
+    graph, over a sweep of grid sizes: what a kernel reading that many bytes per launch
+    gets from HBM on this GPU, launch overhead included.  None if the probe is not built."""
+    import ctypes
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "llm-serve_amd", "csrc", "libw4a16_probe.so")
+    if not os.path.exists(path):
+        return None
+    probe = ctypes.CDLL(path)
+    probe.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    nbytes -= nbytes % 16
+    bufs = [torch.full((nbytes // 2,), 1.0, dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+    best = None
+    for blocks in (512, 1024, 2048, 4096, 8192, 16384):
+        sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+
+        def run():
+            sp = torch.cuda.current_stream(dev).cuda_stream
+            for b in bufs:
+                if probe.probe_read(b.data_ptr(), nbytes, sink.data_ptr(), blocks, sp) != 0:
+                    raise RuntimeError("probe_read launch failed")
+
+        gbs = nbytes / (time_graph(run, stream, 5) / copies * 1e-3) / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, blocks)
+    return best
+
+
+def measured_frac(achieved_gbs: float, ceilings) -> dict:
+    """The roofline kernel against the measured plain read of its own weight bytes per launch."""
+    if not ceilings:
+        return {}
+    key = next((k for k in ceilings if k.startswith("read_") and k.endswith("MB_per_launch_GB/s")), None)
+    if key is None:
+        return {}
+    return {"measured_peak": ceilings[key], "measured_peak_kind": key.removesuffix("_GB/s"),
+            "measured_frac": round(achieved_gbs / ceilings[key], 4)}
+
+
 def measured_ceilings(dev, stream) -> dict:
-    """A 1 GiB device-to-device copy and a hipBLASLt bf16 GEMM at the prefill gate_up shape."""
+    """A 1 GiB device-to-device copy, read-only streams of 1 GiB and of the dominant decode
+    launch's weight bytes (rotating over more than 2 x 256 MB), and a hipBLASLt bf16 GEMM at
+    the prefill gate_up shape."""
     src = torch.empty(2 ** 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     ms = time_graph(lambda: dst.copy_(src), stream, 10)
     copy_gbs = 2 * src.numel() * 2 / (ms * 1e-3) / 1e9
     del src, dst
+    read_1g = read_ceiling(dev, stream, 1 << 30, 2)
+    dk, dn = SHAPES[DOMINANT[0]]
+    wb = weight_bytes(dk, dn)
+    read_dom = read_ceiling(dev, stream, wb, max(2, -(-2 * CACHE_BYTES // wb)))
+    reads = {}
+    if read_1g and read_dom:
+        reads = {"read_1GiB_GB/s": round(read_1g[0], 1),
+                 f"read_{wb / 1e6:.1f}MB_per_launch_GB/s": round(read_dom[0], 1),
+                 "read_probe_blocks": {"1GiB": read_1g[1], f"{wb / 1e6:.1f}MB": read_dom[1]}}
     k, n = SHAPES["gate_up"]
     a = torch.randn((PREFILL_M, k), device=dev).to(torch.bfloat16)
     b = torch.randn((k, n), device=dev).to(torch.bfloat16)
     c = torch.empty((PREFILL_M, n), dtype=torch.bfloat16, device=dev)
     ms = time_graph(lambda: torch.matmul(a, b, out=c), stream, 10)
-    return {"copy_1GiB_read+write_GB/s": round(copy_gbs, 1),
+    return {"copy_1GiB_read+write_GB/s": round(copy_gbs, 1), **reads,
             "hipblaslt_bf16_gate_up_m2048_TFLOP/s": round(2 * PREFILL_M * n * k / (ms * 1e-3) / 1e12, 1)}
 
 
@@ -563,11 +643,15 @@ def main(argv=None):
     dom_ms = per_launch[id(dom)]
     dom_gbs = algorithmic_bytes(dom.m, dom.k, dom.n) / (dom_ms * 1e-3) / 1e9
     points_out = []
+    samples = time_points.samples
     for p in decode_points:
         ms = per_launch[id(p)]
         gbs = algorithmic_bytes(p.m, p.k, p.n) / (ms * 1e-3) / 1e9
+        sv = samples[id(p)]
         points_out.append({"shape": p.name, "M": p.m, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "split": p.split, "copies": p.launches})
+                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "split": p.split, "copies": p.launches,
+                           "us_median": round(statistics.median(sv) * 1e3, 3),
+                           "us_min": round(min(sv) * 1e3, 3), "us_max": round(max(sv) * 1e3, 3)})
         if args.details:
             print(f"decode {p.name:8s} M={p.m:3d} {ms * 1e3:8.2f} us  {gbs:8.1f} GB/s  split={p.split}",
                   file=sys.stderr)
@@ -615,7 +699,7 @@ def main(argv=None):
         if args.details:
             print(f"checkpoint layer: {json.dumps(ckpt_layer)}", file=sys.stderr)
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(gpu_gemm=lambda prob: gpu_gemm_bits(pkg, dev, prob))
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -636,7 +720,7 @@ def main(argv=None):
                      "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "algorithmic_bytes": algorithmic_bytes(dom.m, dom.k, dom.n),
-                     "launch_us": round(dom_ms * 1e3, 3)},
+                     "launch_us": round(dom_ms * 1e3, 3), **measured_frac(dom_gbs, ceilings)},
         "cpu_baseline": cpu,
         "prefill_m2048": prefill,
         "mixed_m512": mixed,

@@ -61,5 +61,23 @@ def build_library(extra_flags: list[str] | None = None, jobs: int = 4) -> str:
     return LIB_PATH
 
 
+PROBE_SOURCE = "probe_read.hip"
+PROBE_PATH = os.path.join(CSRC, "libw4a16_probe.so")
+
+
+def build_probe() -> str:
+    """Compile the benchmark's read probe (csrc/probe_read.hip) into libw4a16_probe.so, a
+    measurement helper kept out of libw4a16.so.  Returns its path."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    tmp = PROBE_PATH + ".tmp"
+    cmd = [hipcc(), *COMPILE_FLAGS, "-shared", os.path.join(CSRC, PROBE_SOURCE), "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SOURCE}:\n{proc.stderr}")
+    os.replace(tmp, PROBE_PATH)
+    return PROBE_PATH
+
+
 if __name__ == "__main__":
     print(build_library())
+    print(build_probe())

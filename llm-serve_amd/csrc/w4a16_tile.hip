@@ -94,7 +94,7 @@ __device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src,
 // j + 1's fragments are read and its weights dequantized while step j's main MFMAs run, so
 // the VALU dequant of one step can hide under the matrix work of the previous one.  The
 // order within a step is left to the compiler: explicit scheduling groups (one main MFMA,
-// then two VALU and one LDS read) measured 5-7 % slower on MI355X at M = 512 and 2048.
+// then two VALU and one LDS read) measured 1.3-2.5 % slower on MI355X at M = 512 and 2048.
 template <int WM, int TW>
 __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const BGroup<TW>& b,
                                           const NibbleConsts& nib, int lane) {
