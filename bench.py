@@ -14,10 +14,14 @@ Method
     streams a different copy and the copies of one point exceed 2 x 256 MB (the
     Infinity Cache), i.e. decode bytes come from HBM.
   * Each point's launches are captured once in a HIP graph (torch.cuda.CUDAGraph) and
-    replayed; HIP events recorded on the replay stream bracket each replay, giving the
-    average kernel duration with host launch overhead removed.  Every timed region is
-    preceded by WARM_MS of untimed replays of the same graphs: after a host-side pause the
-    clocks take tens of milliseconds of work to come back up.
+    replayed back to back, point after point: `steps` replays (>= 220 launches at 20 steps)
+    in four blocks, each bracketed by HIP events on the replay stream, giving the average
+    kernel duration with host launch overhead removed (the dispatch gap between
+    back-to-back kernels, about 1 us, stays in).  Every timed region is preceded by WARM_MS
+    of untimed replays of the same graph: after a host-side pause the clocks take tens of
+    milliseconds of work to come back up.  The cost of alternating between the four
+    projections' kernels within a decode step (up to 2 us per launch for gate_up when its
+    points are interleaved with the others') is what the stack36 legs measure.
   * Algorithmic bytes per GEMM = K N / 2 + K N / 256 + K N / 64 + 2 M K + 2 M N
     (int4 weights, int32 zeros, bf16 scales, bf16 x and y); flops = 2 M N K.
   * `roofline` describes the dominant launch (the decode point with the longest
@@ -42,8 +46,8 @@ Also reported (not part of `value`):
     per launch (the gate_up weight bytes, rotating over more than 2 x 256 MB), and
     torch.matmul (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
     `roofline.measured_frac` is the dominant launch against the 52.3 MB read;
-  * points: every decode point's mean, median, min and max per-launch time over the
-    timed replays;
+  * points: every decode point's mean per-launch time and the median, min and max of its
+    four timed blocks;
   * cpu_baseline.parity_max_rel_err_vs_gpu: the oracle's output against the HIP GEMM's
     on the same inputs (the baseline's own problem);
   * fused_gate_up: the gate_up GEMM with SiLU(gate) * up in its epilogue
@@ -184,41 +188,41 @@ def warm_up(replay, min_ms: float = WARM_MS) -> None:
             return
 
 
+TIMED_BLOCKS = 4
+
+
 def time_points(points, stream, steps, warmup):
-    """Replay every point's graph `warmup` times untimed, then for WARM_MS more, then `steps`
-    times timed.  Returns (per-point mean launch ms, total timed ms)."""
+    """Each point in turn: capture its launches (one per rotating weight copy) in a HIP
+    graph, replay it `warmup` times and then for WARM_MS untimed, then `steps` times back to
+    back in TIMED_BLOCKS blocks, each bracketed by HIP events on the replay stream (at 20
+    steps every decode point runs >= 220 timed launches).  Returns (per-point mean ms per
+    launch, total timed ms); time_points.samples holds each block's ms per launch."""
+    per_point, samples, total = {}, {}, 0.0
     for p in points:
         p.capture(stream)
-    for _ in range(warmup):
-        for p in points:
-            p.graph.replay()
-
-    def replay_all():
-        for p in points:
-            p.graph.replay()
-
-    warm_up(replay_all)
-    per_point = {id(p): [] for p in points}
-    events = []
-    start_all = torch.cuda.Event(enable_timing=True)
-    end_all = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start_all.record(stream)
-        for _ in range(steps):
-            for p in points:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
                 p.graph.replay()
+            warm_up(p.graph.replay)
+        nb = max(1, min(TIMED_BLOCKS, steps))
+        counts = [steps // nb + (1 if i < steps % nb else 0) for i in range(nb)]
+        events = []
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for cnt in counts:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(cnt):
+                    p.graph.replay()
                 e1.record(stream)
-                events.append((p, e0, e1))
-        end_all.record(stream)
-    torch.cuda.synchronize()
-    for p, e0, e1 in events:
-        per_point[id(p)].append(e0.elapsed_time(e1) / p.launches)
-    time_points.samples = per_point  # per-replay ms per launch, for the spread
-    return {id(p): statistics.mean(v) for p, v in ((p, per_point[id(p)]) for p in points)}, \
-        start_all.elapsed_time(end_all)
+                events.append((cnt, e0, e1))
+        torch.cuda.synchronize()
+        block_ms = [e0.elapsed_time(e1) for _, e0, e1 in events]
+        per_point[id(p)] = sum(block_ms) / (steps * p.launches)
+        samples[id(p)] = [ms / (cnt * p.launches) for (cnt, _, _), ms in zip(events, block_ms)]
+        total += sum(block_ms)
+    time_points.samples = samples
+    return per_point, total
 
 
 def cpu_baseline(seconds_budget: float = 12.0, gpu_gemm=None) -> dict:
@@ -556,8 +560,9 @@ def read_traffic(path: str = TRAFFIC_FILE):
 
 
 def profile_point(lib, spec: str, steps: int, dev) -> int:
-    """Counter/trace workload: one 256 MiB bf16 copy (3x) for calibration, then `steps`
-    direct launches of one decode or prefill point over rotating weights.  SHAPE+silu:M
+    """Counter/trace workload: one 256 MiB bf16 copy (3x) for calibration, WARM_MS of
+    untimed launches, then `steps` direct launches of one decode or prefill point over
+    rotating weights.  SHAPE+silu:M
     launches the fused SiLU * up GEMM of that (gate|up) shape; quantize:0 launches the
     quantizer over a [24576, 4096] bf16 weight."""
     name, m = spec.split(":")
@@ -581,11 +586,14 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
     x = torch.randn((m, k), device=dev).to(torch.bfloat16)
     p = Point(lib, name, m, k, n, weights, x)
     stream = torch.cuda.current_stream(dev)
-    for packed, qzeros, scales in weights:  # warm-up
-        if entry(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), p.y.data_ptr(), m, k, n,
-                 128, p.ws.data_ptr() if p.ws_len else None, p.ws_len, stream.cuda_stream) != 0:
-            raise RuntimeError(lib.last_error())
-    torch.cuda.synchronize()
+
+    def launch_all():
+        for packed, qzeros, scales in weights:
+            if entry(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), p.y.data_ptr(), m, k, n,
+                     128, p.ws.data_ptr() if p.ws_len else None, p.ws_len, stream.cuda_stream) != 0:
+                raise RuntimeError(lib.last_error())
+
+    warm_up(launch_all)  # WARM_MS of the same launches first (clock ramp)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     done = 0
