@@ -140,10 +140,16 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
       read_a(a[c ^ 1], j + 1);
       dequant(bf[c ^ 1], j + 1);
     }
+    // 128-row waves raise their issue priority while they issue the step's main MFMAs, so
+    // that the SIMD's other wave (in its dequant or LDS reads) does not starve the matrix
+    // pipe: measured on MI355X 2-3 % faster at M = 2048 (gate_up, down, O), while the
+    // 64-row configurations ran 3-4 % slower with it.
+    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
       for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[c][mt], bf[c][tt], acc[mt][tt]);
+    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(0);
   }
 }
 
