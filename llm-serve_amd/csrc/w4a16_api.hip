@@ -61,9 +61,10 @@ int tile_bn(const GemmPlan& p) {
 // split-K partials costs an extra pass over M x N fp32:
 //  * wide layers (N >= 16384): 32-column workgroups at M = 1 (768 for gate_up), 48 up to
 //    M = 8, 96 beyond (fewer, wider workgroups once x is 16 rows), 64 at M > 32;
-//  * medium layers (4096 < N < 16384): 32 columns up to M = 16, then 48 with K in two;
+//  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 16, then 48 with K
+//    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
-//    N = 4096, four groups in flight per wave beyond M = 4), then wider ones with K split;
+//    N = 4096), then wider ones with K split;
 //  * narrow layers with long K: 16 columns up to M = 4, then wider ones with K split in two
 //    or four.
 GemmPlan plan_decode(int M, int K, int N) {
@@ -78,12 +79,11 @@ GemmPlan plan_decode(int M, int K, int N) {
     else if (M <= 32) { tn = 6; waves = 4; }
     else { tn = 4; waves = 4; depth = 1; }
   } else if (N > 4096) {
-    if (M <= 8) tn = 2;
-    else if (M <= 16) { tn = 2; waves = 4; }
+    if (M <= 1) tn = 1;
+    else if (M <= 16) tn = 2;
     else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
-    if (M <= 4) tn = 1;
-    else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
+    if (M <= 16) tn = 1;
     else if (M <= 32) { tn = 4; depth = 1; split = 4; }
     else { tn = 2; depth = 1; split = 2; }
   } else {
