@@ -108,7 +108,9 @@ GemmPlan plan_decode(int M, int K, int N) {
 // each), one workgroup per CU; shape 1 = 4 waves (64 columns each), two workgroups per CU.
 //  * Tall problems (M >= 1024): 128-row tiles in shape 3 (wm = 8: every dequantized weight
 //    serves 128 rows) when that grid fills the CUs in even rounds (gate_up, O and down at
-//    M = 2048); otherwise 64-row tiles in shape 1 (N = 6144: 384 vs 768 tiles).
+//    M = 2048) or fits in one round, with K split to fill it (QKV, O and down at M = 1024:
+//    -9 to -16 % against 64-row tiles); otherwise 64-row tiles in shape 1 (N = 6144 at
+//    M = 2048: 384 vs 768 tiles).
 //  * Shorter problems: 64-row tiles; shape 1 when the grid is large (>= 512 tiles), else
 //    shape 3.  K is split in powers of two while the grid stays within one round (shape 3:
 //    256 workgroups; shape 1: 512) and every split keeps >= 8 groups; the fp32 partials
@@ -119,6 +121,13 @@ GemmPlan plan_tile(int M, int K, int N) {
   if (M >= 1024) {
     const int t8 = tiles(8);
     if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+    if (t8 <= 256) {
+      // At most one round of 128-row tiles: split K in powers of two while the grid stays
+      // within one round and every split keeps >= 8 groups.
+      int split = 1;
+      while (split < 4 && t8 * split * 2 <= 256 && 8 * split * 2 <= G) split *= 2;
+      return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, split};
+    }
     return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   }
   const int t = tiles(4);
