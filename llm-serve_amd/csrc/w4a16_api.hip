@@ -60,11 +60,11 @@ int tile_bn(const GemmPlan& p) {
 // workgroup reads its K range of x once), the grid shrinks with it, and the exchange of
 // split-K partials costs an extra pass over M x N fp32:
 //  * wide layers (N >= 16384): 32-column workgroups at M = 1 (768 for gate_up), 48 up to
-//    M = 8, 96 beyond (fewer, wider workgroups once x is 16 rows), 64 at M > 32;
+//    M = 8, 96 up to M = 32 (fewer, wider workgroups once x is 16 rows), 64 at M > 32;
 //  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 16, then 48 with K
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
-//    N = 4096), then wider ones with K split;
+//    N = 4096), then 64 columns with K in four;
 //  * narrow layers with long K: 16 columns up to M = 4, then wider ones with K split in two
 //    or four.
 GemmPlan plan_decode(int M, int K, int N) {
@@ -75,8 +75,7 @@ GemmPlan plan_decode(int M, int K, int N) {
   if (N >= 16384) {
     if (M <= 1) tn = 2;
     else if (M <= 8) tn = 3;
-    else if (M <= 16) tn = 6;
-    else if (M <= 32) { tn = 6; waves = 4; }
+    else if (M <= 32) tn = 6;
     else { tn = 4; waves = 4; depth = 1; }
   } else if (N > 4096) {
     if (M <= 1) tn = 1;
@@ -84,8 +83,7 @@ GemmPlan plan_decode(int M, int K, int N) {
     else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
     if (M <= 16) tn = 1;
-    else if (M <= 32) { tn = 4; depth = 1; split = 4; }
-    else { tn = 2; depth = 1; split = 2; }
+    else { tn = 4; depth = 1; split = 4; }
   } else {
     if (M <= 1) { tn = 1; depth = 4; }
     else if (M <= 4) tn = 1;
