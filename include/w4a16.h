@@ -53,7 +53,7 @@ enum w4a16_dtype {
 
 enum w4a16_regime_id {
   W4A16_REGIME_NONE = 0,   /* M == 0: nothing to launch */
-  W4A16_REGIME_DECODE = 1, /* M <= 64 (M < 48 when N >= 16384): split-K, HBM-bound kernel */
+  W4A16_REGIME_DECODE = 1, /* M <= 64 (M <= 48 when N >= 16384): split-K, HBM-bound kernel */
   W4A16_REGIME_TILE = 2    /* larger M: LDS-tiled bf16 MFMA GEMM */
 };
 

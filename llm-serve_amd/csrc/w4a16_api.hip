@@ -60,7 +60,8 @@ int tile_bn(const GemmPlan& p) {
 // workgroup reads its K range of x once), the grid shrinks with it, and the exchange of
 // split-K partials costs an extra pass over M x N fp32:
 //  * wide layers (N >= 16384): 32-column workgroups at M = 1 (768 for gate_up), 48 up to
-//    M = 8, 96 up to M = 32 (fewer, wider workgroups once x is 16 rows), 64 at M > 32;
+//    M = 8, 96 beyond (fewer, wider workgroups once x is 16 rows), one group in flight per
+//    wave at M > 32 (the registers then hold three 16-row activation blocks);
 //  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 16, then 48 with K
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
@@ -76,7 +77,7 @@ GemmPlan plan_decode(int M, int K, int N) {
     if (M <= 1) tn = 2;
     else if (M <= 8) tn = 3;
     else if (M <= 32) tn = 6;
-    else { tn = 4; waves = 4; depth = 1; }
+    else { tn = 6; depth = 1; }
   } else if (N > 4096) {
     if (M <= 1) tn = 1;
     else if (M <= 16) tn = 2;
@@ -136,14 +137,15 @@ GemmPlan plan_tile(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_TILE, 4, 2, shape, split};
 }
 
-// Regime: the decode kernel up to M = 64, except for wide layers (N >= 16384) from M = 48,
-// where the tile kernel with K split in two is faster (measured on the gate_up shape:
-// 28 vs 31 us at M = 48, 29 vs 42 us at M = 64): there the decode kernel's per-wave
-// activation loads (16 rows per block, re-read for every 16 TN columns) outweigh the
-// tile kernel's shared activation stage.
+// Regime: the decode kernel up to M = 64, except for wide layers (N >= 16384) above M = 48,
+// where the tile kernel with K split in two is faster (measured on the gate_up shape: the
+// decode kernel with 96-column workgroups takes 21.9 / 24.4 us at M = 33 / 48 against the
+// tile kernel's 26.7 / 27.2 us, but at M = 64 its best fitting configuration takes 43 us
+// against 28): with four 16-row activation blocks the 96-column workgroup no longer fits
+// the registers, and narrower ones re-read the activations too often.
 GemmPlan plan(int M, int K, int N) {
   if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
-  if (M > kDecodeMaxM || (M >= 48 && N >= 16384)) return plan_tile(M, K, N);
+  if (M > kDecodeMaxM || (M > 48 && N >= 16384)) return plan_tile(M, K, N);
   return plan_decode(M, K, N);
 }
 

@@ -1,5 +1,5 @@
 // Decode / speculative-verify regime (M <= 64; the planner sends wide layers to the tile
-// kernel from M = 48): HBM-bound split-K kernel.
+// kernel above M = 48): HBM-bound split-K kernel.
 //
 // Each wave streams (128-row group, 16-column tile) weight tiles (1 KiB, one 16-byte load
 // per lane), dequantizes them on the matrix cores (dequant_step: the reference's

@@ -1,4 +1,4 @@
-// Chunked-prefill / mixed-batch regime (M > 64, and M >= 48 for N >= 16384): LDS-tiled bf16
+// Chunked-prefill / mixed-batch regime (M > 64, and M > 48 for N >= 16384): LDS-tiled bf16
 // MFMA GEMM with the int4 weights dequantized in registers.
 //
 // Workgroup = NWM x NWN waves, output tile BM x BN (BM = 16 WM NWM, BN = 16 TW NWN).  Wave

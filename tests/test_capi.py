@@ -88,8 +88,8 @@ def test_regime_boundary_and_split_limits(pkg):
     for k, n in QWEN3.values():
         assert L.regime(0, k, n) == 0
         for m in (1, 4, 8, 16, 32, 64):
-            # decode kernel up to M = 64, except wide layers from M = 48 (tile kernel)
-            assert L.regime(m, k, n) == (2 if m >= 48 and n >= 16384 else 1)
+            # decode kernel up to M = 64, except wide layers above M = 48 (tile kernel)
+            assert L.regime(m, k, n) == (2 if m > 48 and n >= 16384 else 1)
             assert 1 <= L.split_k(m, k, n) <= k // 128
         for m in (65, 128, 512, 2048, 4096):
             assert L.regime(m, k, n) == 2

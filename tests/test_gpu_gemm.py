@@ -161,7 +161,7 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
     qw, qz, s = random_awq_gpu(k, n, seed=11)
     packed = awq_mod().repack_awq_qweight(qw)
     for m in (1, 4, 8, 16, 32, 64):
-        assert pkg().awq_regime(m, k, n) == ("tile" if m >= 48 and n >= 16384 else "decode")
+        assert pkg().awq_regime(m, k, n) == ("tile" if m > 48 and n >= 16384 else "decode")
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
         err = rel_err(y, full_reference(x, qw, qz, s))
