@@ -102,33 +102,30 @@ GemmPlan plan_decode(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
 
-// Tile regime, chosen from sweeps on MI355X over the Qwen3-8B shapes at M = 512 and 2048.
-// Two wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by side along N (32 columns
-// each), one workgroup per CU; shape 1 = 4 waves (64 columns each), two workgroups per CU.
-//  * Tall problems (M >= 1024): 128-row tiles in shape 3 (wm = 8: every dequantized weight
-//    serves 128 rows) when that grid fills the CUs in even rounds (gate_up, O and down at
-//    M = 2048) or fits in one round, with K split to fill it (QKV, O and down at M = 1024:
-//    -9 to -16 % against 64-row tiles); otherwise 64-row tiles in shape 1 (N = 6144 at
-//    M = 2048: 384 vs 768 tiles).
-//  * Shorter problems: 64-row tiles; shape 1 when the grid is large (>= 512 tiles), else
-//    shape 3.  K is split in powers of two while the grid stays within one round (shape 3:
-//    256 workgroups; shape 1: 512) and every split keeps >= 8 groups; the fp32 partials
-//    are reduced by the last workgroup of each tile.
+// Tile regime, chosen from sweeps of every tile configuration on MI355X over the Qwen3-8B
+// shapes at M = 128 .. 2048.  Two wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by
+// side along N (32 columns each), one workgroup per CU; shape 1 = 4 waves (64 columns each),
+// two workgroups per CU.
+//  * 128-row tiles in shape 3 (wm = 8: every dequantized weight serves 128 rows) when their
+//    grid fills the CUs in even rounds at M >= 1024 (gate_up, O and down at M = 2048), or
+//    fills 144 .. 256 of one round's workgroups once K is split in two or four with >= 16
+//    groups per split, for M > 128 (QKV and down at M = 384 .. 1024, O at M = 768 and 1024,
+//    gate_up at M = 256: up to 21 % faster than 64-row tiles there; at M <= 128 half-empty
+//    128-row tiles lose, e.g. 45 vs 33 us for gate_up at M = 64).
+//  * Otherwise 64-row tiles: at M >= 1024 in shape 1 (N = 6144 at M = 2048: 384 vs 768
+//    tiles); below, shape 1 when the grid is large (>= 512 tiles), else shape 3, with K
+//    split in powers of two while the grid stays within one round (shape 3: 256 workgroups;
+//    shape 1: 512) and every split keeps >= 8 groups.  Split-K partials are reduced by the
+//    last workgroup of each tile.
 GemmPlan plan_tile(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   auto tiles = [&](int wm) { return ceil_div(M, 16 * wm) * ceil_div(N, 256); };
-  if (M >= 1024) {
-    const int t8 = tiles(8);
-    if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
-    if (t8 <= 256) {
-      // At most one round of 128-row tiles: split K in powers of two while the grid stays
-      // within one round and every split keeps >= 8 groups.
-      int split = 1;
-      while (split < 4 && t8 * split * 2 <= 256 && 8 * split * 2 <= G) split *= 2;
-      return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, split};
-    }
-    return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
-  }
+  const int t8 = tiles(8);
+  if (M >= 1024 && t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+  int s8 = 1;
+  while (s8 < 4 && t8 * s8 * 2 <= 256 && 16 * s8 * 2 <= G) s8 *= 2;
+  if (M > 128 && t8 * s8 >= 144 && t8 * s8 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, s8};
+  if (M >= 1024) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   const int t = tiles(4);
   const int shape = t >= 512 ? 1 : 3;
   const int cap = shape == 1 ? 512 : 256;
