@@ -101,7 +101,7 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 
 # (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2)]
-TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3)]
+TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3, 4)]
 
 
 @pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256)])
@@ -178,6 +178,22 @@ def test_full_qwen3_shapes_prefill_chunk_with_outliers(gpu_lib, shape):
     y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
     err = rel_err(y, full_reference(x, qw, qz, s))
     assert err <= GEMM_REL_TOL, err
+
+
+@pytest.mark.parametrize("shape,m", [("qkv", 768), ("o", 768), ("gate_up", 256), ("down", 384), ("down", 768),
+                                     ("gate_up", 48), ("gate_up", 49)])
+def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
+    """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
+    (QKV / O / down at M = 768, gate_up at 256, down at 384) and the decode / tile boundary
+    of the wide layer (gate_up: decode up to M = 48, tiles from 49), at full shapes."""
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
+    packed = awq_mod().repack_awq_qweight(qw)
+    x = random_x_gpu(m, k, seed=m, outliers=True)
+    assert pkg().awq_regime(m, k, n) == ("decode" if m <= 48 else "tile")
+    y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+    err = rel_err(y, full_reference(x, qw, qz, s))
+    assert err <= GEMM_REL_TOL, (shape, m, err)
 
 
 @pytest.mark.parametrize("shape", ["gate_up", "down"])
