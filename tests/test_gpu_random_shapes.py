@@ -1,0 +1,36 @@
+"""Seeded random shapes through the default planner: every regime, column-tile count, K
+split and tile configuration that the planner reaches for M in 1..3000, K in 128..8192
+and N in 64..8192 (multiples of 128 and 64), against the fp32 product of the reference's
+bf16 weights (same metric and tolerance as every GEMM test)."""
+import numpy as np
+import pytest
+import torch
+
+from awq_helpers import GEMM_REL_TOL, awq_mod, pkg, random_awq_gpu, random_x_gpu, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def shapes(seed: int, count: int):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        k = 128 * int(rng.integers(1, 65))
+        n = 64 * int(rng.integers(1, 129))
+        m = int(rng.choice([rng.integers(1, 17), rng.integers(17, 65), rng.integers(65, 513), rng.integers(513, 3001)]))
+        out.append((m, k, n))
+    return out
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_random_shapes_match_reference(gpu_lib, seed):
+    awq = awq_mod()
+    for i, (m, k, n) in enumerate(shapes(seed, 12)):
+        print(f"random shape seed={seed} i={i} M={m} K={k} N={n} regime={pkg().awq_regime(m, k, n)} "
+              f"split={gpu_lib.split_k(m, k, n)}", flush=True)
+        qw, qz, s = random_awq_gpu(k, n, seed=1000 * seed + i)
+        x = random_x_gpu(m, k, seed=i, outliers=bool(i % 2))
+        y = awq.awq_linear(x, awq.repack_awq_qweight(qw), qz, s, group_size=128)
+        want = x.float() @ awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
+        assert y.shape == (m, n)
+        assert rel_err(y, want) <= GEMM_REL_TOL, (m, k, n)
