@@ -55,7 +55,13 @@ Also reported (not part of `value`):
     against the reference's two steps (the plain GEMM, then torch's SiLU * up on its
     output), at M in {1, 16, 64, 512, 2048};
   * quantize: the GPU AWQ quantizer over a [24576, 4096] bf16 weight (GB/s of weight
-    read + packed output written).
+    read + packed output written);
+  * stack36_normed: stack36_chained's weights with both RMSNorms of each layer, the
+    residual add in the norm prologue (the reference's order): w4a16_gemm_rmsnorm for
+    input_layernorm + QKV and post_attention_layernorm + gate|up + SiLU * up, plain O and
+    down -- 144 GEMM and 72 norm launches per step, one graph;
+  * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
+    in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
 
 Checkpoint mode: `--checkpoint DIR [--layer-id I]` adds `checkpoint_layer`, the four
 projections of layer I of a local Qwen3 AutoAWQ checkpoint (read through its
@@ -351,8 +357,115 @@ def layer_stack(lib, dev, stream, reps: int) -> tuple[dict, dict]:
                          "regimes": sorted({"decode" if lib.regime(m, k, n) == 1 else "tile"
                                             for k, n in SHAPES.values()})}
     chained = layer_stack_chained(lib, dev, stream, reps, layers)
+    normed = layer_stack_normed(lib, dev, stream, reps, layers)
     del layers
-    return out, chained
+    return out, chained, normed
+
+
+def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
+    """36 layers with the reference's full dataflow around the projections (attention left
+    out as in stack36_chained): input_layernorm(h, residual) + QKV as one w4a16_gemm_rmsnorm
+    call, O plain, post_attention_layernorm(h, residual) + gate|up + SiLU * up as one
+    w4a16_gemm_rmsnorm call, down plain -- 144 GEMM and 72 RMSNorm launches per step, one
+    graph.  The residual add sits in the norm prologue here, the reference's order."""
+    out = {}
+    kq, nq = SHAPES["qkv"]
+    ki, ni = SHAPES["gate_up"]
+    for m in STACK_M:
+        h = torch.randn((m, kq), device=dev).to(torch.bfloat16)
+        res = torch.randn((m, kq), device=dev).to(torch.bfloat16)
+        xn = torch.empty((m, kq), dtype=torch.bfloat16, device=dev)
+        nw = (1 + 0.1 * torch.randn(kq, device=dev)).to(torch.bfloat16)
+        qkv = torch.empty((m, nq), dtype=torch.bfloat16, device=dev)
+        attn = torch.empty((m, kq), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((m, ni // 2), dtype=torch.bfloat16, device=dev)
+        ws_len = max(lib.workspace_bytes(m, k, n) for k, n in SHAPES.values())
+        ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
+        wsp = ws.data_ptr() if ws_len else None
+
+        def normed(w, y, k, n, silu, sp):
+            packed, qzeros, scales = w
+            if lib.dll.w4a16_gemm_rmsnorm(h.data_ptr(), res.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
+                                          res.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                          y.data_ptr(), m, k, n, 128, silu, wsp, ws_len, sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def plain(x, w, k, n, sp):
+            packed, qzeros, scales = w
+            if lib.dll.w4a16_gemm(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                  h.data_ptr(), m, k, n, 128, wsp, ws_len, sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def step():
+            sp = torch.cuda.current_stream(dev).cuda_stream
+            for layer in layers:
+                normed(layer["qkv"], qkv, kq, nq, 0, sp)
+                attn.copy_(qkv[:, :kq])
+                plain(attn, layer["o"], *SHAPES["o"], sp)
+                normed(layer["gate_up"], act, ki, ni, 1, sp)
+                plain(act, layer["down"], *SHAPES["down"], sp)
+
+        ms = time_graph(step, stream, reps)
+        out[f"M={m}"] = {"step_us": round(ms * 1e3, 1), "us_per_token": round(ms * 1e3 / m, 2)}
+    return out
+
+
+NORM_M = (1, 16, 2048)
+
+
+def norm_prologue(lib, dev, stream, reps: int) -> dict:
+    """The RMSNorm(+residual) prologue alone (w4a16_add_rmsnorm, hidden 4096), the QKV and
+    gate|up(+SiLU * up) GEMMs alone, and the two in one w4a16_gemm_rmsnorm call, each
+    graph-replayed over rotating weight copies; `prologue_us` = fused - GEMM alone."""
+    out = {}
+    for name, silu in (("qkv", 0), ("gate_up", 1)):
+        k, n = SHAPES[name]
+        copies = max(2, -(-2 * CACHE_BYTES // weight_bytes(k, n)))
+        weights = make_weights(k, n, copies, dev, 777)
+        for m in NORM_M:
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            res = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            res_out = torch.empty_like(res)
+            xn = torch.empty_like(x)
+            nw = (1 + 0.1 * torch.randn(k, device=dev)).to(torch.bfloat16)
+            y = torch.empty((m, n // 2 if silu else n), dtype=torch.bfloat16, device=dev)
+            ws_len = lib.workspace_bytes(m, k, n)
+            ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
+            wsp = ws.data_ptr() if ws_len else None
+            gemm = lib.dll.w4a16_gemm_silu_mul if silu else lib.dll.w4a16_gemm
+
+            def check(rc):
+                if rc != 0:
+                    raise RuntimeError(lib.last_error())
+
+            def fused_step():
+                sp = torch.cuda.current_stream(dev).cuda_stream
+                for packed, qzeros, scales in weights:
+                    check(lib.dll.w4a16_gemm_rmsnorm(x.data_ptr(), res.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
+                                                     res_out.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                     scales.data_ptr(), y.data_ptr(), m, k, n, 128, silu, wsp,
+                                                     ws_len, sp))
+
+            def gemm_step():
+                sp = torch.cuda.current_stream(dev).cuda_stream
+                for packed, qzeros, scales in weights:
+                    check(gemm(xn.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(),
+                               m, k, n, 128, wsp, ws_len, sp))
+
+            def norm_step():
+                sp = torch.cuda.current_stream(dev).cuda_stream
+                for _ in weights:
+                    check(lib.dll.w4a16_add_rmsnorm(x.data_ptr(), res.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
+                                                    res_out.data_ptr(), m, k, sp))
+
+            f_ms = time_graph(fused_step, stream, reps) / copies
+            g_ms = time_graph(gemm_step, stream, reps) / copies
+            n_ms = time_graph(norm_step, stream, reps) / copies
+            out[f"{name} M={m}"] = {"fused_us": round(f_ms * 1e3, 2), "gemm_us": round(g_ms * 1e3, 2),
+                                    "norm_us": round(n_ms * 1e3, 2), "prologue_us": round((f_ms - g_ms) * 1e3, 2),
+                                    "norm_GB/s": round(4 * m * k * 2 / (n_ms * 1e-3) / 1e9, 1)}
+        del weights
+    return out
 
 
 def layer_stack_chained(lib, dev, stream, reps: int, layers) -> dict:
@@ -686,13 +799,14 @@ def main(argv=None):
                 print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
         del pts
 
-    mixed = stack = stack_chained = ceilings = fused = quant = None
+    mixed = stack = stack_chained = stack_normed = ceilings = fused = quant = norm = None
     if not args.no_extra:
         mixed = mixed_batch(lib, dev, stream, max(3, args.steps // 4))
-        stack, stack_chained = layer_stack(lib, dev, stream, max(2, args.steps // 10))
+        stack, stack_chained, stack_normed = layer_stack(lib, dev, stream, max(2, args.steps // 10))
         ceilings = measured_ceilings(dev, stream)
         fused = fused_gate_up(lib, dev, stream, max(3, args.steps // 4))
         quant = quantize_throughput(lib, dev, stream, max(3, args.steps // 4))
+        norm = norm_prologue(lib, dev, stream, max(3, args.steps // 4))
         if args.details:
             print(f"mixed M={MIXED_M}: {json.dumps(mixed)}", file=sys.stderr)
             print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
@@ -700,6 +814,8 @@ def main(argv=None):
             print(f"ceilings: {json.dumps(ceilings)}", file=sys.stderr)
             print(f"fused gate_up: {json.dumps(fused)}", file=sys.stderr)
             print(f"quantize: {json.dumps(quant)}", file=sys.stderr)
+            print(f"stack36_normed: {json.dumps(stack_normed)}", file=sys.stderr)
+            print(f"rmsnorm_prologue: {json.dumps(norm)}", file=sys.stderr)
 
     ckpt_layer = None
     if args.checkpoint:
@@ -734,9 +850,11 @@ def main(argv=None):
         "mixed_m512": mixed,
         "stack36": stack,
         "stack36_chained": stack_chained,
+        "stack36_normed": stack_normed,
         "measured_ceilings": ceilings,
         "fused_gate_up": fused,
         "quantize": quant,
+        "rmsnorm_prologue": norm,
         "checkpoint_layer": ckpt_layer,
         "points": points_out,
     }

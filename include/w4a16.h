@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 2
+#define W4A16_ABI_VERSION 3
 
 enum w4a16_status {
   W4A16_OK = 0,
@@ -144,6 +144,34 @@ int w4a16_gemm_residual(const uint16_t* x, const int32_t* packed, const int32_t*
 int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
                         const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* RMSNorm of each row of x [M, K], with the residual add in front when residual is not NULL:
+ *   s = float(x) + float(residual)  (s = float(x) without a residual), in fp32;
+ *   residual_out = bf16(s);
+ *   x_norm = bf16(float(bf16(s * rsqrt(mean(s * s) + eps))) * float(weight)).
+ * weight is bf16 [K].  residual and residual_out are both given or both NULL; residual_out
+ * may be residual or x (in place), x_norm may be x, x_norm != residual_out.  K % 8 == 0,
+ * K <= 16384, every pointer 16-byte aligned, 0 <= eps <= 1.  rsqrt is correctly rounded
+ * and the sum of squares is an fp32 tree sum, so bf16(s * r) can differ from another fp32
+ * implementation by one bf16 ulp where s * r lies next to a rounding boundary (up to two
+ * ulps of x_norm after the weight product).
+ * Replaces RMSNorm.rms_forward / add_rms_forward (layernorm.py:16-40). */
+int w4a16_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
+                      uint16_t* x_norm, uint16_t* residual_out, int M, int K, void* stream);
+
+/* The RMSNorm(+residual) prologue of w4a16_add_rmsnorm followed, on the same stream and in
+ * the same call, by w4a16_gemm (silu_mul == 0) or w4a16_gemm_silu_mul (silu_mul == 1) of
+ * x_norm: y = x_norm @ W, or SiLU(g) * u of it.  x_norm [M, K] is a caller buffer the
+ * GEMM reads back while it is still in L2 at decode sizes.  Arguments as for those two
+ * calls; the workspace is w4a16_workspace_bytes(M, K, N, 128).  Argument, shape and
+ * workspace errors are reported before anything is enqueued.
+ * Replaces input_layernorm / post_attention_layernorm followed by qkv_proj / gate_up_proj
+ * (qwen3.py:166-173 with layernorm.py:28-40, qwen3.py:126-130). */
+int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* norm_weight, float eps,
+                       uint16_t* x_norm, uint16_t* residual_out, const int32_t* packed,
+                       const int32_t* qzeros, const uint16_t* scales, uint16_t* y, int M, int K, int N,
+                       int group_size, int silu_mul, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* Kernel family w4a16_gemm launches for (M, K, N): a w4a16_regime_id.
  * Replaces the dispatch rule of select_awq_cuda_split_k (awq_cuda.py:17-26) and

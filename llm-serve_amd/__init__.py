@@ -9,8 +9,10 @@ from ._lib import REGIME_DECODE, REGIME_NONE, REGIME_TILE, W4A16Error, W4A16Libr
 from .layers.quantization.awq import (
     AWQLinearMethod,
     AWQRuntimeConfig,
+    add_rms_norm,
     awq_linear,
     awq_linear_residual,
+    awq_linear_rmsnorm,
     awq_linear_silu_mul,
     awq_regime,
     dequantize_awq_gemm,
@@ -26,8 +28,10 @@ __all__ = (
     "REGIME_TILE",
     "W4A16Error",
     "W4A16Library",
+    "add_rms_norm",
     "awq_linear",
     "awq_linear_residual",
+    "awq_linear_rmsnorm",
     "awq_linear_silu_mul",
     "awq_regime",
     "dequantize_awq_gemm",

@@ -47,8 +47,15 @@ _SIGNATURES = {
     "w4a16_gemm_silu_mul_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
                                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size,
                                             _c_ptr]),
+    "w4a16_add_rmsnorm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_gemm_rmsnorm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                    _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
+
+
+def _ptr(t: torch.Tensor | None):
+    return t.data_ptr() if t is not None else None
 
 
 class W4A16Error(RuntimeError):
@@ -205,6 +212,31 @@ class W4A16Library:
                                                     scales.data_ptr(), y.data_ptr(), m, k, n, group_size, ws_ptr,
                                                     ws_len, self._stream(x)),
                        "w4a16_gemm_silu_mul")
+        return y
+
+    def add_rmsnorm(self, x, residual, weight, eps: float, x_norm, residual_out) -> torch.Tensor:
+        """x_norm = RMSNorm(x + residual) * weight, residual_out = bf16(x + residual) (no add
+        and no residual_out when residual is None); [M, K] bf16, contiguous, one GPU."""
+        m, k = x.shape
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_add_rmsnorm(x.data_ptr(), _ptr(residual), weight.data_ptr(), float(eps),
+                                                  x_norm.data_ptr(), _ptr(residual_out), m, k, self._stream(x)),
+                       "w4a16_add_rmsnorm")
+        return x_norm
+
+    def gemm_rmsnorm(self, x, residual, weight, eps: float, x_norm, residual_out, packed, qzeros, scales, y,
+                     n: int, workspace: torch.Tensor | None, group_size: int = 128,
+                     silu_mul: bool = False) -> torch.Tensor:
+        """The RMSNorm(+residual) prologue into x_norm, then y = x_norm @ W (or SiLU(g) * u)."""
+        m, k = x.shape
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_gemm_rmsnorm(x.data_ptr(), _ptr(residual), weight.data_ptr(), float(eps),
+                                                   x_norm.data_ptr(), _ptr(residual_out), packed.data_ptr(),
+                                                   qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(), m, k, n,
+                                                   group_size, int(silu_mul), ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm_rmsnorm")
         return y
 
     def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,

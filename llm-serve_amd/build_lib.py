@@ -15,7 +15,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libw4a16.so"
 LIB_PATH = os.path.join(CSRC, LIB_NAME)
-SOURCES = ("w4a16_format.hip", "w4a16_quant.hip", "w4a16_decode.hip", "w4a16_tile.hip", "w4a16_api.hip")
+SOURCES = ("w4a16_format.hip", "w4a16_quant.hip", "w4a16_decode.hip", "w4a16_tile.hip", "w4a16_norm.hip",
+           "w4a16_api.hip")
 ARCH = "gfx950"
 
 COMPILE_FLAGS = [

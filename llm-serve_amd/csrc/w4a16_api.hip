@@ -256,9 +256,62 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   return ok();
 }
 
+// Arguments of the residual-add + RMSNorm prologue (w4a16_add_rmsnorm, w4a16_gemm_rmsnorm).
+int validate_norm(const void* x, const void* residual, const void* weight, float eps, const void* x_norm,
+                  const void* residual_out, int M, int K) {
+  if (M < 0 || K <= 0) return fail(W4A16_ERR_ARG, "M must be >= 0 and K positive (got M=%d K=%d)", M, K);
+  if (K % 8 || K > w4a16::kNormMaxK)
+    return fail(W4A16_ERR_SHAPE, "the RMSNorm width K must be a multiple of 8 and at most %d (got %d)",
+                w4a16::kNormMaxK, K);
+  if (!(eps >= 0.0f) || eps > 1.0f) return fail(W4A16_ERR_ARG, "eps must be in [0, 1] (got %g)", eps);
+  if (!x || !weight || !x_norm) return fail(W4A16_ERR_ARG, "null tensor pointer");
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return fail(W4A16_ERR_ARG, "residual and residual_out must both be given or both be null");
+  if (residual_out && residual_out == x_norm)
+    return fail(W4A16_ERR_ARG, "x_norm and residual_out must be different buffers");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(x_norm, 16) || !aligned(residual, 16) ||
+      !aligned(residual_out, 16))
+    return fail(W4A16_ERR_ALIGN, "x, residual, weight, x_norm and residual_out must be 16-byte aligned");
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
+
+int w4a16_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
+                      uint16_t* x_norm, uint16_t* residual_out, int M, int K, void* stream) {
+  const int v = validate_norm(x, residual, weight, eps, x_norm, residual_out, M, K);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  return check_launch(w4a16::launch_add_rmsnorm(x, residual, weight, x_norm, residual_out, M, K, eps,
+                                                static_cast<hipStream_t>(stream)),
+                      "add_rmsnorm");
+}
+
+int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* norm_weight, float eps,
+                       uint16_t* x_norm, uint16_t* residual_out, const int32_t* packed, const int32_t* qzeros,
+                       const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size, int silu_mul,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int v = validate_norm(x, residual, norm_weight, eps, x_norm, residual_out, M, K);
+  if (v != W4A16_OK) return v;
+  if (silu_mul != 0 && silu_mul != 1) return fail(W4A16_ERR_ARG, "silu_mul must be 0 or 1 (got %d)", silu_mul);
+  v = validate_gemm(x_norm, packed, qzeros, scales, y, M, K, N, group_size, silu_mul != 0);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  // Every check that could fail the GEMM runs before the prologue is enqueued.
+  const GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
+  const size_t need = workspace_for(p, M, N);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(W4A16_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if (need > 0 && !aligned(workspace, 256)) return fail(W4A16_ERR_ALIGN, "workspace must be 256-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  v = check_launch(w4a16::launch_add_rmsnorm(x, residual, norm_weight, x_norm, residual_out, M, K, eps, s),
+                   "add_rmsnorm");
+  if (v != W4A16_OK) return v;
+  return run_plan(p, x_norm, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s,
+                  silu_mul ? N / 32 : 0);
+}
 
 int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }
 

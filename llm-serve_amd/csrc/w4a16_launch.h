@@ -80,4 +80,12 @@ hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint
                            int M, int K, int N, int wm, int shape, int occ, int split, int up_tiles,
                            hipStream_t stream);
 
+// RMSNorm of each row of x [M, K] (after adding residual [M, K] when it is not null, which
+// then also writes residual_out = bf16(x + residual)); K % 8 == 0, K <= kNormMaxK, every
+// pointer 16-byte aligned; residual_out may be residual or x, x_norm may be x.
+constexpr int kNormMaxK = 16384;
+hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                              uint16_t* x_norm, uint16_t* residual_out, int M, int K, float eps,
+                              hipStream_t stream);
+
 }  // namespace w4a16

@@ -111,6 +111,17 @@ class ColumnParallelLinear(LinearBase):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.apply_linear(x)
 
+    def forward_rmsnorm(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None):
+        """``self(norm(x, residual))`` for an RMSNorm ``norm`` (its ``weight`` and ``eps``) in
+        front of this projection -- input_layernorm then qkv_proj (qwen3.py:166-169) -- as
+        one library call; returns ``(y, new residual)``, the residual None when none is given."""
+        return self._rmsnorm_apply(norm, x, residual, silu_mul=False)
+
+    def _rmsnorm_apply(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None, silu_mul: bool):
+        if self.quant_method is None or not hasattr(self.quant_method, "apply_rmsnorm"):
+            raise ValueError("the fused RMSNorm prologue is implemented for the AWQ HIP backend only")
+        return self.quant_method.apply_rmsnorm(self, x, residual, norm.weight, norm.eps, silu_mul=silu_mul)
+
 
 class MergedColumnParallelLinear(ColumnParallelLinear):
 
@@ -140,6 +151,14 @@ class MergedColumnParallelLinear(ColumnParallelLinear):
         if self.quant_method is None or not hasattr(self.quant_method, "apply_silu_and_mul"):
             raise ValueError("fused SiLU * up is implemented for the AWQ HIP backend only")
         return self.quant_method.apply_silu_and_mul(self, x)
+
+    def forward_rmsnorm_silu_and_mul(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None):
+        """``SiluAndMul()(self(norm(x, residual)))`` -- post_attention_layernorm then the MLP's
+        gate_up and activation (qwen3.py:172-173, 126-130) -- as one library call; returns
+        ``(y, new residual)`` (the residual is None when none is given)."""
+        if len(self.output_sizes) != 2 or self.output_sizes[0] != self.output_sizes[1]:
+            raise ValueError("fused SiLU * up needs exactly two equal output shards (gate, up)")
+        return self._rmsnorm_apply(norm, x, residual, silu_mul=True)
 
 
 class QKVParallelLinear(ColumnParallelLinear):

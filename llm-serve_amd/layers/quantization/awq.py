@@ -16,6 +16,9 @@ Same names, argument meaning and error behaviour as the reference:
 * ``awq_linear_silu_mul`` / ``AWQLinearMethod.apply_silu_and_mul``: the gate|up GEMM with
   the reference's ``SiluAndMul`` (activation.py:8-11, applied at qwen3.py:126-130) fused
   into its epilogue; no reference counterpart as one call
+* ``add_rms_norm``: the reference's ``RMSNorm`` forward (layernorm.py:16-50) on the HIP
+  kernel; ``awq_linear_rmsnorm`` / ``AWQLinearMethod.apply_rmsnorm``: that norm in front of
+  the QKV or gate_up GEMM in one library call (qwen3.py:166-173)
 
 There is one execution backend, the HIP library (libw4a16.so): every tensor operation
 runs there and raises when the library or a GPU is missing -- nothing falls back to a CPU
@@ -182,6 +185,15 @@ class AWQLinearMethod:
             raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
         return awq_linear_silu_mul(inputs, layer.awq_qweight, layer.awq_qzeros, layer.scales,
                                    group_size=self.config.group_size)
+
+    def apply_rmsnorm(self, layer: nn.Module, inputs: torch.Tensor, residual: torch.Tensor | None,
+                      norm_weight: torch.Tensor, eps: float, silu_mul: bool = False):
+        """``self.apply(layer, RMSNorm(inputs, residual))`` (or its SiLU(g) * u) with the
+        norm in the same library call; returns ``(y, residual_out)`` (qwen3.py:166-173)."""
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear_rmsnorm(inputs, residual, norm_weight, eps, layer.awq_qweight, layer.awq_qzeros,
+                                  layer.scales, group_size=self.config.group_size, silu_mul=silu_mul)
 
     def apply(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
         if not hasattr(layer, "awq_qweight"):
@@ -369,6 +381,81 @@ def awq_linear_silu_mul(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzer
         workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
     library.gemm_silu_mul(x, packed_qweight, qzeros, scales.contiguous(), y, k, n, workspace, group_size)
     return y.reshape(*lead, n // 2)
+
+
+def _norm_operands(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor):
+    """Validated [M, K] views of the RMSNorm operands (bf16, contiguous, 16-byte aligned)."""
+    if x.device.type != "cuda":
+        raise ValueError("RMSNorm input must be on a GPU (HIP) device")
+    k = x.shape[-1]
+    tensors = [("input", x), ("weight", weight)] + ([("residual", residual)] if residual is not None else [])
+    for name, t in tensors:
+        if t.dtype != torch.bfloat16 or t.device != x.device:
+            raise ValueError(f"RMSNorm {name} must be a bfloat16 tensor on the input's GPU")
+        if not t.is_contiguous() or not _aligned16(t):
+            raise ValueError(f"RMSNorm {name} must be contiguous and 16-byte aligned")
+    if weight.shape != (k,):
+        raise ValueError(f"RMSNorm weight must have shape ({k},), got {tuple(weight.shape)}")
+    if residual is not None and residual.shape != x.shape:
+        raise ValueError("RMSNorm residual must have the input's shape")
+    if k % 8 or k > 16384:
+        raise ValueError(f"RMSNorm width must be a multiple of 8 and at most 16384 (got {k})")
+    m = x.numel() // k if k else 0
+    return x.reshape(m, k), (residual.reshape(m, k) if residual is not None else None), m, k
+
+
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                 *, residual_out: torch.Tensor | None = None):
+    """The reference's RMSNorm forward (layernorm.py:16-50) on the HIP kernel: without a
+    residual, ``bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)``; with one, the same of
+    ``s = x + residual`` (fp32) and also the new residual ``bf16(s)``, returned as
+    ``(x_norm, residual_out)``.  ``residual_out`` may be ``residual`` (in place)."""
+    xv, rv, m, k = _norm_operands(x, residual, weight)
+    x_norm = torch.empty_like(x)
+    if residual is not None and residual_out is None:
+        residual_out = torch.empty_like(x)
+    if residual_out is not None and (residual_out.shape != x.shape or residual_out.dtype != torch.bfloat16
+                                     or not residual_out.is_contiguous() or not _aligned16(residual_out)):
+        raise ValueError("RMSNorm residual_out must be a contiguous, 16-byte aligned bf16 tensor of the input shape")
+    if m > 0:
+        lib().add_rmsnorm(xv, rv, weight, eps, x_norm.view(m, k),
+                          residual_out.view(m, k) if residual_out is not None else None)
+    return x_norm if residual is None else (x_norm, residual_out)
+
+
+def awq_linear_rmsnorm(inputs: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor, eps: float,
+                       packed_qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, *,
+                       group_size: int, silu_mul: bool = False, residual_out: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None = None):
+    """The RMSNorm(+residual) in front of QKV or gate_up and the projection in one library
+    call (qwen3.py:166-173 and 126-130 with layernorm.py:28-40): returns ``(y, residual_out)``
+    with ``y = awq_linear(add_rms_norm(...))`` -- or, with ``silu_mul``, its SiLU(g) * u --
+    and ``residual_out = bf16(inputs + residual)`` (None without a residual; may be
+    ``residual`` itself).  The normalised activations go through a scratch tensor of the
+    input's shape that the GEMM reads back from L2 at decode sizes."""
+    xv, rv, m, k = _norm_operands(inputs, residual, norm_weight)
+    lead = inputs.shape[:-1]
+    _, _, k2, n = _prepare_linear(xv, packed_qweight, qzeros, scales, group_size)
+    if k2 != k:
+        raise ValueError("RMSNorm width and the layer's input size differ")
+    if silu_mul and n % 128:
+        raise ValueError("AWQ fused SiLU * up requires the gate|up output size to be divisible by 128")
+    if residual is not None and residual_out is None:
+        residual_out = torch.empty_like(inputs)
+    if residual_out is not None and (residual_out.shape != inputs.shape or residual_out.dtype != torch.bfloat16
+                                     or not residual_out.is_contiguous() or not _aligned16(residual_out)):
+        raise ValueError("RMSNorm residual_out must be a contiguous, 16-byte aligned bf16 tensor of the input shape")
+    n_out = n // 2 if silu_mul else n
+    y = torch.empty((m, n_out), dtype=torch.bfloat16, device=inputs.device)
+    if m > 0:
+        library = lib()
+        if workspace is None:
+            workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
+        x_norm = torch.empty((m, k), dtype=torch.bfloat16, device=inputs.device)
+        library.gemm_rmsnorm(xv, rv, norm_weight, eps, x_norm,
+                             residual_out.view(m, k) if residual_out is not None else None, packed_qweight,
+                             qzeros, scales.contiguous(), y, n, workspace, group_size, silu_mul)
+    return y.reshape(*lead, n_out), residual_out
 
 
 def awq_regime(m: int, k: int, n: int) -> str:

@@ -29,6 +29,11 @@ What it restates (reference = HGinkgo/LLM-Serve):
     reference's layer returns it (or, optionally, unrounded), then ``silu_and_mul_ref``.
 * ``quantize_awq_weight``                     llmserve/quantization/awq_calibration.py:35-62
     the producer side of the format, used for known-answer tests and synthetic data.
+* ``add_rms_norm_ref``                        llmserve/layers/layernorm.py:16-40
+    rms_forward / add_rms_forward: s = float(x) (+ float(residual)) in fp32, the new
+    residual bf16(s), then bf16(float(bf16(s * rsqrt(mean(s^2) + eps))) * weight) with
+    the mean in fp64 rounded to fp32, + eps in fp32 (the reference's order), the rsqrt in
+    fp64, and the product s * r rounded to fp32 first, as the reference stores it.
 
 Parity pinning (every function above is checked by tests/test_oracle.py against the
 reference's own known-answer tests, hand-derived constants, torch's bf16 arithmetic
@@ -251,6 +256,31 @@ def quantize_awq_weight(weight, group_size: int = 128, out_dtype: str = "bf16"):
 
 
 # ------------------------------------------------------------- synthetic data
+def add_rms_norm_ref(x_bits, residual_bits, weight_bits, eps: float):
+    """(x_norm bits, residual_out bits or None, s * r in fp64) for rows of bf16 x [M, K].
+
+    layernorm.py:28-40 (add_rms_forward) when ``residual_bits`` is given, layernorm.py:17-26
+    (rms_forward) when it is None.  ``s`` = fp32 sum of the two bf16 inputs (numpy's fp32 add
+    rounds to nearest even as the GPU does); the row mean of s^2 is taken in fp64 and
+    rounded to fp32, eps is added in fp32 (``var + self.eps``), the reciprocal square root is
+    taken in fp64; s * r is rounded to fp32 (the reference's in-place fp32 product)
+    and then to bf16 (``x.to(orig_dtype)``); the product with the bf16 weight is exact in
+    fp32 (two 8-bit significands), so it is rounded once, to bf16."""
+    s = bf16_bits_to_f32(np.asarray(x_bits, dtype=np.uint16))
+    res_out = None
+    if residual_bits is not None:
+        s = (s + bf16_bits_to_f32(np.asarray(residual_bits, dtype=np.uint16))).astype(np.float32)
+        res_out = f32_to_bf16_bits(s)
+    s64 = s.astype(np.float64)
+    var = np.mean(s64 * s64, axis=-1, keepdims=True)
+    var_eps = (var.astype(np.float32) + np.float32(eps)).astype(np.float64)
+    normed = s64 / np.sqrt(var_eps)
+    t = bf16_bits_to_f32(f32_to_bf16_bits(normed.astype(np.float32)))
+    w = bf16_bits_to_f32(np.asarray(weight_bits, dtype=np.uint16))
+    out = f32_to_bf16_bits((t.astype(np.float64) * w.astype(np.float64)).astype(np.float32))
+    return out, res_out, normed
+
+
 def make_problem(seed: int, m: int, k: int, n: int, group_size: int = 128,
                  scale_lo: float = 0.002, scale_hi: float = 0.02,
                  outlier_frac: float = 0.0, outlier_gain: float = 20.0) -> dict:

@@ -38,7 +38,7 @@ def test_binding_signatures_cover_the_header(pkg):
 
 def test_abi_version_and_empty_error(pkg):
     L = pkg.lib()
-    assert L.dll.w4a16_abi_version() == 2
+    assert L.dll.w4a16_abi_version() == 3
     assert isinstance(L.last_error(), str)
 
 
@@ -200,3 +200,32 @@ def test_residual_entry_point_validates_without_launching(pkg):
     assert f(p, p, p, p, p + 2, p, 16, 4096, 4096, 128, None, 0, None) == 3
     assert f(p, p, p, p, p, p, 16, 4096, 4100, 128, None, 0, None) == 2
     assert f(None, None, None, None, None, None, 0, 4096, 4096, 128, None, 0, None) == 0
+
+
+def test_rmsnorm_entry_points_validate_without_launching(pkg):
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    q = p + 32  # a second, distinct aligned address
+    norm = L.dll.w4a16_add_rmsnorm
+    # (x, residual, weight, eps, x_norm, residual_out, M, K, stream)
+    assert norm(p, None, p, 1e-6, p, None, 0, 4096, None) == 0  # M == 0: nothing enqueued
+    assert norm(p, None, p, 1e-6, p, None, 4, 4100, None) == 2 and "multiple of 8" in L.last_error()
+    assert norm(p, None, p, 1e-6, p, None, 4, 16392, None) == 2
+    assert norm(p, p, p, 1e-6, p, None, 4, 4096, None) == 1 and "both" in L.last_error()
+    assert norm(p, p, p, 1e-6, q, q, 4, 4096, None) == 1 and "different" in L.last_error()
+    assert norm(p, None, p, -1.0, p, None, 4, 4096, None) == 1 and "eps" in L.last_error()
+    assert norm(p, None, p, float("nan"), p, None, 4, 4096, None) == 1
+    assert norm(p + 2, None, p, 1e-6, p, None, 4, 4096, None) == 3
+    assert norm(None, None, p, 1e-6, p, None, 4, 4096, None) == 1
+    fused = L.dll.w4a16_gemm_rmsnorm
+    # (x, residual, weight, eps, x_norm, residual_out, packed, qzeros, scales, y, M, K, N, group,
+    #  silu_mul, workspace, workspace_bytes, stream)
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 0, 4096, 4096, 128, 0, None, 0, None) == 0
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4096, 128, 2, None, 0, None) == 1
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4160, 128, 1, None, 0, None) == 2
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4096, 64, 0, None, 0, None) == 2
+    # a planned K split needs the workspace: reported before the norm is enqueued
+    m, k, n = 32, 4096, 4096
+    assert L.split_k(m, k, n) > 1
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0, None, 0, None) == 4

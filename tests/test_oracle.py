@@ -377,3 +377,74 @@ def test_quantizer_matches_torch_cpu_arithmetic():
             np.testing.assert_array_equal(sc, want_s.view(torch.int16).numpy().view(np.uint16))
         else:
             np.testing.assert_array_equal(sc, want_s.numpy())
+
+
+# --------------------------------------------------------------------- RMSNorm(+residual)
+def _bits(a):
+    return ora.f32_to_bf16_bits(np.asarray(a, dtype=np.float32))
+
+
+def test_rms_norm_closed_forms():
+    """Rows whose root mean square is known: [3, 4, 0, 0] has rms 2.5, a constant row c has
+    rms |c|, and eps dominates a row of 1e-4 (1e-4 / sqrt(1e-8 + 1e-6))."""
+    x = _bits([[3, 4, 0, 0], [2, 2, 2, 2], [-0.5, -0.5, -0.5, -0.5], [1e-4, 1e-4, 1e-4, 1e-4]])
+    ones, twos = _bits(np.ones(4)), _bits(np.full(4, 2.0))
+    out, res, normed = ora.add_rms_norm_ref(x, None, ones, 1e-6)
+    assert res is None
+    x32 = ora.bf16_bits_to_f32(x).astype(np.float64)
+    assert np.allclose(normed[0], [1.2, 1.6, 0, 0], rtol=1e-6)
+    assert np.array_equal(out[1], _bits(np.ones(4))) and np.array_equal(out[2], _bits(-np.ones(4)))
+    assert np.allclose(normed[3], x32[3, 0] / np.sqrt(x32[3, 0] ** 2 + 1e-6), rtol=1e-6)
+    assert abs(normed[3, 0] - 0.0995) < 1e-3
+    assert np.array_equal(out[0], _bits([1.2, 1.6, 0, 0]))
+    # weight 2 is exact: every output doubles, bit for bit
+    out2, _, _ = ora.add_rms_norm_ref(x, None, twos, 1e-6)
+    assert np.array_equal(ora.bf16_bits_to_f32(out2), 2 * ora.bf16_bits_to_f32(out))
+
+
+def test_rms_norm_matches_torch_rms_norm_fp64():
+    """The normalised rows (before rounding) against torch.nn.functional.rms_norm in fp64,
+    and the new residual against torch's own bf16 addition."""
+    rng = np.random.default_rng(5)
+    x = _bits(rng.standard_normal((6, 4096)) * 3)
+    r = _bits(rng.standard_normal((6, 4096)) * 5)
+    w = _bits(1 + 0.1 * rng.standard_normal(4096))
+    eps = 1e-6
+    out, res, normed = ora.add_rms_norm_ref(x, r, w, eps)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    rt = torch.from_numpy(r.view(np.int16)).view(torch.bfloat16)
+    assert np.array_equal(res, (xt + rt).view(torch.int16).numpy().view(np.uint16))
+    s = xt.double() + rt.double()
+    want = torch.nn.functional.rms_norm(s, (4096,), eps=eps).numpy()
+    assert np.allclose(normed, want, rtol=2e-7, atol=0)
+
+
+def _torch_fp32_steps(x_bits, r_bits, w_bits, eps, round_before_weight=True):
+    """The reference's steps (layernorm.py:35-40) run by torch on the CPU in fp32."""
+    xt = torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16)
+    rt = torch.from_numpy(r_bits.view(np.int16)).view(torch.bfloat16)
+    wt = torch.from_numpy(w_bits.view(np.int16)).view(torch.bfloat16)
+    s = xt.float().add_(rt.float())
+    var = s.pow(2).mean(dim=-1, keepdim=True)
+    s.mul_(torch.rsqrt(var + eps))
+    t = s.to(torch.bfloat16) if round_before_weight else s
+    return (t * wt).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_rms_norm_agrees_with_torch_fp32_within_one_ulp():
+    """torch's fp32 reduction and rsqrt are one rounding away from the oracle's fp64: the
+    bf16 outputs agree exactly almost everywhere and within one bf16 ulp everywhere.  The
+    same comparison fails when the oracle's intermediate bf16 rounding is taken out (a
+    planted mistake), so the check sees where the roundings sit."""
+    rng = np.random.default_rng(6)
+    x = _bits(rng.standard_normal((8, 4096)))
+    r = _bits(rng.standard_normal((8, 4096)) * 2)
+    w = _bits(1 + 0.3 * rng.standard_normal(4096))
+    out, _, normed = ora.add_rms_norm_ref(x, r, w, 1e-6)
+    got = _torch_fp32_steps(x, r, w, 1e-6)
+    ulp = np.abs(out.view(np.int16).astype(np.int32) - got.view(np.int16).astype(np.int32))
+    assert ulp.max() <= 1 and (ulp == 0).mean() > 0.995
+    # planted mistake: no bf16 rounding of s * r before the weight multiply
+    wf = ora.bf16_bits_to_f32(w).astype(np.float64)
+    wrong = ora.f32_to_bf16_bits((normed.astype(np.float32).astype(np.float64) * wf).astype(np.float32))
+    assert (wrong != got).mean() > 0.05
