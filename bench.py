@@ -676,7 +676,8 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
     """Counter/trace workload: one 256 MiB bf16 copy (3x) for calibration, WARM_MS of
     untimed launches, then `steps` direct launches of one decode or prefill point over
     rotating weights.  SHAPE+silu:M
-    launches the fused SiLU * up GEMM of that (gate|up) shape; quantize:0 launches the
+    launches the fused SiLU * up GEMM of that (gate|up) shape, a trailing +norm the
+    RMSNorm(+residual) prologue with it (w4a16_gemm_rmsnorm); quantize:0 launches the
     quantizer over a [24576, 4096] bf16 weight."""
     name, m = spec.split(":")
     m = int(m)
@@ -684,10 +685,21 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
         q = quantize_throughput(lib, dev, torch.cuda.Stream(dev), steps)
         print(json.dumps({"profile_point": spec, "launches": steps + 2, **q}))
         return 0
+    normed = name.endswith("+norm")
+    name = name.removesuffix("+norm")
     fused = name.endswith("+silu")
     name = name.removesuffix("+silu")
     entry = lib.dll.w4a16_gemm_silu_mul if fused else lib.dll.w4a16_gemm
     k, n = SHAPES[name]
+    if normed:  # the RMSNorm(+residual) prologue and the GEMM in one w4a16_gemm_rmsnorm call
+        res = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        res_out, xn = torch.empty_like(res), torch.empty_like(res)
+        nw = (1 + 0.1 * torch.randn(k, device=dev)).to(torch.bfloat16)
+
+        def entry(xp, pp, zp, sp_, yp, m_, k_, n_, g, wsp, wsl, stp):
+            return lib.dll.w4a16_gemm_rmsnorm(xp, res.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
+                                              res_out.data_ptr(), pp, zp, sp_, yp, m_, k_, n_, g, int(fused), wsp,
+                                              wsl, stp)
     src = torch.ones(CALIBRATION_BYTES // 2, dtype=torch.bfloat16, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):

@@ -151,7 +151,7 @@ int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t*
  *   x_norm = bf16(float(bf16(s * rsqrt(mean(s * s) + eps))) * float(weight)).
  * weight is bf16 [K].  residual and residual_out are both given or both NULL; residual_out
  * may be residual or x (in place), x_norm may be x, x_norm != residual_out.  K % 8 == 0,
- * K <= 16384, every pointer 16-byte aligned, 0 <= eps <= 1.  rsqrt is correctly rounded
+ * K <= 16384, every pointer 16-byte aligned, 0 <= eps <= 1.  rsqrt is evaluated in fp64
  * and the sum of squares is an fp32 tree sum, so bf16(s * r) can differ from another fp32
  * implementation by one bf16 ulp where s * r lies next to a rounding boundary (up to two
  * ulps of x_norm after the weight product).

@@ -64,6 +64,48 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
   return static_cast<uint16_t>(pack_bf16x2(v, 0.0f) & 0xFFFFu);
 }
 
+// Eight bf16 values (one 16-byte chunk) to fp32 and back (round to nearest even).
+__device__ __forceinline__ void unpack_bf16x8(uint4 v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float (&f)[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
+}
+
+// Sum over the 64 lanes of a wave (every lane gets the same total).
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// 1 / sqrt(v) for the RMSNorm row scale, evaluated in fp64 and rounded once to fp32 (within
+// half an fp32 ulp but for fp64's own rounding); once per row, so fp64 costs nothing.
+__device__ __forceinline__ float rsqrt_rn(float v) {
+  return static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(v)));
+}
+
+// RMSNorm scaling of one chunk of s (fp32, the residual sum): bf16(float(bf16(s * rstd)) *
+// weight), the reference's x.to(orig_dtype).mul_(self.weight); the weight product is exact
+// in fp32 (two 8-bit significands) and rounded once.
+__device__ __forceinline__ uint4 rms_scale_bf16x8(const float (&s)[8], float rstd, uint4 weight) {
+  float t[8], w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] = s[i] * rstd;
+  unpack_bf16x8(pack_bf16x8(t), t);
+  unpack_bf16x8(weight, w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] *= w[i];
+  return pack_bf16x8(t);
+}
+
 // Residual epilogue: eight bf16 GEMM outputs plus eight bf16 residuals, added in fp32 and
 // rounded once more -- the reference's order (the layer's bf16 output, then
 // x.float() + residual.float() rounded back to bf16).
