@@ -3,6 +3,7 @@
 Mirrors the reference's own CPU tests: tests/test_awq_reference.py:19-99 (config),
 tests/test_awq_linear_backend.py:48-123, 209-236 (parameters, packed loaders, TP and shard
 contracts) and the error contract of awq.py:203-232, 259-268."""
+import importlib
 from dataclasses import replace
 from types import SimpleNamespace
 from unittest.mock import patch
@@ -226,3 +227,22 @@ def test_quantizer_and_packer_have_no_cpu_path(cal):
         cal.pack_int4(torch.zeros((2, 6), dtype=torch.int32))
     with pytest.raises(TypeError, match="integer"):
         cal.pack_int4(torch.zeros((2, 8)))
+
+
+def test_rmsnorm_module_mirrors_the_reference_interface_and_has_no_cpu_path():
+    """RMSNorm(hidden_size, eps) with a bf16 weight of ones (layernorm.py:8-15); the compute
+    runs only in the HIP library, so a CPU tensor is refused instead of normalised on the host."""
+    layernorm = importlib.import_module("llm-serve_amd.layers.layernorm")
+    awq = importlib.import_module("llm-serve_amd.layers.quantization.awq")
+    norm = layernorm.RMSNorm(64, eps=1e-5)
+    assert norm.eps == 1e-5 and norm.weight.shape == (64,) and norm.weight.dtype == torch.bfloat16
+    assert torch.equal(norm.weight.float(), torch.ones(64))
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        norm(x)
+    with pytest.raises(ValueError, match="GPU"):
+        norm(x, x.clone())
+    with pytest.raises(ValueError, match="GPU"):
+        awq.awq_linear_rmsnorm(x, None, norm.weight, 1e-5, torch.zeros(8, dtype=torch.int32),
+                               torch.zeros(1, 8, dtype=torch.int32), torch.zeros(1, 64, dtype=torch.bfloat16),
+                               group_size=128)
