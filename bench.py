@@ -4,8 +4,8 @@ Headline (`value`): decode-regime aggregate HBM GB/s over the Qwen3-8B projectio
 shapes (QKV 4096x6144, O 4096x4096, gate_up 4096x24576, down 12288x4096) at packed
 M in {1, 4, 8, 16}: sum of algorithmic bytes / sum of kernel time.  One "step" is one
 GEMM at each of those 16 points.  Also reported: M = 32 and 64, the chunked-prefill
-TFLOP/s at M = 2048 (1% of input channels x20), and the oracle CPU baseline on the
-host cores.
+TFLOP/s at M = 2048 (1% of input channels x20), and the reference backend's torch CPU path
+timed on the host cores as the CPU baseline.
 
 Method
   * Inputs are resident in HBM before timing.  Weights are random uniform int32 words
@@ -62,11 +62,6 @@ Also reported (not part of `value`):
     down -- 144 GEMM and 72 norm launches per step, one graph;
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
     in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
-
-Checkpoint mode: `--checkpoint DIR [--layer-id I]` adds `checkpoint_layer`, the four
-projections of layer I of a local Qwen3 AutoAWQ checkpoint (read through its
-model.safetensors.index.json, q|k|v and gate|up merged along N) timed at M in {1, 4, 8, 16}
-on their real weights; `value` stays the synthetic sweep.
 
 Profiling mode: `--profile-point SHAPE:M` runs one point without graphs (a 256 MiB copy
 for counter calibration, then --steps launches over rotating weights) so that
@@ -231,29 +226,50 @@ def time_points(points, stream, steps, warmup):
     return per_point, total
 
 
-def cpu_baseline(seconds_budget: float = 12.0, gpu_gemm=None) -> dict:
-    """The oracle (numpy restatement of the reference backend: dequant to bf16, then an
-    fp32 BLAS matmul, then bf16) on the host at M=16, K=N=4096 (the O projection), repeated
-    for about `seconds_budget` seconds; the median run is reported.  With gpu_gemm (a
-    function of the problem's bit arrays returning the HIP GEMM's bf16 output bits), also
-    the parity of the two results: max |y_gpu - y_cpu| / max(|y_cpu|, rms(y_cpu))."""
-    from oracle import awq_oracle as ora
-
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (platform.processor() as a fallback)."""
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - threadpoolctl is optional
-        threads = os.cpu_count() or 1
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(seconds_budget: float = 12.0, gpu_gemm=None) -> dict:
+    """The reference backend's CPU path (oracle/awq_torch_cpu.py: the same torch ops as the
+    reference's awq_reference_linear -- unpack, bf16 dequant, bf16 matmul on the CPU BLAS)
+    on the host at M=16, K=N=4096 (the O projection) with torch using every host core,
+    after 2 warm-up runs, repeated for about `seconds_budget` seconds; the median run is
+    reported.  With gpu_gemm (a function of the problem's bit arrays returning the HIP
+    GEMM's bf16 output bits), also the parity of the two results:
+    max |y_gpu - y_cpu| / max(|y_cpu|, rms(y_cpu))."""
+    import numpy as np
+
+    from oracle import awq_oracle as ora
+    from oracle import awq_torch_cpu as tref
+
+    threads_before = torch.get_num_threads()
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
     m, k, n = 16, 4096, 4096
     p = ora.make_problem(seed=0, m=m, k=k, n=n)
-    run = lambda: ora.awq_linear_bf16_bits(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)  # noqa: E731
-    y_cpu = ora.bf16_bits_to_f32(run()).astype("float64")
+    qw, qz = torch.from_numpy(p["qweight"]), torch.from_numpy(p["qzeros"])
+    sc = torch.from_numpy(p["scales_bits"].view(np.int16)).view(torch.bfloat16)
+    x = torch.from_numpy(p["x_bits"].view(np.int16)).view(torch.bfloat16)
+    run = lambda: tref.linear(x, qw, qz, sc, 128)  # noqa: E731
+    for _ in range(2):
+        y = run()
+    y_cpu = y.double().numpy()
     times = []
     t_start = time.perf_counter()
     while len(times) < 5 or (time.perf_counter() - t_start < seconds_budget and len(times) < 1000):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
+    torch.set_num_threads(threads_before)
     t = statistics.median(times)
     parity = None
     if gpu_gemm is not None:
@@ -263,9 +279,10 @@ def cpu_baseline(seconds_budget: float = 12.0, gpu_gemm=None) -> dict:
     return {"value": round(algorithmic_bytes(m, k, n) / t / 1e9, 3), "unit": "GB/s", "cores": int(threads),
             "parity_max_rel_err_vs_gpu": parity,
             "kind": "port",
-            "sample": f"oracle dequant+fp32 matmul, M={m} K={k} N={n} (O proj), median of {len(times)} runs "
-                      f"over {time.perf_counter() - t_start:.1f} s, {t * 1e3:.1f} ms/GEMM, host "
-                      f"{platform.processor() or platform.machine()}, os.cpu_count()={os.cpu_count()}"}
+            "sample": f"reference backend's torch CPU path (unpack, bf16 dequant, bf16 matmul; "
+                      f"oracle/awq_torch_cpu.py), M={m} K={k} N={n} (O proj), torch.get_num_threads()={threads}, "
+                      f"median of {len(times)} runs over {time.perf_counter() - t_start:.1f} s after 2 warm-ups, "
+                      f"{t * 1e3:.1f} ms/GEMM, host {cpu_model()}, os.cpu_count()={os.cpu_count()}"}
 
 
 def gpu_gemm_bits(pkg, dev, prob) -> "numpy.ndarray":
@@ -577,28 +594,6 @@ def measured_ceilings(dev, stream) -> dict:
             "hipblaslt_bf16_gate_up_m2048_TFLOP/s": round(2 * PREFILL_M * n * k / (ms * 1e-3) / 1e12, 1)}
 
 
-def checkpoint_layer(lib, dev, stream, path: str, layer_id: int, reps: int) -> dict:
-    """The four projections of one checkpoint layer, repacked on the GPU, each timed as one
-    graph-replayed launch (weights stay in cache across replays: a kernel-time figure, not
-    an HBM one) at M in {1, 4, 8, 16}."""
-    ckpt = importlib.import_module("llm-serve_amd.utils.checkpoint")
-    awq = importlib.import_module("llm-serve_amd.layers.quantization.awq")
-    out = {}
-    for proj in ckpt.load_layer_projections(path, layer_id=layer_id):
-        proj = proj.to(dev)
-        k, n = proj.input_size, proj.output_size
-        weights = [(awq.repack_awq_qweight(proj.qweight), proj.qzeros.contiguous(), proj.scales.contiguous())]
-        row = {"K": k, "N": n}
-        for m in DECODE_M:
-            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
-            p = Point(lib, proj.name, m, k, n, weights, x)
-            ms = time_graph(lambda: p.launch_all(torch.cuda.current_stream(dev).cuda_stream), stream, reps)
-            row[f"M={m}"] = {"us": round(ms * 1e3, 2),
-                             "GB/s": round(algorithmic_bytes(m, k, n) / (ms * 1e-3) / 1e9, 1)}
-        out[proj.name] = row
-    return {"path": os.path.abspath(path), "layer_id": layer_id, "projections": out}
-
-
 FUSED_M = (1, 16, 64, 512, 2048)
 
 
@@ -748,8 +743,6 @@ def main(argv=None):
     ap.add_argument("--no-extra", action="store_true", help="skip the mixed-batch, layer-stack and ceiling legs")
     ap.add_argument("--details", action="store_true", help="print one line per point to stderr")
     ap.add_argument("--profile-point", metavar="SHAPE:M", help="profiling workload for one point (see doc)")
-    ap.add_argument("--checkpoint", metavar="DIR", help="also time one layer of a local Qwen3 AutoAWQ checkpoint")
-    ap.add_argument("--layer-id", type=int, default=0)
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path has no multi-GPU "
@@ -829,12 +822,6 @@ def main(argv=None):
             print(f"stack36_normed: {json.dumps(stack_normed)}", file=sys.stderr)
             print(f"rmsnorm_prologue: {json.dumps(norm)}", file=sys.stderr)
 
-    ckpt_layer = None
-    if args.checkpoint:
-        ckpt_layer = checkpoint_layer(lib, dev, stream, args.checkpoint, args.layer_id, max(3, args.steps))
-        if args.details:
-            print(f"checkpoint layer: {json.dumps(ckpt_layer)}", file=sys.stderr)
-
     cpu = None if args.no_cpu else cpu_baseline(gpu_gemm=lambda prob: gpu_gemm_bits(pkg, dev, prob))
     result = {
         "metric": METRIC,
@@ -867,7 +854,6 @@ def main(argv=None):
         "fused_gate_up": fused,
         "quantize": quant,
         "rmsnorm_prologue": norm,
-        "checkpoint_layer": ckpt_layer,
         "points": points_out,
     }
     print(json.dumps(result))

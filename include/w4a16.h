@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 3
+#define W4A16_ABI_VERSION 4
 
 enum w4a16_status {
   W4A16_OK = 0,
@@ -115,6 +115,14 @@ int w4a16_pack_int4(const int32_t* values, int32_t* packed, int rows, int cols, 
  * Replaces the workspace sizing of awq.py:168-180 and awq_cuda.py:157-176. */
 size_t w4a16_workspace_bytes(int M, int K, int N, int group_size);
 
+/* The largest w4a16_workspace_bytes(M, K, N, group_size) over 1 <= M <= M_max: one buffer of
+ * this size, allocated and zero-filled at load time, serves every call with M <= M_max at
+ * this shape (e.g. M_max = the engine's max_num_batched_tokens, 16384 by default), so the
+ * GEMM calls never allocate.  0 for M_max < 1 or an invalid shape.
+ * Replaces the load-time workspace allocation of process_weights_after_loading
+ * (awq.py:168-180), which the reference sizes for its M <= 16 split-K kernel only. */
+size_t w4a16_workspace_bytes_max(int M_max, int K, int N, int group_size);
+
 /* y[M, N] = x[M, K] @ W with W given as (packed, qzeros, scales); bf16 in and out, fp32
  * accumulation.  M >= 0 (M == 0 is a no-op), K % 128 == 0, N % 64 == 0, group_size == 128,
  * K * N / 2 < 2^31 bytes of packed weights; x, packed, y 16-byte and qzeros, scales 4-byte
@@ -158,6 +166,16 @@ int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t*
  * Replaces RMSNorm.rms_forward / add_rms_forward (layernorm.py:16-40). */
 int w4a16_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
                       uint16_t* x_norm, uint16_t* residual_out, int M, int K, void* stream);
+
+/* RMSNorm without a residual (as w4a16_add_rmsnorm with residual == NULL) of rows read
+ * through two strides: row r of x starts at element
+ * (r / rows_inner) * stride_outer + (r % rows_inner) * stride_inner; x_norm is contiguous
+ * [M, K].  Strides are multiples of 8 elements, x 16-byte aligned; other limits as
+ * w4a16_add_rmsnorm.  Rows of K <= 512 share a wave (8 .. 64 lanes per row).
+ * Replaces RMSNorm.rms_forward (layernorm.py:16-25) on a non-contiguous view: q_norm and
+ * k_norm over q.view(-1, heads, head_dim) of the split QKV output (qwen3.py:87-94). */
+int w4a16_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_outer, int64_t stride_inner,
+                          const uint16_t* weight, float eps, uint16_t* x_norm, int M, int K, void* stream);
 
 /* The RMSNorm(+residual) prologue of w4a16_add_rmsnorm followed, on the same stream and in
  * the same call, by w4a16_gemm (silu_mul == 0) or w4a16_gemm_silu_mul (silu_mul == 1) of

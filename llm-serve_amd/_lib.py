@@ -31,6 +31,7 @@ _SIGNATURES = {
     "w4a16_repack_qweight": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
     "w4a16_dequant_packed": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr]),
     "w4a16_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "w4a16_workspace_bytes_max": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "w4a16_gemm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
                             _c_ptr, _c_size, _c_ptr]),
     "w4a16_regime": (_c_int, [_c_int, _c_int, _c_int]),
@@ -48,10 +49,12 @@ _SIGNATURES = {
                                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size,
                                             _c_ptr]),
     "w4a16_add_rmsnorm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr]),
+    "w4a16_rmsnorm_strided": (_c_int, [_c_ptr, _c_int, ctypes.c_int64, ctypes.c_int64, _c_ptr, ctypes.c_float,
+                                       _c_ptr, _c_int, _c_int, _c_ptr]),
     "w4a16_gemm_rmsnorm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                     _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def _ptr(t: torch.Tensor | None):
@@ -101,6 +104,9 @@ class W4A16Library:
     # ------------------------------------------------------------ host queries
     def workspace_bytes(self, m: int, k: int, n: int, group_size: int = 128) -> int:
         return int(self.dll.w4a16_workspace_bytes(m, k, n, group_size))
+
+    def workspace_bytes_max(self, m_max: int, k: int, n: int, group_size: int = 128) -> int:
+        return int(self.dll.w4a16_workspace_bytes_max(m_max, k, n, group_size))
 
     def workspace_bytes_config(self, m: int, n: int, regime: int, p0: int, split: int) -> int:
         return int(self.dll.w4a16_workspace_bytes_config(m, n, regime, p0, split))
@@ -222,6 +228,17 @@ class W4A16Library:
             self.check(self.dll.w4a16_add_rmsnorm(x.data_ptr(), _ptr(residual), weight.data_ptr(), float(eps),
                                                   x_norm.data_ptr(), _ptr(residual_out), m, k, self._stream(x)),
                        "w4a16_add_rmsnorm")
+        return x_norm
+
+    def rmsnorm_strided(self, x, rows_inner: int, stride_outer: int, stride_inner: int, weight, eps: float,
+                        x_norm, m: int, k: int) -> torch.Tensor:
+        """x_norm [m, k] = RMSNorm of rows read at x + (r // rows_inner) * stride_outer +
+        (r % rows_inner) * stride_inner (elements), no residual."""
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_rmsnorm_strided(x.data_ptr(), rows_inner, stride_outer, stride_inner,
+                                                      weight.data_ptr(), float(eps), x_norm.data_ptr(), m, k,
+                                                      self._stream(x)),
+                       "w4a16_rmsnorm_strided")
         return x_norm
 
     def gemm_rmsnorm(self, x, residual, weight, eps: float, x_norm, residual_out, packed, qzeros, scales, y,

@@ -213,11 +213,10 @@ int validate_gemm(const void* x, const void* packed, const void* qzeros, const v
   return ok();
 }
 
-// up_tiles: 0 for the plain GEMM, N / 32 for the fused SiLU(gate) * up (y is [M, N / 2]).
-// res: null, or a bf16 [M, N] residual added in the epilogue (plain GEMM; may be y).
-int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
-             const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
-             hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr) {
+// Every check a planned GEMM can fail on after argument validation: workspace size and
+// alignment, partial and counter limits of a K split, and the tile kernel's row chunks.
+// Callers run it before enqueueing anything, so a failing call leaves no work behind.
+int check_plan(const GemmPlan& p, int M, int K, int N, const void* workspace, size_t workspace_bytes) {
   if (p.regime == W4A16_REGIME_NONE) return ok();
   const size_t need = workspace_for(p, M, N);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -228,6 +227,20 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   if (need > 0 && counters_needed(p, M, N) > kMaxCounters)
     return fail(W4A16_ERR_SHAPE, "split-K needs %zu arrival counters (limit %zu)", counters_needed(p, M, N),
                 kMaxCounters);
+  if (p.regime == W4A16_REGIME_TILE && (kMaxTensorBytes - 1) / (2 * static_cast<size_t>(K)) < static_cast<size_t>(tile_bm(p)))
+    return fail(W4A16_ERR_SHAPE, "K=%d is too long for one %d-row tile below 2 GiB", K, tile_bm(p));
+  return ok();
+}
+
+// up_tiles: 0 for the plain GEMM, N / 32 for the fused SiLU(gate) * up (y is [M, N / 2]).
+// res: null, or a bf16 [M, N] residual added in the epilogue (plain GEMM; may be y).
+int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+             const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
+             hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr) {
+  if (p.regime == W4A16_REGIME_NONE) return ok();
+  const int c = check_plan(p, M, K, N, workspace, workspace_bytes);
+  if (c != W4A16_OK) return c;
+  const size_t need = workspace_for(p, M, N);
   int* counters = need ? static_cast<int*>(workspace) : nullptr;
   float* partials = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
   const uint32_t* pk = reinterpret_cast<const uint32_t*>(packed);
@@ -242,8 +255,7 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const int bm = tile_bm(p);
   const size_t n_out = up_tiles ? N / 2 : N;
   const size_t fit = (kMaxTensorBytes - 1) / (2 * static_cast<size_t>(K));
-  const int chunk = fit >= static_cast<size_t>(M) ? M : static_cast<int>(fit / bm) * bm;
-  if (chunk <= 0) return fail(W4A16_ERR_SHAPE, "K=%d is too long for one %d-row tile below 2 GiB", K, bm);
+  const int chunk = fit >= static_cast<size_t>(M) ? M : static_cast<int>(fit / bm) * bm;  // > 0: check_plan
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int mc = M - r0 < chunk ? M - r0 : chunk;
     const int rc = check_launch(w4a16::launch_tile_cfg(x + static_cast<size_t>(r0) * K, pk, qz, scales,
@@ -289,6 +301,23 @@ int w4a16_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_
                       "add_rmsnorm");
 }
 
+int w4a16_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_outer, int64_t stride_inner,
+                          const uint16_t* weight, float eps, uint16_t* x_norm, int M, int K, void* stream) {
+  int v = validate_norm(x, nullptr, weight, eps, x_norm, nullptr, M, K);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  if (rows_inner <= 0 || stride_outer < 0 || stride_inner < 0)
+    return fail(W4A16_ERR_ARG, "rows_inner must be positive and the strides non-negative");
+  if (stride_outer % 8 || stride_inner % 8)
+    return fail(W4A16_ERR_ALIGN, "row strides must be multiples of 8 elements (16 bytes)");
+  const int64_t last = static_cast<int64_t>((M - 1) / rows_inner) * stride_outer +
+                       static_cast<int64_t>((M - 1) % rows_inner) * stride_inner + K;
+  if (last >= (int64_t(1) << 40)) return fail(W4A16_ERR_SHAPE, "strided rows span too far");
+  return check_launch(w4a16::launch_rmsnorm_strided(x, rows_inner, stride_outer, stride_inner, weight, x_norm, M, K,
+                                                    eps, static_cast<hipStream_t>(stream)),
+                      "rmsnorm_strided");
+}
+
 int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* norm_weight, float eps,
                        uint16_t* x_norm, uint16_t* residual_out, const int32_t* packed, const int32_t* qzeros,
                        const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size, int silu_mul,
@@ -301,10 +330,8 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
   if (M == 0) return ok();
   // Every check that could fail the GEMM runs before the prologue is enqueued.
   const GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
-  const size_t need = workspace_for(p, M, N);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-    return fail(W4A16_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-  if (need > 0 && !aligned(workspace, 256)) return fail(W4A16_ERR_ALIGN, "workspace must be 256-byte aligned");
+  v = check_plan(p, M, K, N, workspace, workspace_bytes);
+  if (v != W4A16_OK) return v;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   v = check_launch(w4a16::launch_add_rmsnorm(x, residual, norm_weight, x_norm, residual_out, M, K, eps, s),
                    "add_rmsnorm");
@@ -407,6 +434,15 @@ size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
   if (N % 128) return plain;
   const size_t fused = workspace_for(plan_silu_mul(M, K, N), M, N);
   return fused > plain ? fused : plain;
+}
+
+size_t w4a16_workspace_bytes_max(int M_max, int K, int N, int group_size) {
+  size_t most = 0;
+  for (int m = 1; m <= M_max; ++m) {
+    const size_t b = w4a16_workspace_bytes(m, K, N, group_size);
+    most = b > most ? b : most;
+  }
+  return most;
 }
 
 int w4a16_regime(int M, int K, int N) {

@@ -87,5 +87,11 @@ constexpr int kNormMaxK = 16384;
 hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
                               uint16_t* x_norm, uint16_t* residual_out, int M, int K, float eps,
                               hipStream_t stream);
+// RMSNorm without a residual of rows read through two strides: row r of x starts at element
+// (r / rows_inner) * stride_outer + (r % rows_inner) * stride_inner (multiples of 8, x 16-byte
+// aligned); x_norm is contiguous [M, K].
+hipError_t launch_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_outer, int64_t stride_inner,
+                                  const uint16_t* weight, uint16_t* x_norm, int M, int K, float eps,
+                                  hipStream_t stream);
 
 }  // namespace w4a16

@@ -1,5 +1,6 @@
 // RMSNorm with the optional residual add in front of it: the normalisation that feeds
-// the QKV and gate_up projections of every decoder layer.  One workgroup per row.
+// the QKV and gate_up projections of every decoder layer, and the per-head q_norm / k_norm
+// applied to strided views of the QKV output.
 //
 // Per row of K elements, in the reference's order (layernorm.py:17-40):
 //   s  = float(x) + float(residual)            (fp32; s = float(x) without a residual)
@@ -10,6 +11,13 @@
 // residual or x, and x_norm may be x: every element is read by the thread that writes it,
 // before it writes it.  HBM-bound: 4K bytes read and 4K written per row with a residual,
 // 2K + 2K without (the weight row is L2-resident after the first workgroups).
+//
+// LPR lanes work on one row, each on 16-byte chunks: rows of K > 512 take a whole
+// 256-lane workgroup (sum of squares: wave shuffles, then four partial sums through LDS);
+// shorter rows (the 128-wide heads) take LPR = 8 .. 64 lanes of one wave, 256 / LPR rows per
+// workgroup, reduced by shuffles inside the lane group.  Row r of x starts at element
+// (r / rows_inner) * stride_outer + (r % rows_inner) * stride_inner; residual, residual_out
+// and x_norm are contiguous [M, K].
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
 
@@ -17,47 +25,96 @@ namespace w4a16 {
 namespace {
 
 constexpr int kNormThreads = 256;
-constexpr int kNormChunks = kNormMaxK / (8 * kNormThreads);  // 16-byte chunks per thread
 
-template <bool RES>
+template <bool RES, int LPR>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_t* x, const uint16_t* residual,
                                                                     const uint16_t* __restrict__ weight,
-                                                                    uint16_t* x_norm, uint16_t* residual_out, int K,
-                                                                    float eps) {
-  const size_t row = static_cast<size_t>(blockIdx.x) * K;
+                                                                    uint16_t* x_norm, uint16_t* residual_out, int M,
+                                                                    int K, int rows_inner, int64_t stride_outer,
+                                                                    int64_t stride_inner, float eps) {
+  constexpr int kRows = kNormThreads / LPR;             // rows per workgroup
+  // 16-byte chunks per lane: up to 8 for whole-workgroup rows, one for shorter rows (the
+  // launcher picks LPR >= K / 8 for them).
+  constexpr int kChunks = LPR == kNormThreads ? kNormMaxK / (8 * kNormThreads) : 1;
+  const int sub = threadIdx.x / LPR;
+  const int l = threadIdx.x % LPR;
+  const int r = blockIdx.x * kRows + sub;
+  const bool live = r < M;  // uniform over the lanes of a row
+  const int64_t xrow = live ? static_cast<int64_t>(r / rows_inner) * stride_outer +
+                                  static_cast<int64_t>(r % rows_inner) * stride_inner
+                            : 0;
+  const size_t row = static_cast<size_t>(live ? r : 0) * K;
   const int chunks = K >> 3;
-  float s[kNormChunks][8];
+  float s[kChunks][8];
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = threadIdx.x + j * kNormThreads;
-    if (c < chunks) {
-      unpack_bf16x8(*reinterpret_cast<const uint4*>(x + row + 8 * c), s[j]);
+  for (int j = 0; j < kChunks; ++j) {
+    const int c = l + j * LPR;
+    if (live && c < chunks) {
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(x + xrow + 8 * c), s[j]);
       if constexpr (RES) {
-        float r[8];
-        unpack_bf16x8(*reinterpret_cast<const uint4*>(residual + row + 8 * c), r);
+        float rr[8];
+        unpack_bf16x8(*reinterpret_cast<const uint4*>(residual + row + 8 * c), rr);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s[j][i] += r[i];
+        for (int i = 0; i < 8; ++i) s[j][i] += rr[i];
         *reinterpret_cast<uint4*>(residual_out + row + 8 * c) = pack_bf16x8(s[j]);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += s[j][i] * s[j][i];
     }
   }
-  __shared__ float part[kNormThreads / 64];
-  ss = wave_sum64(ss);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float var = ((part[0] + part[1]) + (part[2] + part[3])) / static_cast<float>(K);
-  const float rstd = rsqrt_rn(var + eps);
+  float total;
+  if constexpr (LPR == kNormThreads) {
+    __shared__ float part[kNormThreads / 64];
+    ss = wave_sum64(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    total = (part[0] + part[1]) + (part[2] + part[3]);
+  } else {
 #pragma unroll
-  for (int j = 0; j < kNormChunks; ++j) {
-    const int c = threadIdx.x + j * kNormThreads;
-    if (c < chunks) {
+    for (int off = LPR / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    total = ss;
+  }
+  const float rstd = rsqrt_rn(total / static_cast<float>(K) + eps);
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int c = l + j * LPR;
+    if (live && c < chunks) {
       *reinterpret_cast<uint4*>(x_norm + row + 8 * c) =
           rms_scale_bf16x8(s[j], rstd, *reinterpret_cast<const uint4*>(weight + 8 * c));
     }
   }
+}
+
+template <bool RES, int LPR>
+hipError_t launch_lpr(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, uint16_t* x_norm,
+                      uint16_t* residual_out, int M, int K, int rows_inner, int64_t stride_outer,
+                      int64_t stride_inner, float eps, hipStream_t stream) {
+  constexpr int kRows = kNormThreads / LPR;
+  add_rmsnorm_kernel<RES, LPR><<<(M + kRows - 1) / kRows, kNormThreads, 0, stream>>>(
+      x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer, stride_inner, eps);
+  return hipGetLastError();
+}
+
+template <bool RES>
+hipError_t launch_rows(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, uint16_t* x_norm,
+                       uint16_t* residual_out, int M, int K, int rows_inner, int64_t stride_outer,
+                       int64_t stride_inner, float eps, hipStream_t stream) {
+  const int chunks = K / 8;
+  if (chunks <= 8)
+    return launch_lpr<RES, 8>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                              stride_inner, eps, stream);
+  if (chunks <= 16)
+    return launch_lpr<RES, 16>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                               stride_inner, eps, stream);
+  if (chunks <= 32)
+    return launch_lpr<RES, 32>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                               stride_inner, eps, stream);
+  if (chunks <= 64)
+    return launch_lpr<RES, 64>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                               stride_inner, eps, stream);
+  return launch_lpr<RES, kNormThreads>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                                       stride_inner, eps, stream);
 }
 
 }  // namespace
@@ -66,11 +123,16 @@ hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const
                               uint16_t* x_norm, uint16_t* residual_out, int M, int K, float eps,
                               hipStream_t stream) {
   if (M <= 0) return hipSuccess;
-  if (residual)
-    add_rmsnorm_kernel<true><<<M, kNormThreads, 0, stream>>>(x, residual, weight, x_norm, residual_out, K, eps);
-  else
-    add_rmsnorm_kernel<false><<<M, kNormThreads, 0, stream>>>(x, nullptr, weight, x_norm, nullptr, K, eps);
-  return hipGetLastError();
+  if (residual) return launch_rows<true>(x, residual, weight, x_norm, residual_out, M, K, M, 0, K, eps, stream);
+  return launch_rows<false>(x, nullptr, weight, x_norm, nullptr, M, K, M, 0, K, eps, stream);
+}
+
+hipError_t launch_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_outer, int64_t stride_inner,
+                                  const uint16_t* weight, uint16_t* x_norm, int M, int K, float eps,
+                                  hipStream_t stream) {
+  if (M <= 0) return hipSuccess;
+  return launch_rows<false>(x, nullptr, weight, x_norm, nullptr, M, K, rows_inner, stride_outer, stride_inner, eps,
+                            stream);
 }
 
 }  // namespace w4a16

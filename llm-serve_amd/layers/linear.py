@@ -114,7 +114,8 @@ class ColumnParallelLinear(LinearBase):
     def forward_rmsnorm(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None):
         """``self(norm(x, residual))`` for an RMSNorm ``norm`` (its ``weight`` and ``eps``) in
         front of this projection -- input_layernorm then qkv_proj (qwen3.py:166-169) -- as
-        one library call; returns ``(y, new residual)``, the residual None when none is given."""
+        one library call; returns ``(y, new residual)``.  Without a residual (the first
+        layer) the new residual is ``x`` itself, as qwen3.py:166-167 sets it."""
         return self._rmsnorm_apply(norm, x, residual, silu_mul=False)
 
     def _rmsnorm_apply(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None, silu_mul: bool):
@@ -155,7 +156,7 @@ class MergedColumnParallelLinear(ColumnParallelLinear):
     def forward_rmsnorm_silu_and_mul(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None):
         """``SiluAndMul()(self(norm(x, residual)))`` -- post_attention_layernorm then the MLP's
         gate_up and activation (qwen3.py:172-173, 126-130) -- as one library call; returns
-        ``(y, new residual)`` (the residual is None when none is given)."""
+        ``(y, new residual)`` (``x`` itself when no residual is given)."""
         if len(self.output_sizes) != 2 or self.output_sizes[0] != self.output_sizes[1]:
             raise ValueError("fused SiLU * up needs exactly two equal output shards (gate, up)")
         return self._rmsnorm_apply(norm, x, residual, silu_mul=True)

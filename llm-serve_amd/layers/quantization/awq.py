@@ -38,7 +38,6 @@ from ..._lib import REGIME_DECODE, lib
 
 AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
 EXECUTION_BACKEND = "hip"
-DECODE_MAX_M = 64
 
 
 @dataclass(frozen=True)
@@ -51,6 +50,9 @@ class AWQRuntimeConfig:
     activation_dtype: torch.dtype
     quant_method: str = "awq"
     execution_backend: str = EXECUTION_BACKEND
+    # Most tokens the engine packs into one GEMM (its Config.max_num_batched_tokens, 16384 by
+    # default, config.py:11): the split-K workspace is reserved for that M at load time.
+    max_batched_tokens: int = 16384
 
     @property
     def pack_factor(self) -> int:
@@ -99,9 +101,13 @@ class _WorkspacePool:
     """Split-K workspace shared by all layers issuing on one (device, stream).
 
     Kernels on one stream run in order, so one buffer per stream serves every layer; it
-    is zero-filled when (re)allocated and the kernels re-arm their counters to zero.  A
-    buffer that is outgrown stays referenced for the life of the pool: a HIP graph captured
-    earlier may still address it, so its memory must not return to the allocator."""
+    is zero-filled when (re)allocated and the kernels re-arm their counters to zero.
+    ``reserve`` (called by ``process_weights_after_loading`` for the largest M the engine
+    packs) allocates outside the hot path; ``get`` never allocates while the current stream
+    is capturing a HIP graph -- it raises instead, since an allocation there would become
+    part of the graph.  A buffer that is outgrown stays referenced for the life of the
+    pool: a graph captured earlier may still address it, so its memory must not return to
+    the allocator."""
 
     def __init__(self):
         self._lock = threading.Lock()
@@ -116,6 +122,12 @@ class _WorkspacePool:
         with self._lock:
             buf = self._buffers.get(key)
             if buf is None or buf.numel() < nbytes:
+                if torch.cuda.is_current_stream_capturing():
+                    have = 0 if buf is None else buf.numel()
+                    raise RuntimeError(
+                        f"AWQ split-K workspace of {nbytes} bytes needed during HIP graph capture, but this "
+                        f"stream's workspace holds {have}: reserve it before capturing (process the layers on "
+                        f"this stream, or call WORKSPACE.reserve)")
                 if buf is not None:
                     self._retired.append(buf)
                 size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
@@ -126,14 +138,20 @@ class _WorkspacePool:
     def reserve(self, device: torch.device, nbytes: int) -> None:
         self.get(device, nbytes)
 
+    def reserved_bytes(self, device: torch.device) -> int:
+        stream = torch.cuda.current_stream(device).cuda_stream
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._buffers.get(key)
+            return 0 if buf is None else buf.numel()
+
 
 WORKSPACE = _WorkspacePool()
 
 
-def decode_workspace_bytes(k: int, n: int, group_size: int = 128) -> int:
-    """Largest workspace any M <= 64 call at this shape needs."""
-    library = lib()
-    return max(library.workspace_bytes(m, k, n, group_size) for m in range(1, DECODE_MAX_M + 1))
+def max_workspace_bytes(k: int, n: int, max_tokens: int, group_size: int = 128) -> int:
+    """Largest workspace any call with M <= max_tokens needs at this shape."""
+    return lib().workspace_bytes_max(max_tokens, k, n, group_size)
 
 
 # ------------------------------------------------------------- linear method
@@ -214,8 +232,11 @@ class AWQLinearMethod:
         layer.register_buffer("awq_qweight", packed, persistent=False)
         layer.register_buffer("awq_qzeros", qzeros, persistent=False)
         layer.awq_shape = (k, n)
-        # decode calls then never allocate (hipGraph capture, tight serving loops)
-        WORKSPACE.reserve(packed.device, decode_workspace_bytes(k, n, self.config.group_size))
+        # calls up to the engine's largest packed M then never allocate (hipGraph capture,
+        # tight serving loops)
+        with torch.cuda.device(packed.device):
+            WORKSPACE.reserve(packed.device, max_workspace_bytes(k, n, self.config.max_batched_tokens,
+                                                                 self.config.group_size))
 
 
 # ------------------------------------------------------------ tensor functions
@@ -383,8 +404,11 @@ def awq_linear_silu_mul(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzer
     return y.reshape(*lead, n // 2)
 
 
-def _norm_operands(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor):
-    """Validated [M, K] views of the RMSNorm operands (bf16, contiguous, 16-byte aligned)."""
+def _norm_operands(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, strided_ok: bool = False):
+    """Validated [M, K] views of the RMSNorm operands (bf16, contiguous, 16-byte aligned).
+    With ``strided_ok`` (no residual) x may be a view whose rows lie at two strides (e.g.
+    ``q.view(-1, heads, head_dim)`` of a split QKV output); then the first value returned is
+    x itself and the row layout comes from ``_row_strides``."""
     if x.device.type != "cuda":
         raise ValueError("RMSNorm input must be on a GPU (HIP) device")
     k = x.shape[-1]
@@ -392,6 +416,8 @@ def _norm_operands(x: torch.Tensor, residual: torch.Tensor | None, weight: torch
     for name, t in tensors:
         if t.dtype != torch.bfloat16 or t.device != x.device:
             raise ValueError(f"RMSNorm {name} must be a bfloat16 tensor on the input's GPU")
+        if name == "input" and strided_ok and _row_strides(x) is not None:
+            continue
         if not t.is_contiguous() or not _aligned16(t):
             raise ValueError(f"RMSNorm {name} must be contiguous and 16-byte aligned")
     if weight.shape != (k,):
@@ -401,7 +427,37 @@ def _norm_operands(x: torch.Tensor, residual: torch.Tensor | None, weight: torch
     if k % 8 or k > 16384:
         raise ValueError(f"RMSNorm width must be a multiple of 8 and at most 16384 (got {k})")
     m = x.numel() // k if k else 0
-    return x.reshape(m, k), (residual.reshape(m, k) if residual is not None else None), m, k
+    xv = x if strided_ok and not x.is_contiguous() else x.reshape(m, k)
+    return xv, (residual.reshape(m, k) if residual is not None else None), m, k
+
+
+def _row_strides(x: torch.Tensor):
+    """(rows_inner, stride_outer, stride_inner) in elements when every row of x (its last
+    dimension, unit stride) starts at (r // rows_inner) * stride_outer + (r % rows_inner) *
+    stride_inner from x's first element with 16-byte aligned rows; None otherwise."""
+    if x.stride(-1) != 1 or x.data_ptr() % 16:
+        return None
+    dims = [(size, stride) for size, stride in zip(x.shape[:-1], x.stride()[:-1]) if size != 1]
+    # merge leading dimensions that are contiguous with each other
+    merged: list[list[int]] = []
+    for size, stride in dims:
+        if merged and merged[-1][1] == stride * size:
+            merged[-1] = [merged[-1][0] * size, stride]
+        else:
+            merged.append([size, stride])
+    if not merged:
+        return (1, 0, 0)
+    if len(merged) == 1:
+        rows, stride = merged[0]
+        out = (rows, 0, stride)
+    elif len(merged) == 2:
+        (_, s_outer), (rows_inner, s_inner) = merged
+        out = (rows_inner, s_outer, s_inner)
+    else:
+        return None
+    if out[1] % 8 or out[2] % 8:
+        return None
+    return out
 
 
 def add_rms_norm(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float,
@@ -409,17 +465,24 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.T
     """The reference's RMSNorm forward (layernorm.py:16-50) on the HIP kernel: without a
     residual, ``bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight)``; with one, the same of
     ``s = x + residual`` (fp32) and also the new residual ``bf16(s)``, returned as
-    ``(x_norm, residual_out)``.  ``residual_out`` may be ``residual`` (in place)."""
-    xv, rv, m, k = _norm_operands(x, residual, weight)
-    x_norm = torch.empty_like(x)
+    ``(x_norm, residual_out)``.  ``residual_out`` may be ``residual`` (in place).  Without a
+    residual, x may be a strided view (rows at up to two strides, unit stride inside a row),
+    as q_norm / k_norm see the per-head views of the split QKV output (qwen3.py:87-94); the
+    result is then a new contiguous tensor of x's shape, as the reference's is."""
+    xv, rv, m, k = _norm_operands(x, residual, weight, strided_ok=residual is None)
+    x_norm = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if residual is not None and residual_out is None:
         residual_out = torch.empty_like(x)
     if residual_out is not None and (residual_out.shape != x.shape or residual_out.dtype != torch.bfloat16
                                      or not residual_out.is_contiguous() or not _aligned16(residual_out)):
         raise ValueError("RMSNorm residual_out must be a contiguous, 16-byte aligned bf16 tensor of the input shape")
     if m > 0:
-        lib().add_rmsnorm(xv, rv, weight, eps, x_norm.view(m, k),
-                          residual_out.view(m, k) if residual_out is not None else None)
+        if residual is None and not x.is_contiguous():
+            rows_inner, s_outer, s_inner = _row_strides(x)
+            lib().rmsnorm_strided(x, rows_inner, s_outer, s_inner, weight, eps, x_norm.view(m, k), m, k)
+        else:
+            lib().add_rmsnorm(xv, rv, weight, eps, x_norm.view(m, k),
+                              residual_out.view(m, k) if residual_out is not None else None)
     return x_norm if residual is None else (x_norm, residual_out)
 
 
@@ -430,9 +493,11 @@ def awq_linear_rmsnorm(inputs: torch.Tensor, residual: torch.Tensor | None, norm
     """The RMSNorm(+residual) in front of QKV or gate_up and the projection in one library
     call (qwen3.py:166-173 and 126-130 with layernorm.py:28-40): returns ``(y, residual_out)``
     with ``y = awq_linear(add_rms_norm(...))`` -- or, with ``silu_mul``, its SiLU(g) * u --
-    and ``residual_out = bf16(inputs + residual)`` (None without a residual; may be
-    ``residual`` itself).  The normalised activations go through a scratch tensor of the
-    input's shape that the GEMM reads back from L2 at decode sizes."""
+    and ``residual_out = bf16(inputs + residual)`` (may be ``residual`` itself).  Without a
+    residual the new residual is ``inputs`` itself, as the reference's first decoder layer
+    sets it (qwen3.py:166-167: ``hidden_states, residual = input_layernorm(hidden_states),
+    hidden_states``).  The normalised activations go through a scratch tensor of the input's
+    shape that the GEMM reads back from L2 at decode sizes."""
     xv, rv, m, k = _norm_operands(inputs, residual, norm_weight)
     lead = inputs.shape[:-1]
     _, _, k2, n = _prepare_linear(xv, packed_qweight, qzeros, scales, group_size)
@@ -455,7 +520,7 @@ def awq_linear_rmsnorm(inputs: torch.Tensor, residual: torch.Tensor | None, norm
         library.gemm_rmsnorm(xv, rv, norm_weight, eps, x_norm,
                              residual_out.view(m, k) if residual_out is not None else None, packed_qweight,
                              qzeros, scales.contiguous(), y, n, workspace, group_size, silu_mul)
-    return y.reshape(*lead, n_out), residual_out
+    return y.reshape(*lead, n_out), (residual_out if residual is not None else inputs)
 
 
 def awq_regime(m: int, k: int, n: int) -> str:

@@ -38,7 +38,7 @@ def test_binding_signatures_cover_the_header(pkg):
 
 def test_abi_version_and_empty_error(pkg):
     L = pkg.lib()
-    assert L.dll.w4a16_abi_version() == 3
+    assert L.dll.w4a16_abi_version() == 4
     assert isinstance(L.last_error(), str)
 
 
@@ -229,3 +229,49 @@ def test_rmsnorm_entry_points_validate_without_launching(pkg):
     m, k, n = 32, 4096, 4096
     assert L.split_k(m, k, n) > 1
     assert fused(p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0, None, 0, None) == 4
+
+
+def test_workspace_bytes_max_covers_every_m(pkg):
+    """w4a16_workspace_bytes_max(M_max, K, N) is the largest per-call need up to M_max, for the
+    plain and the fused plans alike, at every Qwen3-8B shape."""
+    L = pkg.lib()
+    for k, n in ((4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)):
+        for m_max in (1, 16, 64, 600):
+            want = max(L.workspace_bytes(m, k, n) for m in range(1, m_max + 1))
+            assert L.workspace_bytes_max(m_max, k, n) == want, (k, n, m_max)
+    # the engine default (16384 tokens) covers chunked prefill: more than any decode-only size
+    assert L.workspace_bytes_max(16384, 12288, 4096) >= L.workspace_bytes_max(64, 12288, 4096)
+    assert L.workspace_bytes_max(16384, 12288, 4096) >= L.workspace_bytes(512, 12288, 4096) > 0
+    assert L.workspace_bytes_max(0, 4096, 4096) == 0
+    assert L.workspace_bytes_max(64, 4096, 4100) == 0
+
+
+def test_rmsnorm_strided_validates_without_launching(pkg):
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    f = L.dll.w4a16_rmsnorm_strided
+    # (x, rows_inner, stride_outer, stride_inner, weight, eps, x_norm, M, K, stream)
+    assert f(p, 32, 6144, 128, p, 1e-6, p, 0, 128, None) == 0  # M == 0: nothing enqueued
+    assert f(p, 32, 6144, 130, p, 1e-6, p, 64, 128, None) == 3 and "multiples of 8" in L.last_error()
+    assert f(p, 0, 6144, 128, p, 1e-6, p, 64, 128, None) == 1
+    assert f(p, 32, -8, 128, p, 1e-6, p, 64, 128, None) == 1
+    assert f(p, 32, 6144, 128, p, 1e-6, p, 64, 132, None) == 2
+    assert f(p + 2, 32, 6144, 128, p, 1e-6, p, 64, 128, None) == 3
+
+
+def test_plan_errors_come_before_anything_is_enqueued(pkg):
+    """w4a16_gemm_rmsnorm runs every plan check (workspace size and alignment) before the norm
+    is enqueued: with host pointers a launch would fault, so a clean error code proves no
+    launch was attempted."""
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 1024)()
+    base = ctypes.addressof(buf)
+    p = base + (256 - base % 256) % 256 if (256 - base % 256) % 256 + 512 <= 1024 else base
+    m, k, n = 32, 4096, 4096
+    need = L.workspace_bytes(m, k, n)
+    assert need > 0
+    fused = L.dll.w4a16_gemm_rmsnorm
+    args = (p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0)
+    assert fused(*args, p, need - 1, None) == 4 and "workspace" in L.last_error()
+    assert fused(*args, p + 16, need, None) == 3 and "256-byte" in L.last_error()

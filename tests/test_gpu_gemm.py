@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, decode_config_accepted, golden_cases,
-                         pkg, random_awq_gpu, random_x_gpu, rel_err, to_gpu)
+                         pkg, random_awq_gpu, random_x_gpu, rel_err, to_gpu, assert_gemm_close)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -31,7 +31,7 @@ def test_gemm_matches_oracle_on_golden_fixtures(gpu_lib, case):
                 "x_bits": c["x_bits"]})
     y = hip_linear(t)
     assert y.dtype == torch.bfloat16 and y.shape == c["y_f64"].shape
-    assert rel_err(y, c["y_f64"]) <= GEMM_REL_TOL
+    assert_gemm_close(y, c["y_f64"])
 
 
 def test_decode_token_counts_reference_recipe(gpu_lib):
@@ -49,7 +49,7 @@ def test_decode_token_counts_reference_recipe(gpu_lib):
         y = hip_linear(t)
         want = ora.bf16_bits_to_f32(ora.awq_linear_bf16_bits(x, base["qweight"], base["qzeros"], s, 128))
         torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.02, atol=0.05)
-        assert rel_err(y, ora.awq_linear_ref(x, base["qweight"], base["qzeros"], s, 128)) <= GEMM_REL_TOL
+        assert_gemm_close(y, ora.awq_linear_ref(x, base["qweight"], base["qzeros"], s, 128))
 
 
 def test_single_token_wide_gemv_reference_recipe(gpu_lib):
@@ -82,8 +82,7 @@ def test_every_decode_configuration(gpu_lib, m):
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
         gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 1, tn, waves, split, ws, p2=depth)
-        err = rel_err(y, want)
-        assert err <= GEMM_REL_TOL, (tn, waves, depth, split, err)
+        assert_gemm_close(y, want, (tn, waves, depth, split))
         if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
@@ -96,7 +95,7 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
     p = ora.make_problem(seed=300 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     y = hip_linear(t)
-    assert rel_err(y, ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)) <= GEMM_REL_TOL
+    assert_gemm_close(y, ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128))
 
 
 # (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
@@ -118,8 +117,7 @@ def test_every_tile_configuration(gpu_lib, m, n):
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
         gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, occ, split, ws, p2=shape)
-        err = rel_err(y, want)
-        assert err <= GEMM_REL_TOL, (wm, shape, occ, split, err)
+        assert_gemm_close(y, want, (wm, shape, occ, split))
         if ws_bytes:  # arrival counters (the first 64 KiB) are re-armed to zero
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
@@ -135,7 +133,7 @@ def test_shared_workspace_across_shapes_and_m(gpu_lib):
         for m in (1, 4, 16, 64, 200, 16, 1):
             x = random_x_gpu(m, k, seed=m)
             y = awq_mod().awq_linear(x, packed, qz, s, group_size=128, workspace=ws)
-            assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL, (n, m)
+            assert_gemm_close(y, full_reference(x, qw, qz, s), (n, m))
     assert int(torch.count_nonzero(ws[:65536])) == 0
 
 
@@ -164,8 +162,7 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
         assert pkg().awq_regime(m, k, n) == ("tile" if m > 48 and n >= 16384 else "decode")
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
-        err = rel_err(y, full_reference(x, qw, qz, s))
-        assert err <= GEMM_REL_TOL, (m, err)
+        assert_gemm_close(y, full_reference(x, qw, qz, s), (m))
 
 
 @pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
@@ -176,8 +173,22 @@ def test_full_qwen3_shapes_prefill_chunk_with_outliers(gpu_lib, shape):
     x = random_x_gpu(2048, k, seed=7, outliers=True)
     assert pkg().awq_regime(2048, k, n) == "tile"
     y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
-    err = rel_err(y, full_reference(x, qw, qz, s))
-    assert err <= GEMM_REL_TOL, err
+    assert_gemm_close(y, full_reference(x, qw, qz, s), "prefill")
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
+@pytest.mark.parametrize("m", [96, 128])
+def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
+    """M = 128 (the largest batched decode step of the 36-layer stack workload) and M = 96 at the
+    four full shapes, with activation outliers: the planner's mid-M plans (K split over
+    workgroups and waves) against the fp32 reference over the oracle-pinned dequant."""
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=15 + m)
+    packed = awq_mod().repack_awq_qweight(qw)
+    x = random_x_gpu(m, k, seed=m + 3, outliers=True)
+    print(f"full shape {shape} m={m} regime={pkg().awq_regime(m, k, n)} split={gpu_lib.split_k(m, k, n)}", flush=True)
+    y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
+    assert_gemm_close(y, full_reference(x, qw, qz, s), (shape, m))
 
 
 @pytest.mark.parametrize("shape,m", [("qkv", 768), ("o", 768), ("gate_up", 256), ("down", 384), ("down", 768),
@@ -192,8 +203,7 @@ def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     x = random_x_gpu(m, k, seed=m, outliers=True)
     assert pkg().awq_regime(m, k, n) == ("decode" if m <= 48 else "tile")
     y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
-    err = rel_err(y, full_reference(x, qw, qz, s))
-    assert err <= GEMM_REL_TOL, (shape, m, err)
+    assert_gemm_close(y, full_reference(x, qw, qz, s), (shape, m))
 
 
 @pytest.mark.parametrize("shape", ["gate_up", "down"])
@@ -203,7 +213,7 @@ def test_mixed_ragged_batch_m512(gpu_lib, shape):
     qw, qz, s = random_awq_gpu(k, n, seed=13)
     x = torch.cat([random_x_gpu(48, k, 1), random_x_gpu(32, k, 2), random_x_gpu(432, k, 3, outliers=True)])
     y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
-    assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+    assert_gemm_close(y, full_reference(x, qw, qz, s))
     # rows are independent: the 48 decode rows alone give the same values within rounding
     y48 = awq_mod().awq_linear(x[:48].contiguous(), awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
     assert rel_err(y48, y[:48].float()) <= GEMM_REL_TOL
@@ -217,7 +227,7 @@ def test_ragged_m(gpu_lib, m):
     y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
     assert y.shape == (m, n)
     if m:
-        assert rel_err(y, full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+        assert_gemm_close(y, full_reference(x, qw, qz, s))
 
 
 def test_leading_dims_are_flattened(gpu_lib):
@@ -226,7 +236,7 @@ def test_leading_dims_are_flattened(gpu_lib):
     x = random_x_gpu(6, k, seed=4).view(2, 3, k)
     y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
     assert y.shape == (2, 3, n)
-    assert rel_err(y.reshape(6, n), full_reference(x.reshape(6, k), qw, qz, s)) <= GEMM_REL_TOL
+    assert_gemm_close(y.reshape(6, n), full_reference(x.reshape(6, k), qw, qz, s))
 
 
 def test_too_small_workspace_is_an_error(gpu_lib):
@@ -282,7 +292,7 @@ def test_layer_forward_matches_oracle(gpu_lib):
         x_bits = ora.f32_to_bf16_bits(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))
         y = layer(bf16_from_bits(x_bits))
         want = ora.awq_linear_ref(x_bits, qweight, qzeros, s_bits, 128)
-        assert rel_err(y, want) <= GEMM_REL_TOL
+        assert_gemm_close(y, want)
 
 
 def test_row_parallel_layer_forward(gpu_lib):
@@ -301,7 +311,7 @@ def test_row_parallel_layer_forward(gpu_lib):
     layer.scales.weight_loader(layer.scales, s)
     layer.quant_method.process_weights_after_loading(layer)
     x = random_x_gpu(16, k, seed=3)
-    assert rel_err(layer(x), full_reference(x, qw, qz, s)) <= GEMM_REL_TOL
+    assert_gemm_close(layer(x), full_reference(x, qw, qz, s))
 
 
 def test_hip_graph_capture_replays_match_eager(gpu_lib):
@@ -346,7 +356,6 @@ def test_activations_beyond_2gib_run_in_row_chunks(gpu_lib):
     y = awq_mod().awq_linear(x, awq_mod().repack_awq_qweight(qw), qz, s, group_size=128)
     assert y.shape == (m, n)
     for lo, hi in ((0, 512), (fit - 1024, fit + 1024), (m - 512, m)):
-        err = rel_err(y[lo:hi], full_reference(x[lo:hi], qw, qz, s))
-        assert err <= GEMM_REL_TOL, (lo, hi, err)
+        assert_gemm_close(y[lo:hi], full_reference(x[lo:hi], qw, qz, s), (lo, hi))
     del x, y
     torch.cuda.empty_cache()

@@ -82,52 +82,3 @@ def test_checkpoint_to_forward_matches_oracle(gpu_lib, tmp_path):
             want = ora.awq_linear_ref(x_bits, s["qweight"], s["qzeros"], s["scales_bits"], 128)
             assert y.shape == want.shape
             assert rel_err(y, want) <= GEMM_REL_TOL, (name, m)
-
-
-def test_layer_projections_from_indexed_checkpoint(gpu_lib, tmp_path):
-    """benchmarks/awq_linear_profile.py:93-146 path: one layer read through the safetensors
-    index, merged q|k|v and gate|up, repacked on the GPU; each GEMM against the oracle; then
-    the benchmark's checkpoint leg over the same directory."""
-    import json
-    import sys
-
-    ckpt = importlib.import_module("llm-serve_amd.utils.checkpoint")
-    awq = importlib.import_module("llm-serve_amd.layers.quantization.awq")
-    hidden, q, kv, inter = 256, 256, 64, 512
-    sizes = {"q_proj": (hidden, q), "k_proj": (hidden, kv), "v_proj": (hidden, kv), "o_proj": (q, hidden),
-             "gate_proj": (hidden, inter), "up_proj": (hidden, inter), "down_proj": (inter, hidden)}
-    shards, files, weight_map = {}, ({}, {}), {}
-    for i, (comp, (k, n)) in enumerate(sizes.items()):
-        shards[comp] = shard(40 + i, k, n)
-        block = "self_attn" if comp in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
-        for name, t in to_tensors(f"model.layers.2.{block}.{comp}", shards[comp]).items():
-            files[i % 2][name] = t
-            weight_map[name] = f"part{i % 2}.safetensors"
-    for j, f in enumerate(files):
-        save_file(f, str(tmp_path / f"part{j}.safetensors"))
-    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
-
-    expected = {"qkv": concat(shards["q_proj"], shards["k_proj"], shards["v_proj"]), "o": shards["o_proj"],
-                "gate_up": concat(shards["gate_proj"], shards["up_proj"]), "down": shards["down_proj"]}
-    rng = np.random.default_rng(5)
-    for proj in ckpt.load_layer_projections(str(tmp_path), layer_id=2):
-        s = expected[proj.name]
-        assert np.array_equal(proj.qweight.numpy(), s["qweight"]) and np.array_equal(proj.qzeros.numpy(), s["qzeros"])
-        dev = proj.to("cuda")
-        packed = awq.repack_awq_qweight(dev.qweight)
-        for m in (4, 200):
-            x_bits = ora.f32_to_bf16_bits(rng.standard_normal((m, proj.input_size)).astype(np.float32))
-            print(f"projection {proj.name} m={m}", flush=True)
-            y = awq.awq_linear(bf16_from_bits(x_bits), packed, dev.qzeros, dev.scales, group_size=128)
-            want = ora.awq_linear_ref(x_bits, s["qweight"], s["qzeros"], s["scales_bits"], 128)
-            assert rel_err(y, want) <= GEMM_REL_TOL, (proj.name, m)
-
-    import os
-    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    if repo not in sys.path:
-        sys.path.insert(0, repo)
-    bench = importlib.import_module("bench")
-    out = bench.checkpoint_layer(gpu_lib, torch.device("cuda"), torch.cuda.Stream(), str(tmp_path), 2, reps=2)
-    assert out["layer_id"] == 2
-    assert [out["projections"][name]["N"] for name in ("qkv", "o", "gate_up", "down")] == [384, 256, 1024, 256]
-    assert all(out["projections"][name]["M=16"]["us"] > 0 for name in out["projections"])

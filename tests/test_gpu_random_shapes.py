@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from awq_helpers import GEMM_REL_TOL, awq_mod, pkg, random_awq_gpu, random_x_gpu, rel_err
+from awq_helpers import GEMM_REL_TOL, assert_gemm_close, awq_mod, pkg, random_awq_gpu, random_x_gpu, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +35,7 @@ def test_random_shapes_match_reference(gpu_lib, seed):
         y = awq.awq_linear(x, awq.repack_awq_qweight(qw), qz, s, group_size=128)
         want = x.float() @ awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
         assert y.shape == (m, n)
-        assert rel_err(y, want) <= GEMM_REL_TOL, (m, k, n)
+        assert_gemm_close(y, want, (m, k, n))
         if n % 128 == 0:  # the same weight as a gate|up pair: fused SiLU(gate) * up epilogue
             f = awq.awq_linear_silu_mul(x, awq.repack_awq_qweight(qw), qz, s, group_size=128)
             g, u = want[:, : n // 2], want[:, n // 2:]

@@ -148,10 +148,132 @@ def test_layer_api_with_rmsnorm_module(gpu_lib):
     assert y.shape == (2, 3, inter) and new_res.shape == (2, 3, k)
     assert torch.equal(y.view(torch.int16), gate_up.forward_silu_and_mul(xn).view(torch.int16))
     assert torch.equal(new_res.view(torch.int16), want_res.view(torch.int16))
-    y2, none = gate_up.forward_rmsnorm(norm, x)
-    assert none is None
+    y2, first_res = gate_up.forward_rmsnorm(norm, x)
+    assert first_res is x  # the first layer's residual is its input (qwen3.py:166-167)
     assert torch.equal(y2.view(torch.int16), gate_up(norm(x)).view(torch.int16))
     with pytest.raises(ValueError, match="weight must have shape"):
         awq.add_rms_norm(x, None, norm.weight[:-8], EPS)
     with pytest.raises(ValueError, match="residual must have"):
         norm(x, res[:1].contiguous())
+
+
+@pytest.mark.parametrize("tokens", [1, 7, 64])
+def test_head_norms_on_strided_qkv_views(gpu_lib, tokens):
+    """q_norm / k_norm (RMSNorm(head_dim)) on q.view(-1, heads, head_dim) and
+    k.view(-1, kv_heads, head_dim) of the split QKV output (qwen3.py:87-94): strided views,
+    normalised in place of the reference's copy; same bar as the contiguous rows, and
+    bit-identical to normalising a contiguous copy."""
+    layernorm = importlib.import_module("llm-serve_amd.layers.layernorm")
+    heads, kv_heads, head = 32, 8, 128
+    qkv_bits = rand_bits((tokens, (heads + 2 * kv_heads) * head), seed=tokens, scale=3.0)
+    qkv = bf16_from_bits(qkv_bits)
+    q, k, _ = qkv.split([heads * head, kv_heads * head, kv_heads * head], dim=-1)
+    with torch.device("cuda"):
+        q_norm, k_norm = layernorm.RMSNorm(head, eps=EPS), layernorm.RMSNorm(head, eps=EPS)
+    w_bits = rand_bits((head,), seed=1, scale=0.2, offset=1.0)
+    q_norm.weight.copy_(bf16_from_bits(w_bits))
+    k_norm.weight.copy_(bf16_from_bits(w_bits))
+    for view, norm, nh, off in ((q.view(-1, heads, head), q_norm, heads, 0),
+                                (k.view(-1, kv_heads, head), k_norm, kv_heads, heads * head)):
+        assert view.is_contiguous() == (tokens == 1)  # one token's heads are contiguous
+        out = norm(view)
+        assert out.shape == view.shape and out.is_contiguous()
+        rows = qkv_bits[:, off: off + nh * head].reshape(tokens * nh, head)
+        want, _, _ = ora.add_rms_norm_ref(rows, None, w_bits, EPS)
+        d = ulp_diff(bits_of(out).reshape(tokens * nh, head), want)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99, (d.max(), (d == 0).mean())
+        assert torch.equal(out.view(torch.int16), norm(view.contiguous()).view(torch.int16))
+    assert np.array_equal(bits_of(qkv), qkv_bits)  # the input is not modified
+
+
+def test_two_layer_step_from_no_residual_matches_oracle(gpu_lib):
+    """Two decoder layers in the reference's order (qwen3.py:163-178) starting with
+    residual=None: the first layer's residual is its input (qwen3.py:166-167), so the
+    post-attention norm adds it.  Every norm's new residual is bit-exact with the oracle
+    (add_rms_forward over the GPU's own inputs) and every projection within the GEMM
+    tolerance of the oracle's fp64 GEMM of the GPU's input to it."""
+    linear = importlib.import_module("llm-serve_amd.layers.linear")
+    layernorm = importlib.import_module("llm-serve_amd.layers.layernorm")
+    awq = awq_mod()
+    cfg = awq.AWQRuntimeConfig(bits=4, group_size=128, zero_point=True, version="gemm", backend="autoawq",
+                               activation_dtype=torch.bfloat16)
+    hidden, head, heads, kv_heads, inter = 1024, 128, 8, 2, 768
+    layers = []
+    for li in range(2):
+        with torch.device("cuda"):
+            mods = {"qkv": linear.QKVParallelLinear(hidden, head, heads, kv_heads, quant_config=cfg),
+                    "o": linear.RowParallelLinear(heads * head, hidden, quant_config=cfg),
+                    "gate_up": linear.MergedColumnParallelLinear(hidden, [inter, inter], quant_config=cfg),
+                    "down": linear.RowParallelLinear(inter, hidden, quant_config=cfg),
+                    "norm1": layernorm.RMSNorm(hidden, eps=EPS), "norm2": layernorm.RMSNorm(hidden, eps=EPS)}
+        host = {}
+        for i, name in enumerate(("qkv", "o", "gate_up", "down")):
+            lay = mods[name]
+            k, n = lay.qweight.shape[0], lay.scales.shape[1]
+            p = ora.make_problem(seed=500 + 10 * li + i, m=1, k=k, n=n, scale_lo=0.001, scale_hi=0.004)
+            host[name] = p
+            lay.qweight.data.copy_(torch.from_numpy(p["qweight"]))
+            lay.qzeros.data.copy_(torch.from_numpy(p["qzeros"]))
+            lay.scales.data.copy_(bf16_from_bits(p["scales_bits"]))
+            lay.quant_method.process_weights_after_loading(lay)
+        for j, name in enumerate(("norm1", "norm2")):
+            wb = rand_bits((hidden,), seed=60 + 2 * li + j, scale=0.1, offset=1.0)
+            host[name] = wb
+            mods[name].weight.copy_(bf16_from_bits(wb))
+        layers.append((mods, host))
+
+    def gemm_ref(x_bits, p):
+        return ora.awq_linear_ref(x_bits, p["qweight"], p["qzeros"], p["scales_bits"], 128)
+
+    m = 5
+    h = bf16_from_bits(rand_bits((m, hidden), seed=99))
+    res = None
+    for li, (mods, host) in enumerate(layers):
+        h_bits = bits_of(h)
+        res_bits = bits_of(res) if res is not None else None
+        qkv, res = mods["qkv"].forward_rmsnorm(mods["norm1"], h, res)
+        xn_bits, want_res, _ = ora.add_rms_norm_ref(h_bits, res_bits, host["norm1"], EPS)
+        if res_bits is None:
+            assert res is h  # the first layer's residual is its input
+        else:
+            assert np.array_equal(bits_of(res), want_res), li
+        assert rel_err(qkv, gemm_ref(xn_bits, host["qkv"])) <= GEMM_REL_TOL, ("qkv", li)
+        attn = qkv[:, : heads * head].contiguous()
+        a = mods["o"](attn)
+        assert rel_err(a, gemm_ref(bits_of(attn), host["o"])) <= GEMM_REL_TOL, ("o", li)
+        res_bits = bits_of(res)
+        x, res = mods["gate_up"].forward_rmsnorm_silu_and_mul(mods["norm2"], a, res)
+        xn2_bits, want_res2, _ = ora.add_rms_norm_ref(bits_of(a), res_bits, host["norm2"], EPS)
+        assert np.array_equal(bits_of(res), want_res2), ("post-attention residual", li)
+        gu = host["gate_up"]
+        want_x = ora.awq_gate_up_silu_mul_ref(xn2_bits, gu["qweight"], gu["qzeros"], gu["scales_bits"], 128,
+                                              round_intermediate=False)
+        assert rel_err(x, want_x) <= GEMM_REL_TOL, ("gate_up", li)
+        h = mods["down"](x)
+        assert rel_err(h, gemm_ref(bits_of(x), host["down"])) <= GEMM_REL_TOL, ("down", li)
+    assert torch.isfinite(h.float()).all()
+
+
+def test_workspace_reserved_at_load_and_never_grown_in_capture(gpu_lib, monkeypatch):
+    """process_weights_after_loading reserves the workspace for the configured largest M; a
+    request beyond the reserve while the stream captures a graph raises instead of
+    allocating."""
+    linear = importlib.import_module("llm-serve_amd.layers.linear")
+    awq = awq_mod()
+    cfg = awq.AWQRuntimeConfig(bits=4, group_size=128, zero_point=True, version="gemm", backend="autoawq",
+                               activation_dtype=torch.bfloat16, max_batched_tokens=1024)
+    k, n = QWEN3_SHAPES["down"]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.device("cuda"):
+            down = linear.RowParallelLinear(k, n, quant_config=cfg)
+        qw, qz, s = random_awq_gpu(k, n, seed=3)
+        for name, t in (("qweight", qw), ("qzeros", qz), ("scales", s)):
+            getattr(down, name).data.copy_(t)
+        down.quant_method.process_weights_after_loading(down)
+        have = awq.WORKSPACE.reserved_bytes(torch.device("cuda"))
+        assert have >= gpu_lib.workspace_bytes_max(1024, k, n) > 0
+        monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+        assert awq.WORKSPACE.get(torch.device("cuda"), have) is not None  # within the reserve: no allocation
+        with pytest.raises(RuntimeError, match="graph capture"):
+            awq.WORKSPACE.get(torch.device("cuda"), have + 1)

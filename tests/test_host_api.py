@@ -246,3 +246,40 @@ def test_rmsnorm_module_mirrors_the_reference_interface_and_has_no_cpu_path():
         awq.awq_linear_rmsnorm(x, None, norm.weight, 1e-5, torch.zeros(8, dtype=torch.int32),
                                torch.zeros(1, 8, dtype=torch.int32), torch.zeros(1, 64, dtype=torch.bfloat16),
                                group_size=128)
+
+
+def test_integration_stub_is_the_tested_file():
+    """INTEGRATION.md's binding stub is tests/reference_awq_hip.py byte for byte, so the code
+    a maintainer copies is the code tests/test_gpu_reference_binding.py runs."""
+    import os
+    import re
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    doc = open(os.path.join(repo, "INTEGRATION.md")).read()
+    m = re.search(r"<!-- stub: tests/reference_awq_hip.py -->\n```python\n(.*?)```\n", doc, flags=re.S)
+    assert m, "INTEGRATION.md has no stub block"
+    assert m.group(1) == open(os.path.join(repo, "tests", "reference_awq_hip.py")).read()
+
+
+def test_norm_row_strides_of_head_views(awq):
+    """Row layout of strided RMSNorm inputs: the per-head views of a split q|k|v output are
+    rows at two strides; contiguous leading dimensions merge; anything else is refused."""
+    qkv = torch.zeros(5, 6144, dtype=torch.bfloat16)
+    q, k, v = qkv.split([4096, 1024, 1024], dim=-1)
+    assert awq._row_strides(q.view(-1, 32, 128)) == (32, 6144, 128)
+    assert awq._row_strides(k.view(-1, 8, 128)) == (8, 6144, 128)
+    assert awq._row_strides(q[:1].view(-1, 32, 128)) == (32, 0, 128)
+    assert awq._row_strides(qkv.view(5, 48, 128)) == (240, 0, 128)      # contiguous: one stride
+    t = torch.zeros(2, 3, 4, 136, dtype=torch.bfloat16)[:, :, :, :128]
+    assert awq._row_strides(t) == (24, 0, 136)                          # padded rows: one stride
+    assert awq._row_strides(torch.zeros(2, 3, 4, 136, dtype=torch.bfloat16)[:, 1:, :, :128]) == (8, 1632, 136)
+    assert awq._row_strides(torch.zeros(4, 132, dtype=torch.bfloat16)[:, :128]) is None  # rows 8-byte aligned only
+    assert awq._row_strides(torch.zeros(4, 128, dtype=torch.bfloat16)[:, ::2]) is None  # inner stride 2
+    assert awq._row_strides(torch.zeros(2, 3, 5, 64, dtype=torch.bfloat16).permute(2, 0, 1, 3)) == (6, 64, 320)
+    assert awq._row_strides(torch.zeros(2, 3, 5, 64, dtype=torch.bfloat16).permute(0, 2, 1, 3)) is None  # 3 strides
+
+
+def test_runtime_config_reserves_for_the_engine_batch(awq):
+    cfg = awq.AWQRuntimeConfig(bits=4, group_size=128, zero_point=True, version="gemm", backend="autoawq",
+                               activation_dtype=torch.bfloat16)
+    assert cfg.max_batched_tokens == 16384  # the reference engine's max_num_batched_tokens (config.py:11)

@@ -153,91 +153,3 @@ def test_loader_unknown_checkpoint_name_is_an_error(mods, tmp_path):
     with pytest.raises(AttributeError):
         loader.load_model(qkv_model(linear, cfg), write(tmp_path, {"lm_head.weight": torch.zeros(2, 2)}),
                           process_weights=False)
-
-
-# ------------------------------------------------------- per-layer projection reader
-# Mirrors the reference's tests/test_awq_linear_profile.py:7-56 and the index contract of
-# benchmarks/awq_linear_profile.py:93-146.
-@pytest.fixture(scope="module")
-def ckpt(pkg):
-    return importlib.import_module("llm-serve_amd.utils.checkpoint")
-
-
-def test_merge_projection_tensors_uses_checkpoint_output_dimension(ckpt):
-    parts = [(torch.full((128, n // 8), v, dtype=torch.int32), torch.full((1, n // 8), v + 3, dtype=torch.int32),
-              torch.full((1, n), v + 6, dtype=torch.bfloat16)) for v, n in ((1, 16), (2, 8), (3, 8))]
-    proj = ckpt.merge_projection_tensors("qkv", parts)
-    assert proj.name == "qkv"
-    assert (proj.qweight.shape, proj.qzeros.shape, proj.scales.shape) == ((128, 4), (1, 4), (1, 32))
-    assert (proj.output_size, proj.input_size) == (32, 128)
-    assert torch.equal(proj.qweight[:, :2], torch.full((128, 2), 1, dtype=torch.int32))
-    assert torch.equal(proj.scales[:, -8:], torch.full((1, 8), 9, dtype=torch.bfloat16))
-    assert proj.payload_bytes == 128 * 4 * 4 + 4 * 4 + 32 * 2
-
-
-def test_merge_projection_tensors_rejects_incompatible_inputs(ckpt):
-    first = (torch.zeros((128, 1), dtype=torch.int32), torch.zeros((1, 1), dtype=torch.int32),
-             torch.ones((1, 8), dtype=torch.bfloat16))
-    second = (torch.zeros((256, 1), dtype=torch.int32), torch.zeros((2, 1), dtype=torch.int32),
-              torch.ones((2, 8), dtype=torch.bfloat16))
-    with pytest.raises(ValueError, match="input/group"):
-        ckpt.merge_projection_tensors("invalid", [first, second])
-    with pytest.raises(ValueError, match="at least one"):
-        ckpt.merge_projection_tensors("empty", [])
-    with pytest.raises(ValueError, match="qweight packed output"):
-        ckpt.merge_projection_tensors("bad", [(first[0], first[1], torch.ones((1, 16), dtype=torch.bfloat16))])
-
-
-LAYER_SIZES = {"q_proj": (128, 32), "k_proj": (128, 16), "v_proj": (128, 16), "o_proj": (32, 128),
-               "gate_proj": (128, 64), "up_proj": (128, 64), "down_proj": (64, 128)}
-
-
-def write_indexed_layer(tmp_path, layer_id, drop=None):
-    """A two-file checkpoint of one Qwen3 layer with its index; every tensor of component c
-    holds the value ``position of c + tensor offset`` so the merge order is visible."""
-    import json
-
-    files = ({}, {})
-    weight_map = {}
-    for i, (comp, (k, n)) in enumerate(LAYER_SIZES.items()):
-        block = "self_attn" if comp in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
-        prefix = f"model.layers.{layer_id}.{block}.{comp}"
-        for key, t in {"qweight": torch.full((k, n // 8), i, dtype=torch.int32),
-                       "qzeros": torch.full((k // 32, n // 8), 10 + i, dtype=torch.int32),
-                       "scales": torch.full((k // 32, n), 20 + i, dtype=torch.bfloat16)}.items():
-            name = f"{prefix}.{key}"
-            if name == drop:
-                continue
-            fname = f"model-0000{1 + i % 2}-of-00002.safetensors"
-            files[i % 2][name] = t
-            weight_map[name] = fname
-    files[0]["model.embed_tokens.weight"] = torch.zeros(4, 4)
-    weight_map["model.embed_tokens.weight"] = "model-00001-of-00002.safetensors"
-    for j, f in enumerate(files):
-        save_file(f, str(tmp_path / f"model-0000{1 + j}-of-00002.safetensors"))
-    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
-    return str(tmp_path)
-
-
-def test_load_layer_projections_merges_components_in_order(ckpt, tmp_path):
-    projs = ckpt.load_layer_projections(write_indexed_layer(tmp_path, 3), layer_id=3)
-    assert [p.name for p in projs] == ["qkv", "o", "gate_up", "down"]
-    qkv, o, gate_up, down = projs
-    assert qkv.qweight.shape == (128, 8) and qkv.output_size == 64 and qkv.input_size == 128
-    assert qkv.qweight[0].tolist() == [0] * 4 + [1] * 2 + [2] * 2
-    assert qkv.qzeros[0].tolist() == [10] * 4 + [11] * 2 + [12] * 2
-    assert gate_up.scales.shape == (4, 128)
-    assert gate_up.scales[0, :64].eq(24).all() and gate_up.scales[0, 64:].eq(25).all()
-    assert (o.input_size, o.output_size) == (32, 128)
-    assert (down.input_size, down.output_size) == (64, 128)
-    assert down.qweight.eq(6).all()
-
-
-def test_load_layer_projections_reports_missing_tensors(ckpt, tmp_path):
-    with pytest.raises(ValueError, match="index.json"):
-        ckpt.load_layer_projections(str(tmp_path), layer_id=0)
-    path = write_indexed_layer(tmp_path, 0, drop="model.layers.0.mlp.up_proj.scales")
-    with pytest.raises(ValueError, match=r"missing AWQ tensors: \['model.layers.0.mlp.up_proj.scales'\]"):
-        ckpt.load_layer_projections(path, layer_id=0)
-    with pytest.raises(ValueError, match="missing AWQ tensors"):
-        ckpt.load_layer_projections(path, layer_id=1)

@@ -448,3 +448,29 @@ def test_rms_norm_agrees_with_torch_fp32_within_one_ulp():
     wf = ora.bf16_bits_to_f32(w).astype(np.float64)
     wrong = ora.f32_to_bf16_bits((normed.astype(np.float32).astype(np.float64) * wf).astype(np.float32))
     assert (wrong != got).mean() > 0.05
+
+
+# ------------------------------------------------- torch CPU restatement (CPU baseline)
+def test_torch_cpu_backend_matches_the_numpy_oracle():
+    """oracle/awq_torch_cpu.py (the CPU baseline's subject) against the numpy oracle: unpack
+    and dequant bit-exact (including the KAT words and negative int32 words), the linear within
+    the bf16 GEMM tolerance of the fp64 oracle, and rows independent (the reference's
+    matmul over a batch equals its rows one by one, up to accumulation order)."""
+    import torch
+    from oracle import awq_torch_cpu as tref
+
+    words = np.array([[0x75316420, 0xFDB9ECA8 - 2 ** 32], [-1, 0]], dtype=np.int32)
+    assert np.array_equal(tref.unpack_int4(torch.from_numpy(words)).numpy(), ora.unpack_awq_int4(words))
+    assert tref.unpack_int4(torch.from_numpy(words[:1, :1])).tolist() == [list(range(8))]  # round-trip KAT row
+    for seed, (m, k, n) in enumerate(((3, 256, 64), (16, 512, 128))):
+        p = ora.make_problem(seed=40 + seed, m=m, k=k, n=n)
+        qw, qz = torch.from_numpy(p["qweight"]), torch.from_numpy(p["qzeros"])
+        s = torch.from_numpy(p["scales_bits"].view(np.int16)).view(torch.bfloat16)
+        x = torch.from_numpy(p["x_bits"].view(np.int16)).view(torch.bfloat16)
+        w = tref.dequantize(qw, qz, s, 128)
+        want_w = ora.dequantize_awq_gemm_bits(p["qweight"], p["qzeros"], p["scales_bits"], 128)
+        assert np.array_equal(w.view(torch.int16).numpy().view(np.uint16), want_w)
+        y = tref.linear(x, qw, qz, s, 128)
+        assert y.dtype == torch.bfloat16
+        want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
+        assert ora.gemm_rel_err(y.float().numpy(), want) <= 1e-2
