@@ -133,6 +133,20 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
                const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* w4a16_gemm for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation): no workspace argument; the split-K
+ * workspace is a 48 MiB device array of the library itself, one per GPU, held until the
+ * process ends, set up on the first call on each device (symbol lookup, its counters
+ * cleared by a kernel on `stream`).  Allocates nothing.  Problems whose plan needs more
+ * than 48 MiB of workspace (w4a16_workspace_bytes) are rejected with W4A16_ERR_WORKSPACE
+ * before anything is enqueued (every Qwen3-8B projection at M <= 16384 fits).  Calls that
+ * overlap on one GPU (two streams at once) share the array and race: serialize them.
+ * Arguments, limits and results otherwise as w4a16_gemm (same kernels, same bits).
+ * No counterpart in the reference: an allocation-free entry for the callers above. */
+int w4a16_gemm_noalloc(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                       const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
+                       void* stream);
+
 /* y[M, N] = bf16(bf16(x[M, K] @ W) + residual[M, N]): the GEMM with the residual add that
  * follows the O and down projections (the reference's add_rms_forward: x.float() +
  * residual.float() then bf16, layernorm.py:35-36) done in the epilogue.  residual may be y itself

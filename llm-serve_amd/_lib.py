@@ -34,6 +34,8 @@ _SIGNATURES = {
     "w4a16_workspace_bytes_max": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "w4a16_gemm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
                             _c_ptr, _c_size, _c_ptr]),
+    "w4a16_gemm_noalloc": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+                                    _c_ptr]),
     "w4a16_regime": (_c_int, [_c_int, _c_int, _c_int]),
     "w4a16_split_k": (_c_int, [_c_int, _c_int, _c_int]),
     "w4a16_gemm_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,

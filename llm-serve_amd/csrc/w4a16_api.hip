@@ -3,9 +3,15 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/w4a16.h"
 #include "w4a16_common.h"
 #include "w4a16_launch.h"
+
+// Split-K workspace of w4a16_gemm_noalloc (see scratch_for_current_device below).
+constexpr size_t kScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
@@ -287,9 +293,71 @@ int validate_norm(const void* x, const void* residual, const void* weight, float
   return ok();
 }
 
+// ---------------------------------------------------------------------------
+// Library-owned split-K workspace of w4a16_gemm_noalloc, for callers that cannot allocate
+// device memory.  `scratch` is a device array of the code object: each GPU the library
+// runs on holds its own copy, at its own address, until the process ends.  In host code the
+// name is only a stand-in for the symbol; its device address comes from hipGetSymbolAddress
+// on each device (with that device current) and is the only thing host code passes on.
+// Layout as any workspace: arrival counters in the first kCounterBytes, then fp32 partials.
+// The counters start at zero (cleared once per device on first use by a fill kernel on the
+// caller's stream) and every kernel re-arms the ones it used; calls that overlap on one GPU
+// share the array and race.
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices];  // per device; null until set up
+
+__global__ void clear_words(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Device address of the current device's scratch, set up on the first call on that device
+// (symbol lookup, then the counters cleared on `stream`).  Returns a W4A16 status.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return fail(W4A16_ERR_LAUNCH, "no current HIP device (or device index >= %d)", kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(W4A16_ERR_LAUNCH, "hipGetSymbolAddress of the library scratch failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    clear_words<<<16, 256, 0, stream>>>(static_cast<uint32_t*>(ptr), static_cast<int>(kCounterBytes / 4));
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess)
+      return fail(W4A16_ERR_LAUNCH, "clearing the library scratch failed on device %d: %s", dev, hipGetErrorString(le));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
+
+int w4a16_gemm_noalloc(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                       uint16_t* y, int M, int K, int N, int group_size, void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  const GemmPlan p = plan(M, K, N);
+  const size_t need = workspace_for(p, M, N);
+  if (need > kScratchBytes)
+    return fail(W4A16_ERR_WORKSPACE,
+                "M=%d K=%d N=%d needs %zu bytes of split-K workspace; w4a16_gemm_noalloc holds %zu (use w4a16_gemm "
+                "with a caller workspace)",
+                M, K, N, need, kScratchBytes);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int r = scratch_for_current_device(s, &ws);
+    if (r != W4A16_OK) return r;
+  }
+  return run_plan(p, x, packed, qzeros, scales, y, M, K, N, ws, need > 0 ? kScratchBytes : 0, s);
+}
 
 int w4a16_add_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
                       uint16_t* x_norm, uint16_t* residual_out, int M, int K, void* stream) {

@@ -275,3 +275,11 @@ def test_plan_errors_come_before_anything_is_enqueued(pkg):
     args = (p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0)
     assert fused(*args, p, need - 1, None) == 4 and "workspace" in L.last_error()
     assert fused(*args, p + 16, need, None) == 3 and "256-byte" in L.last_error()
+
+
+def test_noalloc_scratch_covers_every_planned_workspace(pkg):
+    """w4a16_gemm_noalloc's 48 MiB scratch holds the largest workspace the planner asks for at
+    the Qwen3-8B shapes for every M up to the engine's 16384 tokens."""
+    L = pkg.lib()
+    for k, n in ((4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)):
+        assert L.workspace_bytes_max(16384, k, n) <= 48 << 20, (k, n)
