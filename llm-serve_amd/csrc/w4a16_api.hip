@@ -109,46 +109,95 @@ GemmPlan plan_decode(int M, int K, int N) {
 }
 
 // Tile regime, chosen from sweeps of every tile configuration on MI355X over the Qwen3-8B
-// shapes at M = 128 .. 2048.  Two wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by
-// side along N (32 columns each), one workgroup per CU; shape 1 = 4 waves (64 columns each),
-// two workgroups per CU.
-//  * 128-row tiles in shape 3 (wm = 8: every dequantized weight serves 128 rows) when their
-//    grid fills the CUs in even rounds at M >= 1024 (gate_up, O and down at M = 2048), or
-//    fills 144 .. 256 of one round's workgroups once K is split in two or four with >= 16
-//    groups per split, for M > 128 (QKV and down at M = 384 .. 1024, O at M = 768 and 1024,
-//    gate_up at M = 256: up to 21 % faster than 64-row tiles there; at M <= 128 half-empty
-//    128-row tiles lose, e.g. 45 vs 33 us for gate_up at M = 64).
-//  * Otherwise 64-row tiles: at M >= 1024 in shape 1 (N = 6144 at M = 2048: 384 vs 768
-//    tiles); below, shape 1 when the grid is large (>= 512 tiles), else shape 3, with K
-//    split in powers of two while the grid stays within one round (shape 3: 256 workgroups;
-//    shape 1: 512) and every split keeps >= 8 groups.  Split-K partials are reduced by the
-//    last workgroup of each tile.
-GemmPlan plan_tile(int M, int K, int N) {
+// shapes at M = 32 .. 2048.  Wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by side
+// along N (32 columns each), one workgroup per CU; shape 1 = 4 waves (64 columns each), two
+// workgroups per CU; shapes 4 and 5 = 8 waves as 4 K slices x 2 along N (64 columns) or 2 K
+// slices x 4 along N (128 columns), the slices summed through LDS.
+//
+// Up to M = 256 (the mid range: speculative-verify and small mixed batches, the 36-layer
+// stack's batched decode steps) narrow column blocks with the K split over the waves of a
+// workgroup keep the grid at one round of 144 .. 256 workgroups with little or no split-K
+// exchange between workgroups; short rows blocks (32 rows) re-dequantize the weights per
+// row block but read each activation stage once per 64 columns:
+//  * wide layers (N >= 16384): 64-row tiles of 128 columns up to M = 64, then 128-row
+//    tiles of 128 columns, then (M > 128) of 256 columns, K not split;
+//  * long K (>= 8192): 32-row tiles up to M = 64 (64 columns up to M = 32, then 128),
+//    64 rows up to M = 128, 128 rows beyond, 128 columns, K split in four;
+//  * otherwise 32-row tiles of 64 columns up to M = 64 (up to M = 128 for N <= 4096), then
+//    64-row tiles (128 columns above M = 128 when N > 4096); K split in powers of two only
+//    until the grid has 144 workgroups, with >= 8 groups per split.
+// Measured against the best of every configuration at M = 32, 48, 64, 96, 128, 192, 256: within
+// 6 % at every point, 1.6 % in total (e.g. O M=128: 12.9 us, from 20.5 us with the 64-row
+// tiles of 256 columns used before; QKV M=64: 12.7 vs 16.1 us for the decode kernel).
+GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  auto tiles = [&](int wm) { return ceil_div(M, 16 * wm) * ceil_div(N, 256); };
-  const int t8 = tiles(8);
-  if (M >= 1024 && t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
-  int s8 = 1;
-  while (s8 < 4 && t8 * s8 * 2 <= 256 && 16 * s8 * 2 <= G) s8 *= 2;
-  if (M > 128 && t8 * s8 >= 144 && t8 * s8 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, s8};
-  if (M >= 1024) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
-  const int t = tiles(4);
-  const int shape = t >= 512 ? 1 : 3;
-  const int cap = shape == 1 ? 512 : 256;
-  int split = 1;
-  while (split < 8 && t * split * 2 <= cap && 8 * split * 2 <= G) split *= 2;
-  return GemmPlan{W4A16_REGIME_TILE, 4, 2, shape, split};
+  int wm, shape, split = 1;
+  if (N >= 16384) {
+    if (M <= 64) { wm = 4; shape = 5; }
+    else { wm = 8; shape = M <= 128 ? 5 : 3; }
+  } else if (K >= 8192) {
+    wm = M <= 64 ? 2 : M <= 128 ? 4 : 8;
+    shape = M <= 32 ? 4 : 5;
+  } else {
+    wm = (M <= 64 || (M <= 128 && N <= 4096)) ? 2 : 4;
+    shape = (M > 128 && N > 4096) ? 5 : 4;
+  }
+  const w4a16::TileShape ts = w4a16::tile_shape(shape);
+  const int tiles = ceil_div(M, 16 * wm * ts.nwm) * ceil_div(N, 16 * ts.tw * ts.nwn);
+  if (N < 16384)
+    while (tiles * split < 144 && G / (2 * split) >= 8) split *= 2;
+  return GemmPlan{W4A16_REGIME_TILE, wm, 2, shape, split};
 }
 
-// Regime: the decode kernel up to M = 64, except for wide layers (N >= 16384) above M = 48,
-// where the tile kernel with K split in two is faster (measured on the gate_up shape: the
-// decode kernel with 96-column workgroups takes 21.9 / 24.4 us at M = 33 / 48 against the
-// tile kernel's 26.7 / 27.2 us, but at M = 64 its best fitting configuration takes 43 us
-// against 28): with four 16-row activation blocks the 96-column workgroup no longer fits
-// the registers, and narrower ones re-read the activations too often.
+// 256 < M <= 1024 (chunked-prefill chunks and mixed batches), 128-row tiles unless they leave
+// too few workgroups: 256 columns (shape 3) when that grid alone has >= 144 workgroups (wide
+// layers only from M = 768), else 128 columns (shape 5, 2 K slices), K split in two or more
+// for long K while the grid is below 144 workgroups; short-K narrow layers switch to 64-row
+// tiles of 128 columns instead of splitting K.  From a sweep of every tile configuration at
+// M = 384, 512, 768, 1024: within 3.5 % of the best at every point, up to 10 % faster than the
+// 256-column tiles with K split used before (O M=512: 25.9 vs 28.8 us, gate_up M=512: 122 vs
+// 128 us).
+GemmPlan plan_large(int M, int K, int N) {
+  const int G = K / w4a16::kGroup;
+  const int t3 = ceil_div(M, 128) * ceil_div(N, 256);
+  if (t3 >= 144 && !(N >= 16384 && M <= 512)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+  const int t5 = ceil_div(M, 128) * ceil_div(N, 128);
+  if (t5 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 5, 1};
+  int split = 1;
+  if (K >= 8192) {
+    while (t5 * split < 144 && G / (2 * split) >= 16) split *= 2;
+    return GemmPlan{W4A16_REGIME_TILE, 8, 2, 5, split};
+  }
+  const int t4 = ceil_div(M, 64) * ceil_div(N, 128);
+  while (t4 * split < 144 && G / (2 * split) >= 8) split *= 2;
+  return GemmPlan{W4A16_REGIME_TILE, 4, 2, 5, split};
+}
+
+// Beyond M = 1024 (whole prefill chunks): 128-row tiles of 256 columns (shape 3: every
+// dequantized weight serves 128 rows) when their grid fills the CUs in even rounds (gate_up,
+// O and down at M = 2048), or fills 144 .. 256 of one round's workgroups once K is split in two
+// or four with >= 16 groups per split; otherwise 64-row tiles of 256 columns, two workgroups
+// per CU (shape 1; QKV at M = 2048: 384 vs 768 tiles).  Split-K partials are reduced by the
+// last workgroup of each tile.
+GemmPlan plan_tile(int M, int K, int N) {
+  if (M <= 256) return plan_mid(M, K, N);
+  if (M <= 1024) return plan_large(M, K, N);
+  const int G = K / w4a16::kGroup;
+  const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
+  if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+  int s8 = 1;
+  while (s8 < 4 && t8 * s8 * 2 <= 256 && 16 * s8 * 2 <= G) s8 *= 2;
+  if (t8 * s8 >= 144 && t8 * s8 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, s8};
+  return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
+}
+
+// Regime: the decode kernel up to M = 32, and up to M = 48 for wide layers (N >= 16384),
+// where it still beats the tile kernel (gate_up: 19.2 / 24.5 us at M = 32 / 48 against 27.5 /
+// 28.2 us); the tile kernel beyond (M = 48 on the narrow layers: QKV 12.5 vs 13.8 us, O 10.3
+// vs 12.6 us, down 18.6 vs 20.1 us).
 GemmPlan plan(int M, int K, int N) {
   if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
-  if (M > kDecodeMaxM || (M > 48 && N >= 16384)) return plan_tile(M, K, N);
+  if (M > (N >= 16384 ? 48 : 32)) return plan_tile(M, K, N);
   return plan_decode(M, K, N);
 }
 
@@ -580,8 +629,8 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
       return fail(W4A16_ERR_ARG, "decode configuration needs %d ring and accumulator registers per lane (limit 176)",
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
-    if (p0 != 4 && p0 != 6 && p0 != 8 && p0 != 16) return fail(W4A16_ERR_ARG, "tile wm must be 4, 6, 8 or 16");
-    if (p2 < 0 || p2 > 3) return fail(W4A16_ERR_ARG, "tile shape code must be 0..3");
+    if (p0 != 2 && p0 != 4 && p0 != 8) return fail(W4A16_ERR_ARG, "tile wm must be 2, 4 or 8");
+    if (p2 < 0 || p2 > 7) return fail(W4A16_ERR_ARG, "tile shape code must be 0..7");
     if (p1 != 1 && p1 != 2) return fail(W4A16_ERR_ARG, "tile occupancy must be 1 or 2");
     if (!w4a16::tile_config_compiled(p0, p2, p1))
       return fail(W4A16_ERR_ARG, "tile configuration wm %d, shape %d, occupancy %d is not compiled", p0, p2, p1);
@@ -616,7 +665,7 @@ size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split)
   // Tile regime: enough for every tile shape (taller or wider tiles pad more).
   size_t most = workspace_for(GemmPlan{regime, p0, 0, 1, split}, M, N);
   if (regime != W4A16_REGIME_TILE) return most;
-  for (int shape = 2; shape <= 3; ++shape) {
+  for (int shape = 2; shape <= 7; ++shape) {
     const size_t b = workspace_for(GemmPlan{regime, p0, 0, shape, split}, M, N);
     most = b > most ? b : most;
   }

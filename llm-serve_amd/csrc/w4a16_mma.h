@@ -1,0 +1,297 @@
+// Pieces of the LDS-staged GEMM kernel (tile_kernel): the raw loads of one 128-deep group of
+// a wave's weight tiles, the MFMA work of one group against an activation stage in LDS, the
+// workgroup-to-tile mapping and the output side (slice sum, split-K exchange, epilogue).
+//
+// Activation stage layout: BM rows x one 128-deep group, row-major (256 bytes per row), the
+// sixteen 16-byte chunks of row r stored at chunk position c ^ (r & 15): the 16 lanes reading
+// one fragment chunk (16 consecutive rows) then hit 16 different chunk positions, i.e. all
+// 64 LDS banks once.
+#pragma once
+
+#include <type_traits>
+
+#include "w4a16_common.h"
+
+namespace w4a16 {
+
+constexpr int kARowBytes = kGroup * 2;  // one activation row of a stage
+
+// Workgroup -> (K split, m-block, n-block).  XCD-major enumeration: consecutive blockIdx go
+// to different XCDs (round-robin), so undo that and give each XCD a contiguous run of
+// logical tiles.  Within a K split the logical tiles run in groups of kGroupM m-blocks: m
+// fastest inside a group, then n, so an XCD works on few m-blocks across many n-blocks at a
+// time -- their activation rows stay in its L2 while the weights stream past (instead of
+// every n-block re-fetching all rows).
+struct TileCoord {
+  int sidx, mbk, nbk;
+};
+
+__device__ __forceinline__ TileCoord tile_coord(int b, int m_blocks, int n_blocks, int split) {
+  constexpr int kGroupM = 4;
+  const int total = m_blocks * n_blocks * split;
+  const int per = total >> 3, rem = total & 7, xcd = b & 7, idx = b >> 3;
+  const int L = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  const int tiles = m_blocks * n_blocks;
+  const int sidx = L / tiles;
+  const int Lt = L - sidx * tiles;
+  const int grp = Lt / (kGroupM * n_blocks);
+  const int in_grp = Lt - grp * (kGroupM * n_blocks);
+  const int gm = m_blocks - grp * kGroupM < kGroupM ? m_blocks - grp * kGroupM : kGroupM;
+  return TileCoord{sidx, grp * kGroupM + in_grp % gm, in_grp / gm};
+}
+
+// Raw loads of one group for a wave's TW layout tiles: one 16-byte weight load per tile,
+// and the scale-pair and zero words of the lane's column in each tile.  Decoding waits
+// until the group is consumed.  An invalid group (past the K range, or a wave whose columns
+// lie past N) fetches nothing.
+template <int TW>
+struct BGroup {
+  u32x4_t w[TW];
+  uint32_t s[TW];   // bf16 scale pair holding the lane's column
+  uint32_t zw[TW];  // AutoAWQ zero word holding the lane's column
+};
+
+struct BSources {
+  __amdgpu_buffer_rsrc_t w, s, z;
+};
+
+// The wave's tiles are t0 + tt, plus dt for tt >= TW / 2 (dt = 0 for the plain GEMM; for
+// the fused gate/up product the second half are the up tiles of the first half's gate tiles).
+template <int TW>
+__device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src, int g, bool valid, int N, int t0,
+                                             int dt, int lane) {
+  const int NT = N / kTileCols;
+  const int c = lane & 15;
+  const uint32_t oob = valid ? 0u : kOutOfRange;
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt) {
+    const int t = t0 + tt + (tt >= TW / 2 ? dt : 0);
+    const uint32_t wo = valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : kOutOfRange;
+    b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
+    const int col = kTileCols * t + c;
+    b.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
+    b.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u),
+                                                    0, 0);
+  }
+}
+
+// One 128-deep group: per 32-row step, the matrix-core dequant of the wave's TW weight
+// tiles (2 TW scaling MFMAs), then WM x TW main MFMAs against the wave's 16 WM rows of the
+// LDS activation tile (`stage` points at the first of them).  Software-pipelined: step
+// j + 1's fragments are read and its weights dequantized while step j's main MFMAs run, so
+// the VALU dequant of one step can hide under the matrix work of the previous one.  The
+// order within a step is left to the compiler: explicit scheduling groups (one main MFMA,
+// then two VALU and one LDS read) measured 1.3-2.5 % slower on MI355X at M = 512 and 2048.
+template <int WM, int TW>
+__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const BGroup<TW>& b,
+                                          const NibbleConsts& nib, int lane) {
+  const int arow = lane & 15;
+  const int zshift = awq_shift(lane & 7);
+  TileScale ts[TW];
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt) ts[tt] = make_tile_scale(b.s[tt], (b.zw[tt] >> zshift) & 0xFu, lane);
+  auto read_a = [&](bf16x8_t (&a)[WM], int j) {
+    const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 15);  // row & 15 == lane & 15
+    const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt) a[mt] = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
+  };
+  auto dequant = [&](bf16x8_t (&bf)[TW], int j) {
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
+  };
+  if constexpr (WM * TW > 16) {
+    // Large wave tiles: no register double-buffering (the accumulators fill the AGPRs);
+    // the WM x TW independent MFMAs of a step leave the scheduler enough work to overlap.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8_t a[WM];
+      bf16x8_t bf[TW];
+      read_a(a, j);
+      dequant(bf, j);
+#pragma unroll
+      for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[mt], bf[tt], acc[mt][tt]);
+    }
+    return;
+  }
+  bf16x8_t a[2][WM];
+  bf16x8_t bf[2][TW];
+  read_a(a[0], 0);
+  dequant(bf[0], 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = j & 1;
+    if (j < 3) {
+      read_a(a[c ^ 1], j + 1);
+      dequant(bf[c ^ 1], j + 1);
+    }
+    // 128-row waves raise their issue priority while they issue the step's main MFMAs, so
+    // that the SIMD's other wave (in its dequant or LDS reads) does not starve the matrix
+    // pipe: measured on MI355X 2-3 % faster at M = 2048 (gate_up, down, O), while the
+    // 64-row configurations ran 3-4 % slower with it.
+    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[c][mt], bf[c][tt], acc[mt][tt]);
+    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(0);
+  }
+}
+
+// The output side of a tile workgroup.
+struct TileOut {
+  uint16_t* y;
+  const uint16_t* res;  // residual added in the epilogue (may be y), or null
+  float* partials;      // split-K fp32 fragments
+  int* counters;        // split-K arrival counters, one per output tile
+  int M, N, n_out, split, sidx, tile, ntiles;
+  int row_w;            // first output row of the wave
+  int col_w;            // first output column of the wave
+  bool act;             // fused SiLU(gate) * up: y is [M, N / 2]
+  bool active;          // the wave has output columns (col_w < n_out)
+};
+
+// After the K loop: the sum of the workgroup's K slices (WK > 1), the split-K exchange
+// between workgroups (split > 1) and the epilogue.  stage(i), i < S, is LDS region i of
+// kStage bytes; all of them are free here.  Every wave of the workgroup calls this (the
+// barriers count them all); only slice 0 holds results afterwards.
+template <int WM, int TW, int NWG, int WK, int S, int kStage, class StageFn>
+__device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stage, int* is_last_lds,
+                                            const TileOut& o, int wave_in, int wk, int lane) {
+  if constexpr (WK > 1) {
+    // Sum the slices' tiles in slice order: slices 1 .. WK - 1 park theirs in the stages
+    // (lane-major fragments, 1 KiB each), slice 0 adds them to its own.
+    constexpr int kFragsW = WM * TW;
+    constexpr int kPerStage = kStage / 1024;  // 1 KiB fragments per stage
+    static_assert((WK - 1) * NWG * kFragsW <= S * kPerStage, "slice tiles exceed the stages");
+    auto park = [&](int k2, int f) {  // fragment f of wave wave_in of slice k2 >= 1
+      const int fi = ((k2 - 1) * NWG + wave_in) * kFragsW + f;
+      return reinterpret_cast<f32x4_t*>(stage(fi / kPerStage)) + (fi % kPerStage) * 64 + lane;
+    };
+    if (wk > 0) {
+#pragma unroll
+      for (int f = 0; f < kFragsW; ++f) *park(wk, f) = acc[f / TW][f % TW];
+    }
+    __syncthreads();
+    if (wk == 0) {
+      for (int k2 = 1; k2 < WK; ++k2)
+#pragma unroll
+        for (int f = 0; f < kFragsW; ++f) acc[f / TW][f % TW] += *park(k2, f);
+    }
+    __syncthreads();
+  }
+
+  if (o.split > 1) {
+    // Every workgroup stores its fp32 fragments (lane-major, 1 KiB per 16 x 16 MFMA tile)
+    // into partials[sidx][tile][wave of slice 0]; the last to arrive sums all splits in
+    // split order, KC fragments at a time so that the loads of a chunk share one wait.  Only
+    // slice 0 holds results; the other slices take part in the barriers alone.
+    const int ntiles = o.ntiles;
+    const int tile = o.tile;
+    const int split = o.split, sidx = o.sidx;
+    float* partials = o.partials;
+    int* counters = o.counters;
+    constexpr int kFrags = WM * TW;
+    constexpr int KC = kFrags % 8 == 0 ? 8 : 4;
+    static_assert(kFrags % KC == 0, "fragments must split into chunks");
+    const __amdgpu_buffer_rsrc_t rp =
+        make_buffer(partials, static_cast<uint32_t>(split) * ntiles * NWG * kFrags * 1024u);
+    const uint32_t lane_off = static_cast<uint32_t>(lane) * 16u;
+    auto frag_off = [&](int sp, int f) {
+      return (((static_cast<uint32_t>(sp) * ntiles + tile) * NWG + wave_in) * kFrags + f) * 1024u + lane_off;
+    };
+    if (wk == 0) {
+#pragma unroll
+      for (int f = 0; f < kFrags; ++f) store_fragment(rp, frag_off(sidx, f), acc[f / TW][f % TW]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) *is_last_lds = (arrive(&counters[tile]) == split - 1);
+    __syncthreads();
+    if (!*is_last_lds || wk != 0) return;
+#pragma unroll
+    for (int c = 0; c < kFrags; c += KC) {
+      f32x4_t tot[KC];
+#pragma unroll
+      for (int f = 0; f < KC; ++f) tot[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < split; ++sp) {
+        if (sp == sidx) {
+#pragma unroll
+          for (int f = 0; f < KC; ++f) tot[f] += acc[(c + f) / TW][(c + f) % TW];
+        } else {
+          f32x4_t part[KC];
+#pragma unroll
+          for (int f = 0; f < KC; ++f) part[f] = load_fragment(rp, frag_off(sp, c + f));
+#pragma unroll
+          for (int f = 0; f < KC; ++f) tot[f] += part[f];
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < KC; ++f) acc[(c + f) / TW][(c + f) % TW] = tot[f];
+    }
+    if (threadIdx.x == 0) rearm(&counters[tile]);
+  }
+
+  if (!o.active || wk != 0) return;
+  // Epilogue (slice 0): bf16 through LDS (row-major 16 WM rows x the wave's output columns:
+  // rows of CPR 16-byte chunks swizzled by row), then 16-byte coalesced stores.  The stages
+  // are free after the last barrier.
+  constexpr int WR = 16 * WM;  // rows of a wave
+  constexpr int kStageRows = kStage / (WR * 32 * TW);
+  static_assert(kStageRows >= 1 && kStageRows * S >= NWG, "epilogue staging exceeds the stages");
+  uint8_t* ep = stage(wave_in / kStageRows) + (wave_in % kStageRows) * (WR * 32 * TW);
+  auto store_rows = [&](auto cpr_tag) {
+    constexpr int CPR = decltype(cpr_tag)::value;
+    constexpr int PITCH = 16 * CPR;
+    constexpr int kRowsPerRound = 64 / CPR;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+    for (int round = 0; round < WR / kRowsPerRound; ++round) {
+      const int r = kRowsPerRound * round + lane / CPR;
+      const int q = lane % CPR;
+      const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + ((q ^ (r % CPR)) << 4));
+      const int row = o.row_w + r;
+      if (row < o.M) {
+        const size_t off = static_cast<size_t>(row) * o.n_out + o.col_w + 8 * q;
+        *reinterpret_cast<uint4*>(o.y + off) = o.res ? add_bf16x8(v, *reinterpret_cast<const uint4*>(o.res + off)) : v;
+      }
+    }
+  };
+  if (!o.act) {
+    constexpr int CPR = 2 * TW;  // 16-byte chunks per row
+    constexpr int PITCH = 16 * CPR;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * mt + 4 * (lane >> 4) + i;
+          const int c = 16 * tt + (lane & 15);
+          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][tt][i]);
+        }
+    store_rows(std::integral_constant<int, CPR>{});
+  } else {
+    constexpr int H = TW / 2;
+    constexpr int CPR = TW;  // half the columns
+    constexpr int PITCH = 16 * CPR;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < H; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * mt + 4 * (lane >> 4) + i;
+          const int c = 16 * tt + (lane & 15);
+          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul(acc[mt][tt][i], acc[mt][tt + H][i]));
+        }
+    store_rows(std::integral_constant<int, CPR>{});
+  }
+}
+
+}  // namespace w4a16

@@ -87,9 +87,9 @@ def test_regime_boundary_and_split_limits(pkg):
     L = pkg.lib()
     for k, n in QWEN3.values():
         assert L.regime(0, k, n) == 0
-        for m in (1, 4, 8, 16, 32, 64):
-            # decode kernel up to M = 64, except wide layers above M = 48 (tile kernel)
-            assert L.regime(m, k, n) == (2 if m > 48 and n >= 16384 else 1)
+        for m in (1, 4, 8, 16, 32, 33, 48, 49, 64):
+            # decode kernel up to M = 32, and up to M = 48 on wide layers (tile kernel beyond)
+            assert L.regime(m, k, n) == (1 if m <= (48 if n >= 16384 else 32) else 2)
             assert 1 <= L.split_k(m, k, n) <= k // 128
         for m in (65, 128, 512, 2048, 4096):
             assert L.regime(m, k, n) == 2
@@ -129,9 +129,9 @@ def test_forced_config_validation(pkg):
     assert "registers" in L.last_error()
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 1, 2, 1, None, 0, None) == 1  # bad wm
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 3, 2, 1, None, 0, None) == 1  # bad occupancy
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 16, 2, 2, 1, None, 0, None) == 1  # wm 16 is not compiled
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 2, 2, 3, 1, None, 0, None) == 1  # wm 2 x shape 3: not compiled
     assert "not compiled" in L.last_error()
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 7, 1, None, 0, None) == 1  # bad tile shape code
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 8, 1, None, 0, None) == 1  # bad tile shape code
     assert "shape" in L.last_error()
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 2, 1, None, 0, None) == 1  # bad regime
     # split > 1 without workspace

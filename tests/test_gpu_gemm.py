@@ -99,7 +99,8 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 
 
 # (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
-TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2)]
+TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
+                (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1)]
 TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3, 4)]
 
 
@@ -159,7 +160,7 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
     qw, qz, s = random_awq_gpu(k, n, seed=11)
     packed = awq_mod().repack_awq_qweight(qw)
     for m in (1, 4, 8, 16, 32, 64):
-        assert pkg().awq_regime(m, k, n) == ("tile" if m > 48 and n >= 16384 else "decode")
+        assert pkg().awq_regime(m, k, n) == ("decode" if m <= (48 if n >= 16384 else 32) else "tile")
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
         assert_gemm_close(y, full_reference(x, qw, qz, s), (m))
@@ -192,16 +193,18 @@ def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
 
 
 @pytest.mark.parametrize("shape,m", [("qkv", 768), ("o", 768), ("gate_up", 256), ("down", 384), ("down", 768),
-                                     ("gate_up", 48), ("gate_up", 49)])
+                                     ("gate_up", 48), ("gate_up", 49), ("o", 32), ("o", 33), ("qkv", 33),
+                                     ("down", 33), ("down", 257), ("qkv", 257)])
 def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
-    (QKV / O / down at M = 768, gate_up at 256, down at 384) and the decode / tile boundary
-    of the wide layer (gate_up: decode up to M = 48, tiles from 49), at full shapes."""
+    (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundaries
+    (decode up to M = 32, up to 48 on the wide layer) and the end of the mid-range plans
+    (M = 257), at full shapes."""
     k, n = QWEN3_SHAPES[shape]
     qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
     packed = awq_mod().repack_awq_qweight(qw)
     x = random_x_gpu(m, k, seed=m, outliers=True)
-    assert pkg().awq_regime(m, k, n) == ("decode" if m <= 48 else "tile")
+    assert pkg().awq_regime(m, k, n) == ("decode" if m <= (48 if n >= 16384 else 32) else "tile")
     y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
     assert_gemm_close(y, full_reference(x, qw, qz, s), (shape, m))
 
