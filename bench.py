@@ -58,8 +58,9 @@ Also reported (not part of `value`):
     read + packed output written);
   * stack36_normed: stack36_chained's weights with both RMSNorms of each layer, the
     residual add in the norm prologue (the reference's order): w4a16_gemm_rmsnorm for
-    input_layernorm + QKV and post_attention_layernorm + gate|up + SiLU * up, plain O and
-    down -- 144 GEMM and 72 norm launches per step, one graph;
+    input_layernorm + QKV and post_attention_layernorm + gate|up + SiLU * up (the residual
+    alternating between two buffers), plain O and down -- 144 GEMM launches per step, plus 72
+    norm launches where M > 2 (at M <= 2 the norm runs inside the decode kernel), one graph;
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
     in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
 
@@ -391,6 +392,7 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
     for m in STACK_M:
         h = torch.randn((m, kq), device=dev).to(torch.bfloat16)
         res = torch.randn((m, kq), device=dev).to(torch.bfloat16)
+        res2 = torch.empty_like(res)  # the new residual goes to the other buffer (no in-place update)
         xn = torch.empty((m, kq), dtype=torch.bfloat16, device=dev)
         nw = (1 + 0.1 * torch.randn(kq, device=dev)).to(torch.bfloat16)
         qkv = torch.empty((m, nq), dtype=torch.bfloat16, device=dev)
@@ -400,10 +402,10 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
         ws = torch.zeros(max(ws_len, 256), dtype=torch.uint8, device=dev)
         wsp = ws.data_ptr() if ws_len else None
 
-        def normed(w, y, k, n, silu, sp):
+        def normed(w, y, k, n, silu, r_in, r_out, sp):
             packed, qzeros, scales = w
-            if lib.dll.w4a16_gemm_rmsnorm(h.data_ptr(), res.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
-                                          res.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+            if lib.dll.w4a16_gemm_rmsnorm(h.data_ptr(), r_in.data_ptr(), nw.data_ptr(), 1e-6, xn.data_ptr(),
+                                          r_out.data_ptr(), packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
                                           y.data_ptr(), m, k, n, 128, silu, wsp, ws_len, sp) != 0:
                 raise RuntimeError(lib.last_error())
 
@@ -416,10 +418,10 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
         def step():
             sp = torch.cuda.current_stream(dev).cuda_stream
             for layer in layers:
-                normed(layer["qkv"], qkv, kq, nq, 0, sp)
+                normed(layer["qkv"], qkv, kq, nq, 0, res, res2, sp)
                 attn.copy_(qkv[:, :kq])
                 plain(attn, layer["o"], *SHAPES["o"], sp)
-                normed(layer["gate_up"], act, ki, ni, 1, sp)
+                normed(layer["gate_up"], act, ki, ni, 1, res2, res, sp)
                 plain(act, layer["down"], *SHAPES["down"], sp)
 
         ms = time_graph(step, stream, reps)

@@ -65,22 +65,23 @@ int tile_bn(const GemmPlan& p) {
 // wave, split = K splits).  The activation traffic per weight byte falls as tn grows (each
 // workgroup reads its K range of x once), the grid shrinks with it, and the exchange of
 // split-K partials costs an extra pass over M x N fp32:
-//  * wide layers (N >= 16384): 32-column workgroups at M = 1 (768 for gate_up), 48 up to
-//    M = 8, 96 beyond (fewer, wider workgroups once x is 16 rows), one group in flight per
-//    wave at M > 32 (the registers then hold three 16-row activation blocks);
+//  * wide layers (N >= 16384): 32-column workgroups up to M = 2 (768 for gate_up), 48 up
+//    to M = 8, 96 beyond (fewer, wider workgroups: every wave repeats the kernel's scalar
+//    set-up, so the grid's wave count is a fixed cost), one group in flight per wave at
+//    M > 32 (the registers then hold three 16-row activation blocks);
 //  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 16, then 48 with K
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
 //    N = 4096), then 64 columns with K in four;
-//  * narrow layers with long K: 16 columns up to M = 4, then wider ones with K split in two
-//    or four.
+//  * narrow layers with long K: 16 columns at M = 1, 32 with K in two or four up to M = 8,
+//    then 64 columns with K in four.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
   const int T = N / 16;
   int tn = 2, waves = 8, depth = 2, split = 1;
   if (N >= 16384) {
-    if (M <= 1) tn = 2;
+    if (M <= 2) tn = 2;
     else if (M <= 8) tn = 3;
     else if (M <= 32) tn = 6;
     else { tn = 6; depth = 1; }
@@ -93,7 +94,8 @@ GemmPlan plan_decode(int M, int K, int N) {
     else { tn = 4; depth = 1; split = 4; }
   } else {
     if (M <= 1) { tn = 1; depth = 4; }
-    else if (M <= 4) tn = 1;
+    else if (M <= 2) { tn = 2; split = 2; }
+    else if (M <= 4) { tn = 2; split = 4; }
     else if (M <= 8) { tn = 2; split = 2; }
     else { tn = 4; depth = 1; split = 4; if (M > 32) waves = 4; }
   }
@@ -202,9 +204,9 @@ GemmPlan plan(int M, int K, int N) {
 }
 
 // The fused SiLU(gate) * up product of a gate|up weight [K, N] runs the plain GEMM's plan,
-// except that a decode workgroup must hold whole gate/up tile pairs: an odd tile count
-// becomes the next even one that divides N / 16 and fits the registers (the LDS check may
-// then split K further).
+// except that a decode workgroup must hold whole gate/up tile pairs: an odd tile count tn
+// becomes 2 tn (measured best for tn = 3 at M = 3..8), or the largest even count below
+// that divides N / 16 and fits the registers (the LDS check may then split K further).
 GemmPlan plan_silu_mul(int M, int K, int N) {
   GemmPlan p = plan(M, K, N);
   if (p.regime != W4A16_REGIME_DECODE || p.p0 % 2 == 0) return p;
@@ -212,7 +214,7 @@ GemmPlan plan_silu_mul(int M, int K, int N) {
   const int MB = (M + 15) / 16;
   const int T = N / 16;
   const bool xl = w4a16::decode_stages_x(M, K, p.split);
-  int tn = p.p0 == 1 ? 2 : 4;
+  int tn = 2 * p.p0;
   while (tn > 2 && (T % tn != 0 || !w4a16::decode_config_fits(MB, tn, 1, xl))) tn -= 2;
   while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
   p.p0 = tn;
@@ -289,9 +291,11 @@ int check_plan(const GemmPlan& p, int M, int K, int N, const void* workspace, si
 
 // up_tiles: 0 for the plain GEMM, N / 32 for the fused SiLU(gate) * up (y is [M, N / 2]).
 // res: null, or a bf16 [M, N] residual added in the epilogue (plain GEMM; may be y).
+// norm: the decode kernel's RMSNorm prologue (decode regime with staged rows only), or null.
 int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
              const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
-             hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr) {
+             hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr,
+             const w4a16::DecodeNorm* norm = nullptr) {
   if (p.regime == W4A16_REGIME_NONE) return ok();
   const int c = check_plan(p, M, K, N, workspace, workspace_bytes);
   if (c != W4A16_OK) return c;
@@ -302,7 +306,7 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
   if (p.regime == W4A16_REGIME_DECODE)
     return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, res, partials, counters, M, K, N, p.p0,
-                                                 p.p2, p.p1, p.split, up_tiles, stream),
+                                                 p.p2, p.p1, p.split, up_tiles, norm, stream),
                         "decode");
   // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
   // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
@@ -450,11 +454,27 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
   v = check_plan(p, M, K, N, workspace, workspace_bytes);
   if (v != W4A16_OK) return v;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int up_tiles = silu_mul ? N / 32 : 0;
+  // A decode plan with M <= 2 rows staged in LDS, no K split and at most 4 groups per wave
+  // (M = 1, 2 at the Qwen3-8B QKV and gate|up shapes) takes the norm as a prologue of the
+  // GEMM kernel: one launch, and x_norm is written once by the first workgroup, never read
+  // back.  Its outputs must not alias the inputs (other workgroups still read x and
+  // residual while the first one writes).
+  const bool distinct = x_norm != x && x_norm != residual && (residual_out == nullptr ||
+                                                               (residual_out != x && residual_out != residual));
+  if (p.regime == W4A16_REGIME_DECODE && distinct) {
+    const size_t lds = w4a16::decode_norm_lds_bytes(M, K, p.p0, p.p1, p.p2, p.split);
+    if (lds > 0 && lds <= w4a16::kDecodeMaxLds) {
+      const w4a16::DecodeNorm nrm{residual, norm_weight, residual_out, x_norm, eps};
+      return run_plan(p, x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s, up_tiles, nullptr,
+                      &nrm);
+    }
+  }
+  // Otherwise the norm kernel writes x_norm and the GEMM reads it back (from L2 at decode sizes).
   v = check_launch(w4a16::launch_add_rmsnorm(x, residual, norm_weight, x_norm, residual_out, M, K, eps, s),
                    "add_rmsnorm");
   if (v != W4A16_OK) return v;
-  return run_plan(p, x_norm, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s,
-                  silu_mul ? N / 32 : 0);
+  return run_plan(p, x_norm, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s, up_tiles);
 }
 
 int w4a16_abi_version(void) { return W4A16_ABI_VERSION; }

@@ -23,6 +23,18 @@
 // vector-memory instructions are then the TN weight loads per group (plus the activation
 // fragments when they are not staged).  The slices are private, so no barrier delays the
 // start of the stream: a wave waits only for its own loads.
+//
+// RMSNorm prologue (NR = M <= 2 rows, with staged activations and no K split): each lane
+// loads its share of the wave's activation rows, residual rows and norm-weight slices into
+// registers before the ring's weight loads are issued, and the norm runs while those are in
+// flight: per-row sums of squares of s = x + res, exchanged between the waves through LDS
+// (one barrier that waits for LDS only, summed in wave order), then x_norm = bf16(bf16(s *
+// rstd) * w) is written into the wave's activation slice in the staged layout; the first
+// workgroup also writes the new residual and the normalized rows.  The row statistic needs
+// the whole row, which a workgroup without a K split reads anyway, so the norm costs no
+// kernel launch and no round trip of x_norm -- but every workgroup repeats it, on its
+// critical path: measured on MI355X it adds 1.4 - 1.9 us to the Qwen3-8B QKV / gate|up
+// GEMMs at M = 1, against about 3 us for the separate norm kernel.
 #include <atomic>
 
 #include "w4a16_common.h"
@@ -43,6 +55,7 @@ struct DecodeArgs {
   int* counters;
   int M, K, N, split;
   int up_tiles;  // 0: plain GEMM; else fused SiLU(gate) * up with up tiles this far past gate
+  DecodeNorm norm;  // used by the NORM kernels only
 };
 
 // LDS layout of the staged operands.  A wave owns at most `items` groups (its groups
@@ -75,6 +88,39 @@ __host__ __device__ inline DecodeLds decode_lds_layout(int M, int K, int tn, int
   l.reduce = static_cast<uint32_t>(waves) * ((M + 15) / 16) * tn * 1024u;
   l.total = l.staged > l.reduce ? l.staged : l.reduce;
   return l;
+}
+
+// Launch constants, the same for every wave, computed once on the host: the LDS layout,
+// the buffer sizes, the K split's group ranges and a multiplier for dividing by M.  (Every
+// wave runs its own copy of whatever scalar set-up the kernel does, and the scalar unit is
+// shared by the waves of a CU: at decode sizes, with 8 - 24 waves per CU, the divisions
+// and layout arithmetic this replaces kept the weight stream from starting for 1 - 3 us.)
+struct DecodeGeom {
+  uint32_t z_off, x_off, c_off, d_off, wave_bytes;  // LDS layout (s_off = 0)
+  uint32_t x_bytes, w_bytes, s_bytes, z_bytes;      // buffer sizes
+  int G;                                            // 128-row groups of K
+  int gq, gr;      // split s covers gq groups (gq + 1 for s < gr), starting at s gq + min(s, gr)
+  uint32_t m_mul;  // ceil(2^16 / M): v / M == (v * m_mul) >> 16 for 0 <= v < 2^12
+};
+
+inline DecodeGeom decode_geom(int M, int K, int N, int tn, int waves, int split, bool xl, bool pre) {
+  const DecodeLds l = decode_lds_layout(M, K, tn, waves, split, xl, pre);
+  const int G = K / kGroup;
+  DecodeGeom g{};
+  g.z_off = l.z_off;
+  g.x_off = l.x_off;
+  g.c_off = l.c_off;
+  g.d_off = l.d_off;
+  g.wave_bytes = l.wave_bytes;
+  g.x_bytes = static_cast<uint32_t>(M) * K * 2u;
+  g.w_bytes = static_cast<uint32_t>(K) * (N / 2);
+  g.s_bytes = static_cast<uint32_t>(G) * N * 2u;
+  g.z_bytes = static_cast<uint32_t>(G) * (N / 8) * 4u;
+  g.G = G;
+  g.gq = G / split;
+  g.gr = G % split;
+  g.m_mul = (65536u + static_cast<uint32_t>(M) - 1u) / static_cast<uint32_t>(M);
+  return g;
 }
 
 // Column tiles of a workgroup.  Plain: tiles tb + tt, tt < TN.  Fused gate/up (TN even,
@@ -178,10 +224,11 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 // Copy the scale pairs, zero words and (XL) activation rows of the wave's items (groups
 // g_first + i W, i < n_items) into its LDS slice `wl` with direct-to-LDS buffer loads (64
 // consecutive LDS words or 16-byte chunks per instruction, every lane busy; lanes past the
-// end fetch nothing).
-template <int TN, bool XL, int W>
+// end fetch nothing).  With NORM the activation slice is written by the norm prologue.
+template <int TN, bool XL, int W, bool NORM = false>
 __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay, const DecodeSources& src, int M,
-                                               int K, int N, int tb, int dt, int g_first, int n_items, int lane) {
+                                               int K, int N, int tb, int dt, int g_first, int n_items, int lane,
+                                               uint32_t m_mul) {
   constexpr int kSW = TN * 8;  // scale-pair words per group (8 per tile)
   constexpr int kZW = TN * 2;  // zero words per group (2 per tile)
   const int s_words = n_items * kSW;
@@ -204,21 +251,114 @@ __device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay
         w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(wl + lay.z_off + b * 4), 4, off, 0, 0, 0);
   }
-  if constexpr (XL) {
+  if constexpr (XL && !NORM) {
     // LDS chunk C = (i M + r) 16 + cc holds global chunk cc ^ (r & 15) of row r of item i's
     // group: the 16 rows of one fragment read then sit in 16 different chunk positions,
     // i.e. on all 64 banks once.
     const int chunks = n_items * M * 16;
     for (int b = 0; b < chunks; b += 64) {
       const int C = b + lane;
-      const int im = C >> 4;
-      const int i = im / M;
+      const int im = C >> 4;  // < 2^12: a workgroup stages at most 32 KiB of 256-byte row slices
+      const int i = static_cast<int>((static_cast<uint32_t>(im) * m_mul) >> 16);
       const int r = im - i * M;
       const int cc = (C & 15) ^ (r & 15);
       const uint32_t off =
           C < chunks ? (static_cast<uint32_t>(r) * K + static_cast<uint32_t>(g_first + i * W) * kGroup) * 2u + cc * 16u
                      : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_void_t*)(wl + lay.x_off + b * 16), 16, off, 0, 0, 0);
+    }
+  }
+}
+
+// Operands of the RMSNorm prologue held by one lane: lane l works on item i = l / 16 of the
+// wave (at most kNormItems items; lanes past n_items idle) at staged chunk position p = l % 16
+// of each of the M <= 4 rows, i.e. on row r's 16-byte chunk c = p ^ r of the item's group --
+// the chunk the staged layout keeps at position p -- so the wave's 64 lanes cover its four
+// items and each lane does M chunks.
+constexpr int kNormItems = 4;
+// Rows of the prologue: NR = M registers' worth each (at M >= 3 the extra loads and registers
+// made the one-launch form slower than the norm kernel plus the GEMM on MI355X).
+constexpr int kNormMaxRows = 2;
+template <int NR>  // rows held: M <= NR
+struct NormRegs {
+  u32x4_t x[NR], r[NR], w[NR];
+};
+
+__device__ __forceinline__ uint4 as_uint4(u32x4_t v) { return make_uint4(v[0], v[1], v[2], v[3]); }
+
+// Issues the lane's activation, residual (a null residual: a zero-length buffer, which
+// loads zeros) and weight chunks; rows past M and items past n_items fetch nothing.
+template <int W, int NR>
+__device__ __forceinline__ void load_norm_operands(NormRegs<NR>& nr, const DecodeSources& src,
+                                                   __amdgpu_buffer_rsrc_t rres, __amdgpu_buffer_rsrc_t rw, int M, int K,
+                                                   int g_first, int n_items, int lane) {
+  const int i = lane >> 4;
+  const int p = lane & 15;
+  const uint32_t g0 = static_cast<uint32_t>(g_first + i * W) * kGroup;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const bool ok = r < M && i < n_items;
+    const uint32_t col = (g0 + 8u * static_cast<uint32_t>(p ^ r)) * 2u;
+    const uint32_t xo = ok ? static_cast<uint32_t>(r) * K * 2u + col : kOutOfRange;
+    nr.x[r] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo, 0, 0);
+    nr.r[r] = __builtin_amdgcn_raw_buffer_load_b128(rres, xo, 0, 0);
+    nr.w[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? col : kOutOfRange, 0, 0);
+  }
+}
+
+// The prologue proper: s = x + res in fp32 (s = x without a residual); per row, the sum of
+// s^2 over the lane's chunk, over the wave's 64 lanes (xor shuffles) to part[wave][row], a
+// workgroup barrier on LDS alone (the weight loads in flight are not waited for), the row
+// scale from the sum over the waves in wave order, then x_norm written into the wave's
+// activation slice; the writer workgroup also stores res_out = bf16(s) and x_out = x_norm.
+// Every workgroup computes the same values in the same order.
+template <int W, int NR>
+__device__ __forceinline__ void norm_rows(const NormRegs<NR>& nr, uint8_t* wl, const DecodeLds& lay, float (*part)[4],
+                                          int wave, int lane, int M, int K, int g_first, int n_items, bool writer,
+                                          const DecodeNorm& nrm) {
+  const int i = lane >> 4;
+  const int p = lane & 15;
+  const bool live = i < n_items;
+  const bool has_res = nrm.res != nullptr;
+  float sv[NR][8];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (r < M) {
+      unpack_bf16x8(as_uint4(nr.x[r]), sv[r]);
+      if (has_res) {
+        float rv[8];
+        unpack_bf16x8(as_uint4(nr.r[r]), rv);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) sv[r][q] += rv[q];
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss += sv[r][q] * sv[r][q];
+      ss = wave_sum64(ss);
+      if (lane == 0) part[wave][r] = ss;
+    }
+  }
+  // Only LDS needs ordering here: a workgroup-scope fence on the local address space waits
+  // for LDS operations alone, so the barrier leaves the ring's loads in flight.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  const size_t g0 = static_cast<size_t>(g_first + i * W) * kGroup;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (r < M) {
+      float t = 0.f;
+      for (int w = 0; w < W; ++w) t += part[w][r];
+      const float rstd = rsqrt_rn(t / static_cast<float>(K) + nrm.eps);
+      if (live) {
+        const uint4 out = rms_scale_bf16x8(sv[r], rstd, as_uint4(nr.w[r]));
+        *reinterpret_cast<uint4*>(wl + lay.x_off + (i * M + r) * 256 + p * 16) = out;
+        if (writer) {
+          const size_t off = static_cast<size_t>(r) * K + g0 + 8 * (p ^ r);
+          *reinterpret_cast<uint4*>(nrm.x_out + off) = out;
+          if (has_res) *reinterpret_cast<uint4*>(nrm.res_out + off) = pack_bf16x8(sv[r]);
+        }
+      }
     }
   }
 }
@@ -247,7 +387,7 @@ __device__ __forceinline__ void build_tile_scales(uint8_t* wl, const DecodeLds& 
   }
 }
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -255,18 +395,19 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             uint16_t* y, const uint16_t* res,
                                                             float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
-                                                            int split, int up_tiles) {
+                                                            int split, int up_tiles, DecodeGeom geo, DecodeNorm nrm) {
+  constexpr bool NORM = NR > 0;
+  static_assert(!NORM || (XL && MB == 1), "the norm prologue works on staged rows (M <= 4)");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
+  __shared__ float norm_part[NORM ? WAVES : 1][4];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   constexpr int W = WAVES;
-  const int G = K / kGroup;
   const int cb = blockIdx.x;
   const int sidx = blockIdx.y;
-  const int g_begin = (G * sidx) / split;
-  const int g_end = (G * (sidx + 1)) / split;
-  const int nG = g_end - g_begin;
+  const int g_begin = sidx * geo.gq + (sidx < geo.gr ? sidx : geo.gr);
+  const int nG = geo.gq + (sidx < geo.gr ? 1 : 0);
   // Fused SiLU(gate) * up (TN even): the workgroup's H gate tiles are output tiles
   // cb H .. cb H + H - 1 of the [M, N / 2] result.
   constexpr int H = TN / 2;
@@ -274,13 +415,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const int tb = act ? cb * H : cb * TN;
   const int dt = act ? up_tiles - H : 0;
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
-  const DecodeLds lay = decode_lds_layout(M, K, TN, W, split, XL, kPre);
+  const DecodeLds lay{0u, geo.z_off, geo.x_off, geo.c_off, geo.d_off, geo.wave_bytes, 0u, 0u, 0u};
 
   DecodeSources src;
-  src.x = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
-  src.w = make_buffer(packed, static_cast<uint32_t>(K) * (N / 2));
-  src.s = make_buffer(scales, static_cast<uint32_t>(G) * N * 2u);
-  src.z = make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u);
+  src.x = make_buffer(x, geo.x_bytes);
+  src.w = make_buffer(packed, geo.w_bytes);
+  src.s = make_buffer(scales, geo.s_bytes);
+  src.z = make_buffer(qzeros, geo.z_bytes);
   uint32_t x_row[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -297,7 +438,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // The wave's groups: gi = wave + i W of the K range, i < n_items.
   const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
   uint8_t* wl = lds + wave * lay.wave_bytes;
-  stage_operands<TN, XL, W>(wl, lay, src, M, K, N, tb, dt, g_begin + wave, n_items, lane);
+  stage_operands<TN, XL, W, NORM>(wl, lay, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
+  NormRegs<(NR > 0 ? NR : 1)> nr;
+  if constexpr (NORM)
+    load_norm_operands<W>(nr, src, make_buffer(nrm.res, nrm.res ? geo.x_bytes : 0u),
+                          make_buffer(nrm.w, static_cast<uint32_t>(K) * 2u), M, K, g_begin + wave, n_items, lane);
   __builtin_amdgcn_sched_barrier(0);  // the staging loads stay ahead of the ring's
 
   // Depth-DEPTH ring over the wave's items: item i is loaded while item i - DEPTH is being
@@ -308,6 +453,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d)
     load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
+  // The norm prologue works from registers while the ring's loads are in flight (its
+  // register loads are waited for individually), then writes the activation slice.
+  if constexpr (NORM)
+    norm_rows<W>(nr, wl, lay, norm_part, wave, lane, M, K, g_begin + wave, n_items, blockIdx.x == 0 && sidx == 0, nrm);
   // Direct-to-LDS loads may complete out of order with the register loads issued after
   // them (they do when those hit in cache), so a partial vmcnt wait does not cover them:
   // wait for everything, the ring included, before the first group reads the slice.
@@ -431,15 +580,25 @@ size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
       .total;
 }
 
+size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
+  const int G = K / kGroup;
+  if (M > kNormMaxRows || split != 1 || !decode_stages_x(M, K, split) || (G + waves - 1) / waves > kNormItems)
+    return 0;
+  return decode_lds_layout(M, K, tn, waves, split, true, decode_prebuilt_scales(waves, depth)).total;
+}
+
 constexpr int kMaxDevices = 64;
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   if constexpr (!decode_config_fits(MB, TN, DEPTH, XL)) {
     return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
-  const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, decode_prebuilt_scales(WAVES, DEPTH)).total;
+  constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
+  const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
+  const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
+  if (lds > kDecodeMaxLds) return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
     // call from a racing thread is harmless).  A failed call returns before the launch: a
@@ -448,65 +607,75 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     if (!raised[dev].load(std::memory_order_acquire)) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL>),
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                static_cast<int>(kDecodeMaxLds));
       if (e != hipSuccess) return e;
       raised[dev].store(true, std::memory_order_release);
     }
   }
-  decode_kernel<MB, TN, DEPTH, WAVES, XL><<<grid, 64 * WAVES, lds, stream>>>(
-      a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles);
+  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR><<<grid, 64 * WAVES, lds, stream>>>(
+      a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles,
+      geo, a.norm);
   return hipGetLastError();
   }
 }
 
 template <int MB, int TN, int DEPTH, int WAVES>
-static hipError_t launch_decode_x(const DecodeArgs& a, hipStream_t stream) {
+static hipError_t launch_decode_x(const DecodeArgs& a, bool norm, hipStream_t stream) {
   if constexpr (MB == 1) {
-    if (decode_stages_x(a.M, a.K, a.split)) return launch_decode_t<MB, TN, DEPTH, WAVES, true>(a, stream);
+    if (decode_stages_x(a.M, a.K, a.split)) {
+      if (norm) {
+        if (a.M == 1) return launch_decode_t<MB, TN, DEPTH, WAVES, true, 1>(a, stream);
+        if (a.M == 2) return launch_decode_t<MB, TN, DEPTH, WAVES, true, 2>(a, stream);
+        return hipErrorInvalidValue;  // M <= kNormMaxRows (checked by the API)
+      }
+      return launch_decode_t<MB, TN, DEPTH, WAVES, true>(a, stream);
+    }
   }
+  if (norm) return hipErrorInvalidValue;  // the prologue needs staged rows (checked by the API)
   return launch_decode_t<MB, TN, DEPTH, WAVES, false>(a, stream);
 }
 
 template <int MB, int TN, int DEPTH>
-static hipError_t launch_decode_w(const DecodeArgs& a, int waves, hipStream_t stream) {
+static hipError_t launch_decode_w(const DecodeArgs& a, int waves, bool norm, hipStream_t stream) {
   switch (waves) {
-    case 4: return launch_decode_x<MB, TN, DEPTH, 4>(a, stream);
-    default: return launch_decode_x<MB, TN, DEPTH, 8>(a, stream);
+    case 4: return launch_decode_x<MB, TN, DEPTH, 4>(a, norm, stream);
+    default: return launch_decode_x<MB, TN, DEPTH, 8>(a, norm, stream);
   }
 }
 
 template <int MB, int TN>
-static hipError_t launch_decode_d(const DecodeArgs& a, int depth, int waves, hipStream_t stream) {
+static hipError_t launch_decode_d(const DecodeArgs& a, int depth, int waves, bool norm, hipStream_t stream) {
   switch (depth) {
-    case 1: return launch_decode_w<MB, TN, 1>(a, waves, stream);
-    case 2: return launch_decode_w<MB, TN, 2>(a, waves, stream);
-    default: return launch_decode_w<MB, TN, 4>(a, waves, stream);
+    case 1: return launch_decode_w<MB, TN, 1>(a, waves, norm, stream);
+    case 2: return launch_decode_w<MB, TN, 2>(a, waves, norm, stream);
+    default: return launch_decode_w<MB, TN, 4>(a, waves, norm, stream);
   }
 }
 
 template <int MB>
-static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int waves, hipStream_t stream) {
+static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int waves, bool norm, hipStream_t stream) {
   switch (tn) {
-    case 1: return launch_decode_d<MB, 1>(a, depth, waves, stream);
-    case 2: return launch_decode_d<MB, 2>(a, depth, waves, stream);
-    case 3: return launch_decode_d<MB, 3>(a, depth, waves, stream);
-    case 4: return launch_decode_d<MB, 4>(a, depth, waves, stream);
-    default: return launch_decode_d<MB, 6>(a, depth, waves, stream);
+    case 1: return launch_decode_d<MB, 1>(a, depth, waves, norm, stream);
+    case 2: return launch_decode_d<MB, 2>(a, depth, waves, norm, stream);
+    case 3: return launch_decode_d<MB, 3>(a, depth, waves, norm, stream);
+    case 4: return launch_decode_d<MB, 4>(a, depth, waves, norm, stream);
+    default: return launch_decode_d<MB, 6>(a, depth, waves, norm, stream);
   }
 }
 
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
                              int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
-                             hipStream_t stream) {
-  const DecodeArgs a{x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, up_tiles};
+                             const DecodeNorm* norm, hipStream_t stream) {
+  const DecodeArgs a{x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, up_tiles,
+                     norm ? *norm : DecodeNorm{}};
   switch ((M + 15) / 16) {
-    case 1: return launch_decode_m<1>(a, tn, depth, waves, stream);
-    case 2: return launch_decode_m<2>(a, tn, depth, waves, stream);
-    case 3: return launch_decode_m<3>(a, tn, depth, waves, stream);
-    default: return launch_decode_m<4>(a, tn, depth, waves, stream);
+    case 1: return launch_decode_m<1>(a, tn, depth, waves, norm != nullptr, stream);
+    case 2: return launch_decode_m<2>(a, tn, depth, waves, norm != nullptr, stream);
+    case 3: return launch_decode_m<3>(a, tn, depth, waves, norm != nullptr, stream);
+    default: return launch_decode_m<4>(a, tn, depth, waves, norm != nullptr, stream);
   }
 }
 

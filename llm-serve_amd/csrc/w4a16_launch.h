@@ -53,13 +53,33 @@ constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
   return decode_ring_regs(mb, tn, depth, xl) <= 176;
 }
 
+// RMSNorm(+residual) prologue of a decode GEMM whose activations are staged in LDS: the
+// GEMM input is x_norm = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * w), s = x + res (fp32; s = x
+// without res), computed by every workgroup from its staged rows; the first workgroup also
+// writes res_out = bf16(s) (when res is given) and x_out = x_norm.  None of res_out, x_out
+// may alias x or res.
+struct DecodeNorm {
+  const uint16_t* res;  // [M, K] residual or null
+  const uint16_t* w;    // [K] norm weight
+  uint16_t* res_out;    // [M, K] new residual (null iff res is null)
+  uint16_t* x_out;      // [M, K] normalized activations
+  float eps;
+};
+
+// LDS bytes of a decode workgroup that also runs the norm prologue (the same layout as
+// without it: the prologue works from registers and writes the activation slice), or 0 if
+// the configuration cannot run it (M > 2, activations not staged, a K split, or more than
+// four groups per wave).
+size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int split);
+
 // up_tiles: 0 for the plain GEMM (y is [M, N]); N / 32 for the fused SiLU(gate) * up of a
 // gate|up weight (tn even, N % 128 == 0, y is [M, N / 2]).  res: null, or a bf16 [M, N]
-// residual added in the epilogue (plain GEMM only; may be y itself).
+// residual added in the epilogue (plain GEMM only; may be y itself).  norm: null, or the
+// prologue above (requires decode_norm_lds_bytes(...) in (0, kDecodeMaxLds]).
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
                              int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
-                             hipStream_t stream);
+                             const DecodeNorm* norm, hipStream_t stream);
 
 // LDS-tiled MFMA GEMM.  A tile shape code selects the wave grid: wk K slices of nwm waves
 // along M x nwn along N, each wave owning tw 16-column layout tiles and 16 wm rows, so the

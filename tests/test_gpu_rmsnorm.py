@@ -86,22 +86,62 @@ def test_add_rmsnorm_in_place(gpu_lib):
 
 @pytest.mark.parametrize("shape,silu", [("qkv", False), ("gate_up", True), ("gate_up", False)])
 def test_fused_norm_gemm_equals_norm_then_gemm(gpu_lib, shape, silu):
-    """Every regime (decode without / with a K split, the tile kernel) at the real shapes."""
+    """Every regime (the decode kernel with the norm as its prologue at M <= 2, the decode
+    kernel with and without a K split after the norm kernel, the tile kernel) at the real
+    shapes: the call's normalised activations x_norm are within the norm's bar of the oracle
+    (two ulps, > 99 % exact), its GEMM output equals the plain (or SiLU * up) GEMM of that
+    x_norm bit for bit, and the new residual is bit-exact; the same with the residual updated
+    in place (which always takes the norm kernel)."""
     k, n = QWEN3_SHAPES[shape]
     awq = awq_mod()
+    lib = awq.lib()
     qw, qz, s = random_awq_gpu(k, n, seed=71)
     packed = awq.repack_awq_qweight(qw)
-    w = bf16_from_bits(rand_bits((k,), seed=5, scale=0.1, offset=1.0))
-    for m in (1, 4, 16, 33, 64, 300, 2048):
+    w_bits = rand_bits((k,), seed=5, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    for m in (1, 2, 4, 5, 16, 33, 64, 300, 2048):
         print(f"gemm_rmsnorm {shape} silu={silu} m={m}", flush=True)
-        x = bf16_from_bits(rand_bits((m, k), seed=m))
-        res = bf16_from_bits(rand_bits((m, k), seed=m + 1, scale=4.0))
-        y, res_out = awq.awq_linear_rmsnorm(x, res, w, EPS, packed, qz, s, group_size=128, silu_mul=silu)
-        xn, want_res = awq.add_rms_norm(x, res, w, EPS)
-        plain = (awq.awq_linear_silu_mul if silu else awq.awq_linear)(xn, packed, qz, s, group_size=128)
-        assert y.shape == plain.shape
-        assert torch.equal(y.view(torch.int16), plain.view(torch.int16)), m
-        assert torch.equal(res_out.view(torch.int16), want_res.view(torch.int16)), m
+        x_bits, r_bits = rand_bits((m, k), seed=m), rand_bits((m, k), seed=m + 1, scale=4.0)
+        x, res = bf16_from_bits(x_bits), bf16_from_bits(r_bits)
+        want_xn, want_res, _ = ora.add_rms_norm_ref(x_bits, r_bits, w_bits, EPS)
+        n_out = n // 2 if silu else n
+        ws = torch.zeros(max(lib.workspace_bytes(m, k, n), 256), dtype=torch.uint8, device="cuda")
+        for in_place in (False, True):
+            res_in = res.clone()
+            res_out = res_in if in_place else torch.empty_like(res)
+            xn = torch.empty_like(x)
+            y = torch.empty((m, n_out), dtype=torch.bfloat16, device="cuda")
+            lib.gemm_rmsnorm(x, res_in, w, EPS, xn, res_out, packed, qz, s, y, n, ws, silu_mul=silu)
+            assert np.array_equal(bits_of(res_out), want_res), (m, in_place)
+            d = ulp_diff(bits_of(xn), want_xn)
+            assert d.max() <= 2 and (d == 0).mean() > 0.99, (m, in_place, d.max(), (d == 0).mean())
+            plain = (awq.awq_linear_silu_mul if silu else awq.awq_linear)(xn, packed, qz, s, group_size=128)
+            assert torch.equal(y.view(torch.int16), plain.view(torch.int16)), (m, in_place)
+
+
+def test_fused_norm_prologue_without_residual_and_first_layer(gpu_lib):
+    """The decode prologue without a residual (the first layer's input_layernorm): x_norm
+    within the bar of the oracle's rms_forward, the GEMM of it bit-identical; the layer API
+    returns the input itself as the new residual."""
+    k, n = QWEN3_SHAPES["qkv"]
+    awq = awq_mod()
+    lib = awq.lib()
+    qw, qz, s = random_awq_gpu(k, n, seed=72)
+    packed = awq.repack_awq_qweight(qw)
+    w_bits = rand_bits((k,), seed=6, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    for m in (1, 2):
+        x_bits = rand_bits((m, k), seed=40 + m, scale=2.0)
+        x = bf16_from_bits(x_bits)
+        xn = torch.empty_like(x)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        lib.gemm_rmsnorm(x, None, w, EPS, xn, None, packed, qz, s, y, n, None)
+        want_xn, _, _ = ora.add_rms_norm_ref(x_bits, None, w_bits, EPS)
+        d = ulp_diff(bits_of(xn), want_xn)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99, (m, d.max())
+        assert torch.equal(y.view(torch.int16), awq.awq_linear(xn, packed, qz, s, group_size=128).view(torch.int16))
+        y2, first_res = awq.awq_linear_rmsnorm(x, None, w, EPS, packed, qz, s, group_size=128)
+        assert first_res is x and torch.equal(y2.view(torch.int16), y.view(torch.int16))
 
 
 @pytest.mark.parametrize("m", [1, 16, 200])
