@@ -43,11 +43,14 @@ Also reported (not part of `value`):
     36 copies per step, one graph;
   * measured_ceilings: a 1 GiB device copy (read + write GB/s), plain streaming reads
     (llm-serve_amd/csrc/probe_read.hip, best of six grid sizes) of 1 GiB and of 52.3 MB
-    per launch (the gate_up weight bytes, rotating over more than 2 x 256 MB), and
-    torch.matmul (hipBLASLt) bf16 at the M = 2048 gate_up shape, beside the nominal peaks;
-    `roofline.measured_frac` is the dominant launch against the 52.3 MB read;
-  * points: every decode point's mean per-launch time and the median, min and max of its
-    four timed blocks;
+    per launch (the gate_up weight bytes, rotating over more than 2 x 256 MB) and of every
+    other projection's weight bytes per launch (read_per_launch_by_shape: 13.1 MB QKV,
+    8.7 MB O, 26.2 MB down), and torch.matmul (hipBLASLt) bf16 at the M = 2048 gate_up
+    shape, beside the nominal peaks; `roofline.measured_frac` is the dominant launch
+    against the 52.3 MB read;
+  * points: every decode point's mean per-launch time, the median, min and max of its four
+    timed blocks, and read_ceiling_frac: its GB/s over the plain read of its shape's weight
+    bytes per launch;
   * cpu_baseline.parity_max_rel_err_vs_gpu: the oracle's output against the HIP GEMM's
     on the same inputs (the baseline's own problem);
   * fused_gate_up: the gate_up GEMM with SiLU(gate) * up in its epilogue
@@ -587,6 +590,13 @@ def measured_ceilings(dev, stream) -> dict:
         reads = {"read_1GiB_GB/s": round(read_1g[0], 1),
                  f"read_{wb / 1e6:.1f}MB_per_launch_GB/s": round(read_dom[0], 1),
                  "read_probe_blocks": {"1GiB": read_1g[1], f"{wb / 1e6:.1f}MB": read_dom[1]}}
+        # the same probe at every projection's weight bytes per launch (decode's ceiling)
+        per_shape = {}
+        for name, (k, n) in SHAPES.items():
+            b = weight_bytes(k, n)
+            r = read_dom if name == DOMINANT[0] else read_ceiling(dev, stream, b, max(2, -(-2 * CACHE_BYTES // b)))
+            per_shape[name] = {"MB": round(b / 1e6, 1), "GB/s": round(r[0], 1), "blocks": r[1]}
+        reads["read_per_launch_by_shape"] = per_shape
     k, n = SHAPES["gate_up"]
     a = torch.randn((PREFILL_M, k), device=dev).to(torch.bfloat16)
     b = torch.randn((k, n), device=dev).to(torch.bfloat16)
@@ -824,6 +834,10 @@ def main(argv=None):
             print(f"stack36_normed: {json.dumps(stack_normed)}", file=sys.stderr)
             print(f"rmsnorm_prologue: {json.dumps(norm)}", file=sys.stderr)
 
+    by_shape = (ceilings or {}).get("read_per_launch_by_shape", {})
+    for pt in points_out:  # each decode point against a plain read of its shape's weight bytes
+        if pt["shape"] in by_shape:
+            pt["read_ceiling_frac"] = round(pt["GB/s"] / by_shape[pt["shape"]]["GB/s"], 4)
     cpu = None if args.no_cpu else cpu_baseline(gpu_gemm=lambda prob: gpu_gemm_bits(pkg, dev, prob))
     result = {
         "metric": METRIC,

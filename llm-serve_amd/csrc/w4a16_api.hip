@@ -69,10 +69,11 @@ int tile_bn(const GemmPlan& p) {
 //    to M = 8, 96 beyond (fewer, wider workgroups: every wave repeats the kernel's scalar
 //    set-up, so the grid's wave count is a fixed cost), one group in flight per wave at
 //    M > 32 (the registers then hold three 16-row activation blocks);
-//  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 16, then 48 with K
+//  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 8, then 48 with K
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
-//    N = 4096), then 64 columns with K in four;
+//    N = 4096; from M = 5 on, 4 waves with four groups each in flight), then 64 columns with
+//    K in four;
 //  * narrow layers with long K: 16 columns at M = 1, 32 with K in two or four up to M = 8,
 //    then 64 columns with K in four.
 GemmPlan plan_decode(int M, int K, int N) {
@@ -87,10 +88,11 @@ GemmPlan plan_decode(int M, int K, int N) {
     else { tn = 6; depth = 1; }
   } else if (N > 4096) {
     if (M <= 1) tn = 1;
-    else if (M <= 16) tn = 2;
+    else if (M <= 8) tn = 2;
     else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
-    if (M <= 16) tn = 1;
+    if (M <= 4) tn = 1;
+    else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
     else { tn = 4; depth = 1; split = 4; }
   } else {
     if (M <= 1) { tn = 1; depth = 4; }
@@ -104,8 +106,11 @@ GemmPlan plan_decode(int M, int K, int N) {
   // Other shapes: the widest tile count <= tn that divides N / 16 and fits the registers.
   while (depth > 1 && !w4a16::decode_config_fits(MB, tn, depth, xl)) depth /= 2;
   while (tn > 1 && (T % tn != 0 || tn == 5 || !w4a16::decode_config_fits(MB, tn, depth, xl))) --tn;
-  // Very long K: split it until the staged operands of a workgroup fit in LDS.
-  while (w4a16::decode_lds_bytes(M, K, tn, waves, depth, split) > w4a16::kDecodeMaxLds && split < G)
+  // Very long K: split it until the staged operands of a workgroup fit in LDS and a wave's
+  // staging loads fit its registers.
+  while ((w4a16::decode_lds_bytes(M, K, tn, waves, depth, split) > w4a16::kDecodeMaxLds ||
+          !w4a16::decode_stage_fits(M, K, tn, waves, split)) &&
+         split < G)
     split = split * 2 > G ? G : split * 2;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
 }
@@ -218,7 +223,9 @@ GemmPlan plan_silu_mul(int M, int K, int N) {
   while (tn > 2 && (T % tn != 0 || !w4a16::decode_config_fits(MB, tn, 1, xl))) tn -= 2;
   while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
   p.p0 = tn;
-  while (w4a16::decode_lds_bytes(M, K, tn, p.p1, p.p2, p.split) > w4a16::kDecodeMaxLds && p.split < G)
+  while ((w4a16::decode_lds_bytes(M, K, tn, p.p1, p.p2, p.split) > w4a16::kDecodeMaxLds ||
+          !w4a16::decode_stage_fits(M, K, tn, p.p1, p.split)) &&
+         p.split < G)
     p.split = p.split * 2 > G ? G : p.split * 2;
   return p;
 }
@@ -645,6 +652,9 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
     if (w4a16::decode_lds_bytes(M, K, p0, p1, p2, split) > w4a16::kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
                   w4a16::decode_lds_bytes(M, K, p0, p1, p2, split), w4a16::kDecodeMaxLds);
+    if (!w4a16::decode_stage_fits(M, K, p0, p1, split))
+      return fail(W4A16_ERR_ARG, "decode configuration stages more scale, zero or activation words per wave than "
+                  "its registers hold (split K further)");
     if (!w4a16::decode_config_fits((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)))
       return fail(W4A16_ERR_ARG, "decode configuration needs %d ring and accumulator registers per lane (limit 176)",
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));

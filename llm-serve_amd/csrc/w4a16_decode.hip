@@ -221,52 +221,95 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
   }
 }
 
-// Copy the scale pairs, zero words and (XL) activation rows of the wave's items (groups
-// g_first + i W, i < n_items) into its LDS slice `wl` with direct-to-LDS buffer loads (64
-// consecutive LDS words or 16-byte chunks per instruction, every lane busy; lanes past the
-// end fetch nothing).  With NORM the activation slice is written by the norm prologue.
-template <int TN, bool XL, int W, bool NORM = false>
-__device__ __forceinline__ void stage_operands(uint8_t* wl, const DecodeLds& lay, const DecodeSources& src, int M,
-                                               int K, int N, int tb, int dt, int g_first, int n_items, int lane,
-                                               uint32_t m_mul) {
+// Staging of the scale pairs, zero words and (XL) activation rows of the wave's items
+// (groups g_first + i W, i < n_items) into its LDS slice `wl`, in two steps around the issue
+// of the weight ring: load_staged() issues ordinary register loads (64 consecutive words or
+// 16-byte chunks per instruction, every lane busy; lanes past the end fetch nothing),
+// store_staged() writes them to the slice once they have arrived.  (Direct-to-LDS loads, the
+// obvious alternative, cost 0.35 - 1.5 us of issue time per launch at the Qwen3-8B decode
+// shapes on MI355X, growing with the waves per CU; register loads issue at once.)  At most
+// kStageS x 64 scale words, kStageZ x 64 zero words and kStageX x 64 activation chunks per
+// wave (decode_stage_fits()).  With NORM the activation slice is written by the norm
+// prologue instead.
+template <int TN, bool XL>
+struct StagedRegs {
+  uint32_t s[kStageS];
+  uint32_t z[kStageZ];
+  u32x4_t x[XL ? kStageX : 1];
+};
+
+template <int TN, bool XL, int W, bool NORM>
+__device__ __forceinline__ void load_staged(StagedRegs<TN, XL>& st, const DecodeSources& src, int M, int K, int N,
+                                            int tb, int dt, int g_first, int n_items, int lane, uint32_t m_mul) {
   constexpr int kSW = TN * 8;  // scale-pair words per group (8 per tile)
   constexpr int kZW = TN * 2;  // zero words per group (2 per tile)
   const int s_words = n_items * kSW;
-  for (int b = 0; b < s_words; b += 64) {
-    const int w = b + lane;
-    const int i = w / kSW;
-    const int j = w - i * kSW;
-    const int sj = tb * 8 + j + (j >= (TN / 2) * 8 ? dt * 8 : 0);
-    const uint32_t off =
-        w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + sj) * 4u : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)(wl + lay.s_off + b * 4), 4, off, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < kStageS; ++u) {
+    if (u == 0 || 64 * u < s_words) {  // uniform
+      const int w = 64 * u + lane;
+      const int i = w / kSW;
+      const int j = w - i * kSW;
+      const int sj = tb * 8 + j + (j >= (TN / 2) * 8 ? dt * 8 : 0);
+      const uint32_t off =
+          w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + sj) * 4u : kOutOfRange;
+      st.s[u] = __builtin_amdgcn_raw_buffer_load_b32(src.s, off, 0, 0);
+    }
   }
   const int z_words = n_items * kZW;
-  for (int b = 0; b < z_words; b += 64) {
-    const int w = b + lane;
-    const int i = w / kZW;
-    const int j = w - i * kZW;
-    const int zj = tb * 2 + j + (j >= (TN / 2) * 2 ? dt * 2 : 0);
-    const uint32_t off =
-        w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(wl + lay.z_off + b * 4), 4, off, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < kStageZ; ++u) {
+    if (u == 0 || 64 * u < z_words) {
+      const int w = 64 * u + lane;
+      const int i = w / kZW;
+      const int j = w - i * kZW;
+      const int zj = tb * 2 + j + (j >= (TN / 2) * 2 ? dt * 2 : 0);
+      const uint32_t off =
+          w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
+      st.z[u] = __builtin_amdgcn_raw_buffer_load_b32(src.z, off, 0, 0);
+    }
   }
   if constexpr (XL && !NORM) {
     // LDS chunk C = (i M + r) 16 + cc holds global chunk cc ^ (r & 15) of row r of item i's
     // group: the 16 rows of one fragment read then sit in 16 different chunk positions,
     // i.e. on all 64 banks once.
     const int chunks = n_items * M * 16;
-    for (int b = 0; b < chunks; b += 64) {
-      const int C = b + lane;
-      const int im = C >> 4;  // < 2^12: a workgroup stages at most 32 KiB of 256-byte row slices
-      const int i = static_cast<int>((static_cast<uint32_t>(im) * m_mul) >> 16);
-      const int r = im - i * M;
-      const int cc = (C & 15) ^ (r & 15);
-      const uint32_t off =
-          C < chunks ? (static_cast<uint32_t>(r) * K + static_cast<uint32_t>(g_first + i * W) * kGroup) * 2u + cc * 16u
-                     : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_void_t*)(wl + lay.x_off + b * 16), 16, off, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kStageX; ++u) {
+      if (u == 0 || 64 * u < chunks) {
+        const int C = 64 * u + lane;
+        const int im = C >> 4;  // < 2^12: a workgroup stages at most 32 KiB of 256-byte row slices
+        const int i = static_cast<int>((static_cast<uint32_t>(im) * m_mul) >> 16);
+        const int r = im - i * M;
+        const int cc = (C & 15) ^ (r & 15);
+        const uint32_t off =
+            C < chunks
+                ? (static_cast<uint32_t>(r) * K + static_cast<uint32_t>(g_first + i * W) * kGroup) * 2u + cc * 16u
+                : kOutOfRange;
+        st.x[u] = __builtin_amdgcn_raw_buffer_load_b128(src.x, off, 0, 0);
+      }
     }
+  }
+}
+
+// Lanes past a region's end write into its rounding (every region is a multiple of 64
+// words or 64 chunks).
+template <int TN, bool XL, bool NORM>
+__device__ __forceinline__ void store_staged(const StagedRegs<TN, XL>& st, uint8_t* wl, const DecodeLds& lay, int M,
+                                             int n_items, int lane) {
+  const int s_words = n_items * TN * 8;
+#pragma unroll
+  for (int u = 0; u < kStageS; ++u)
+    if (u == 0 || 64 * u < s_words) reinterpret_cast<uint32_t*>(wl + lay.s_off)[64 * u + lane] = st.s[u];
+  const int z_words = n_items * TN * 2;
+#pragma unroll
+  for (int u = 0; u < kStageZ; ++u)
+    if (u == 0 || 64 * u < z_words) reinterpret_cast<uint32_t*>(wl + lay.z_off)[64 * u + lane] = st.z[u];
+  if constexpr (XL && !NORM) {
+    const int chunks = n_items * M * 16;
+#pragma unroll
+    for (int u = 0; u < kStageX; ++u)
+      if (u == 0 || 64 * u < chunks) reinterpret_cast<u32x4_t*>(wl + lay.x_off)[64 * u + lane] = st.x[u];
   }
 }
 
@@ -438,7 +481,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // The wave's groups: gi = wave + i W of the K range, i < n_items.
   const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
   uint8_t* wl = lds + wave * lay.wave_bytes;
-  stage_operands<TN, XL, W, NORM>(wl, lay, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
+  StagedRegs<TN, XL> staged;
+  load_staged<TN, XL, W, NORM>(staged, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
   NormRegs<(NR > 0 ? NR : 1)> nr;
   if constexpr (NORM)
     load_norm_operands<W>(nr, src, make_buffer(nrm.res, nrm.res ? geo.x_bytes : 0u),
@@ -453,14 +497,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d)
     load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
-  // The norm prologue works from registers while the ring's loads are in flight (its
-  // register loads are waited for individually), then writes the activation slice.
+  // The staged operands go to LDS as soon as they arrive (the ring's loads stay in flight:
+  // the compiler waits for each register load individually), then the norm prologue works
+  // from its registers and writes the activation slice.
+  store_staged<TN, XL, NORM>(staged, wl, lay, M, n_items, lane);
   if constexpr (NORM)
     norm_rows<W>(nr, wl, lay, norm_part, wave, lane, M, K, g_begin + wave, n_items, blockIdx.x == 0 && sidx == 0, nrm);
-  // Direct-to-LDS loads may complete out of order with the register loads issued after
-  // them (they do when those hit in cache), so a partial vmcnt wait does not cover them:
-  // wait for everything, the ring included, before the first group reads the slice.
-  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);  // vmcnt(0), expcnt and lgkmcnt untouched
   if constexpr (kPre) build_tile_scales<TN>(wl, lay, n_items, lane);
 
   const NibbleConsts nib = nibble_consts();
@@ -575,6 +617,13 @@ bool decode_stages_x(int M, int K, int split) {
   return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
 }
 
+bool decode_stage_fits(int M, int K, int tn, int waves, int split) {
+  const int G = K / kGroup;
+  const int items = ((G + split - 1) / split + waves - 1) / waves;
+  return items * tn * 8 <= 64 * kStageS && items * tn * 2 <= 64 * kStageZ &&
+         (!decode_stages_x(M, K, split) || items * M * 16 <= 64 * kStageX);
+}
+
 size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
   return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split), decode_prebuilt_scales(waves, depth))
       .total;
@@ -598,7 +647,8 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
   const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
-  if (lds > kDecodeMaxLds) return hipErrorInvalidValue;  // checked by the API before launch
+  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, a.split))
+    return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
     // call from a racing thread is harmless).  A failed call returns before the launch: a
