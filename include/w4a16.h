@@ -193,10 +193,13 @@ int w4a16_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_oute
 
 /* The RMSNorm(+residual) prologue of w4a16_add_rmsnorm followed, on the same stream and in
  * the same call, by w4a16_gemm (silu_mul == 0) or w4a16_gemm_silu_mul (silu_mul == 1) of
- * x_norm: y = x_norm @ W, or SiLU(g) * u of it.  x_norm [M, K] is a caller buffer the
- * GEMM reads back while it is still in L2 at decode sizes.  Arguments as for those two
- * calls; the workspace is w4a16_workspace_bytes(M, K, N, 128).  Argument, shape and
- * workspace errors are reported before anything is enqueued.
+ * x_norm: y = x_norm @ W, or SiLU(g) * u of it.  x_norm [M, K] (a caller buffer) and
+ * residual_out receive the norm's outputs.  At M <= 2 on decode plans without a K split
+ * (the Qwen3-8B QKV and gate|up shapes) and with x_norm / residual_out distinct from x and
+ * residual, the norm runs inside the GEMM kernel (one launch); otherwise the norm kernel
+ * writes x_norm and the GEMM reads it back (from L2 at decode sizes).  Arguments as for
+ * those two calls; the workspace is w4a16_workspace_bytes(M, K, N, 128).  Argument, shape
+ * and workspace errors are reported before anything is enqueued.
  * Replaces input_layernorm / post_attention_layernorm followed by qkv_proj / gate_up_proj
  * (qwen3.py:166-173 with layernorm.py:28-40, qwen3.py:126-130). */
 int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16_t* norm_weight, float eps,
