@@ -109,7 +109,7 @@ GemmPlan plan_decode(int M, int K, int N) {
   // Very long K: split it until the staged operands of a workgroup fit in LDS and a wave's
   // staging loads fit its registers.
   while ((w4a16::decode_lds_bytes(M, K, tn, waves, depth, split) > w4a16::kDecodeMaxLds ||
-          !w4a16::decode_stage_fits(M, K, tn, waves, split)) &&
+          !w4a16::decode_stage_fits(M, K, tn, waves, depth, split)) &&
          split < G)
     split = split * 2 > G ? G : split * 2;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
@@ -224,7 +224,7 @@ GemmPlan plan_silu_mul(int M, int K, int N) {
   while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
   p.p0 = tn;
   while ((w4a16::decode_lds_bytes(M, K, tn, p.p1, p.p2, p.split) > w4a16::kDecodeMaxLds ||
-          !w4a16::decode_stage_fits(M, K, tn, p.p1, p.split)) &&
+          !w4a16::decode_stage_fits(M, K, tn, p.p1, p.p2, p.split)) &&
          p.split < G)
     p.split = p.split * 2 > G ? G : p.split * 2;
   return p;
@@ -652,7 +652,7 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
     if (w4a16::decode_lds_bytes(M, K, p0, p1, p2, split) > w4a16::kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",
                   w4a16::decode_lds_bytes(M, K, p0, p1, p2, split), w4a16::kDecodeMaxLds);
-    if (!w4a16::decode_stage_fits(M, K, p0, p1, split))
+    if (!w4a16::decode_stage_fits(M, K, p0, p1, p2, split))
       return fail(W4A16_ERR_ARG, "decode configuration stages more scale, zero or activation words per wave than "
                   "its registers hold (split K further)");
     if (!w4a16::decode_config_fits((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)))

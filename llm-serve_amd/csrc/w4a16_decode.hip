@@ -60,12 +60,12 @@ struct DecodeArgs {
 
 // LDS layout of the staged operands.  A wave owns at most `items` groups (its groups
 // gi = wave + i W of the workgroup's K range); its slice holds, per item i, scale pairs
-// [items][TN * 8] words, zero words [items][TN * 2], then (XL) activations [items][M][128]
-// bf16 with 16-byte chunks swizzled by row, then (pre) the dequant operands built from
-// the scales and zeros (build_tile_scales): C inputs [items][TN][16 columns] x 16 bytes and
+// [items][TN * 8] words and zero words [items][TN * 2], then (XL) activations
+// [items][M][128] bf16 with 16-byte chunks swizzled by row, then (pre) the dequant operands
+// built from the scales and zeros: C inputs [items][TN][16 columns] x 16 bytes and
 // diagonals [items][TN][16] x 8 bytes.  Region sizes are rounded so that the last
-// direct-to-LDS load of a region (64 lanes x 4 or 16 bytes) stays in it.  The cross-wave
-// reduction reuses the same memory after the streaming loop.
+// 64-lane store of a region (4 or 16 bytes per lane) stays in it.  The cross-wave reduction
+// reuses the same memory after the streaming loop.
 struct DecodeLds {
   uint32_t s_off, z_off, x_off, c_off, d_off, wave_bytes, staged, reduce, total;
 };
@@ -228,45 +228,73 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 // store_staged() writes them to the slice once they have arrived.  (Direct-to-LDS loads, the
 // obvious alternative, cost 0.35 - 1.5 us of issue time per launch at the Qwen3-8B decode
 // shapes on MI355X, growing with the waves per CU; register loads issue at once.)  At most
-// kStageS x 64 scale words, kStageZ x 64 zero words and kStageX x 64 activation chunks per
-// wave (decode_stage_fits()).  With NORM the activation slice is written by the norm
+// kStageS x 64 scale words, kStageZ x 64 zero words and kStageX x 64 activation chunks
+// per wave (decode_stage_fits()).  With NORM the activation slice is written by the norm
 // prologue instead.
-template <int TN, bool XL>
+// Prebuilt dequant operands (PRE) of one-tile workgroups come straight from one scale and
+// one zero word per lane and (item, column) entry -- the words of its own entry -- with no
+// round trip of the raw words through LDS: measured on MI355X 2-4 % faster for QKV and O at
+// M <= 4.  With more tiles the entries outnumber the contiguous words several times, and
+// the extra loads cost more than the round trip (gate_up M=1 +6 %, down M=4 +8 %).
+template <int TN, bool PRE>
+constexpr bool direct_entries() {
+  return PRE && TN == 1;
+}
+
+template <int TN, bool XL, bool PRE>
 struct StagedRegs {
-  uint32_t s[kStageS];
-  uint32_t z[kStageZ];
+  uint32_t s[direct_entries<TN, PRE>() ? kStageE : kStageS];  // scale words: contiguous, or per entry
+  uint32_t z[direct_entries<TN, PRE>() ? kStageE : kStageZ];  // zero words, likewise
   u32x4_t x[XL ? kStageX : 1];
 };
 
-template <int TN, bool XL, int W, bool NORM>
-__device__ __forceinline__ void load_staged(StagedRegs<TN, XL>& st, const DecodeSources& src, int M, int K, int N,
+template <int TN, bool XL, int W, bool NORM, bool PRE>
+__device__ __forceinline__ void load_staged(StagedRegs<TN, XL, PRE>& st, const DecodeSources& src, int M, int K, int N,
                                             int tb, int dt, int g_first, int n_items, int lane, uint32_t m_mul) {
-  constexpr int kSW = TN * 8;  // scale-pair words per group (8 per tile)
-  constexpr int kZW = TN * 2;  // zero words per group (2 per tile)
-  const int s_words = n_items * kSW;
+  if constexpr (direct_entries<TN, PRE>()) {
+    // entry e = (item, column c) of the single tile: the words holding column c's scale and zero
+    const int entries = n_items * 16;
 #pragma unroll
-  for (int u = 0; u < kStageS; ++u) {
-    if (u == 0 || 64 * u < s_words) {  // uniform
-      const int w = 64 * u + lane;
-      const int i = w / kSW;
-      const int j = w - i * kSW;
-      const int sj = tb * 8 + j + (j >= (TN / 2) * 8 ? dt * 8 : 0);
-      const uint32_t off =
-          w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + sj) * 4u : kOutOfRange;
-      st.s[u] = __builtin_amdgcn_raw_buffer_load_b32(src.s, off, 0, 0);
+    for (int u = 0; u < kStageE; ++u) {
+      if (u == 0 || 64 * u < entries) {  // uniform
+        const int e = 64 * u + lane;
+        const int col = kTileCols * tb + (e & 15);
+        const int g = g_first + (e >> 4) * W;
+        const bool ok = e < entries;
+        st.s[u] = __builtin_amdgcn_raw_buffer_load_b32(
+            src.s, ok ? static_cast<uint32_t>(g * N + (col & ~1)) * 2u : kOutOfRange, 0, 0);
+        st.z[u] = __builtin_amdgcn_raw_buffer_load_b32(
+            src.z, ok ? static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u : kOutOfRange, 0, 0);
+      }
     }
-  }
-  const int z_words = n_items * kZW;
+  } else {
+    constexpr int kSW = TN * 8;  // scale-pair words per group (8 per tile)
+    constexpr int kZW = TN * 2;  // zero words per group (2 per tile)
+    const int s_words = n_items * kSW;
 #pragma unroll
-  for (int u = 0; u < kStageZ; ++u) {
-    if (u == 0 || 64 * u < z_words) {
-      const int w = 64 * u + lane;
-      const int i = w / kZW;
-      const int j = w - i * kZW;
-      const int zj = tb * 2 + j + (j >= (TN / 2) * 2 ? dt * 2 : 0);
-      const uint32_t off =
-          w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
-      st.z[u] = __builtin_amdgcn_raw_buffer_load_b32(src.z, off, 0, 0);
+    for (int u = 0; u < kStageS; ++u) {
+      if (u == 0 || 64 * u < s_words) {  // uniform
+        const int w = 64 * u + lane;
+        const int i = w / kSW;
+        const int j = w - i * kSW;
+        const int sj = tb * 8 + j + (j >= (TN / 2) * 8 ? dt * 8 : 0);
+        const uint32_t off =
+            w < s_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 1) + sj) * 4u : kOutOfRange;
+        st.s[u] = __builtin_amdgcn_raw_buffer_load_b32(src.s, off, 0, 0);
+      }
+    }
+    const int z_words = n_items * kZW;
+#pragma unroll
+    for (int u = 0; u < kStageZ; ++u) {
+      if (u == 0 || 64 * u < z_words) {
+        const int w = 64 * u + lane;
+        const int i = w / kZW;
+        const int j = w - i * kZW;
+        const int zj = tb * 2 + j + (j >= (TN / 2) * 2 ? dt * 2 : 0);
+        const uint32_t off =
+            w < z_words ? static_cast<uint32_t>((g_first + i * W) * (N >> 3) + zj) * 4u : kOutOfRange;
+        st.z[u] = __builtin_amdgcn_raw_buffer_load_b32(src.z, off, 0, 0);
+      }
     }
   }
   if constexpr (XL && !NORM) {
@@ -292,19 +320,59 @@ __device__ __forceinline__ void load_staged(StagedRegs<TN, XL>& st, const Decode
   }
 }
 
+// Dequant operands of every (item, tile, column) entry of the wave, built once instead of
+// per tile and group in the loop (make_tile_scale depends on the lane only through lane % 4,
+// which equals the entry's column % 4 for every lane that later reads entry c).  It saves
+// about 12 VALU instructions per tile and group but puts an LDS round trip before the first
+// group: measured on MI355X it pays with 8 waves and a ring at least two groups deep
+// (gate_up M=16 -4 %), and costs 2-8 % with 4 waves or a one-group ring, where that
+// latency is not hidden.  From the staged raw words in LDS:
+template <int TN>
+__device__ __forceinline__ void build_tile_scales(uint8_t* wl, const DecodeLds& lay, int n_items, int lane) {
+  const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off);
+  const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off);
+  f32x4_t* lc = reinterpret_cast<f32x4_t*>(wl + lay.c_off);
+  s16x4_t* ld = reinterpret_cast<s16x4_t*>(wl + lay.d_off);
+  const int entries = n_items * TN * 16;
+  for (int e = lane; e < entries; e += 64) {
+    const int c = e & 15;
+    const int it = e >> 4;  // item * TN + tile
+    const uint32_t z = (lz[it * 2 + (c >> 3)] >> awq_shift(c & 7)) & 0xFu;
+    const TileScale t = make_tile_scale(ls[it * 8 + (c >> 1)], z, c);
+    lc[e] = t.cin;
+    ld[e] = t.diag;
+  }
+}
+
 // Lanes past a region's end write into its rounding (every region is a multiple of 64
-// words or 64 chunks).
-template <int TN, bool XL, bool NORM>
-__device__ __forceinline__ void store_staged(const StagedRegs<TN, XL>& st, uint8_t* wl, const DecodeLds& lay, int M,
+// words or 64 chunks).  With PRE the dequant operands are built here: from the lane's own
+// entry words (direct_entries), or from the raw words once they are in LDS.
+template <int TN, bool XL, bool NORM, bool PRE>
+__device__ __forceinline__ void store_staged(const StagedRegs<TN, XL, PRE>& st, uint8_t* wl, const DecodeLds& lay, int M,
                                              int n_items, int lane) {
-  const int s_words = n_items * TN * 8;
+  if constexpr (direct_entries<TN, PRE>()) {
+    const int entries = n_items * 16;
 #pragma unroll
-  for (int u = 0; u < kStageS; ++u)
-    if (u == 0 || 64 * u < s_words) reinterpret_cast<uint32_t*>(wl + lay.s_off)[64 * u + lane] = st.s[u];
-  const int z_words = n_items * TN * 2;
+    for (int u = 0; u < kStageE; ++u) {
+      const int e = 64 * u + lane;
+      if ((u == 0 || 64 * u < entries) && e < entries) {
+        const int c = e & 15;
+        const TileScale t = make_tile_scale(st.s[u], (st.z[u] >> awq_shift(c & 7)) & 0xFu, c);
+        reinterpret_cast<f32x4_t*>(wl + lay.c_off)[e] = t.cin;
+        reinterpret_cast<s16x4_t*>(wl + lay.d_off)[e] = t.diag;
+      }
+    }
+  } else {
+    const int s_words = n_items * TN * 8;
 #pragma unroll
-  for (int u = 0; u < kStageZ; ++u)
-    if (u == 0 || 64 * u < z_words) reinterpret_cast<uint32_t*>(wl + lay.z_off)[64 * u + lane] = st.z[u];
+    for (int u = 0; u < kStageS; ++u)
+      if (u == 0 || 64 * u < s_words) reinterpret_cast<uint32_t*>(wl + lay.s_off)[64 * u + lane] = st.s[u];
+    const int z_words = n_items * TN * 2;
+#pragma unroll
+    for (int u = 0; u < kStageZ; ++u)
+      if (u == 0 || 64 * u < z_words) reinterpret_cast<uint32_t*>(wl + lay.z_off)[64 * u + lane] = st.z[u];
+    if constexpr (PRE) build_tile_scales<TN>(wl, lay, n_items, lane);
+  }
   if constexpr (XL && !NORM) {
     const int chunks = n_items * M * 16;
 #pragma unroll
@@ -406,30 +474,6 @@ __device__ __forceinline__ void norm_rows(const NormRegs<NR>& nr, uint8_t* wl, c
   }
 }
 
-// Dequant operands of every (item, tile, column) of the wave, built once from the staged
-// scale pairs and zero words: one lane per column instead of every lane per tile and group
-// (make_tile_scale depends on the lane only through lane % 4, which equals the column's
-// c % 4 for every lane that later reads entry c).  It saves about 12 VALU instructions per
-// tile and group but puts LDS round trips before the first group: measured on MI355X it
-// pays with 8 waves and a ring at least two groups deep (gate_up M=16 -4 %), and costs
-// 2-8 % with 4 waves or a one-group ring, where that latency is not hidden.
-template <int TN>
-__device__ __forceinline__ void build_tile_scales(uint8_t* wl, const DecodeLds& lay, int n_items, int lane) {
-  const uint32_t* ls = reinterpret_cast<const uint32_t*>(wl + lay.s_off);
-  const uint32_t* lz = reinterpret_cast<const uint32_t*>(wl + lay.z_off);
-  f32x4_t* lc = reinterpret_cast<f32x4_t*>(wl + lay.c_off);
-  s16x4_t* ld = reinterpret_cast<s16x4_t*>(wl + lay.d_off);
-  const int entries = n_items * TN * 16;
-  for (int e = lane; e < entries; e += 64) {
-    const int c = e & 15;
-    const int it = e >> 4;  // item * TN + tile
-    const uint32_t z = (lz[it * 2 + (c >> 3)] >> awq_shift(c & 7)) & 0xFu;
-    const TileScale t = make_tile_scale(ls[it * 8 + (c >> 1)], z, c);
-    lc[e] = t.cin;
-    ld[e] = t.diag;
-  }
-}
-
 template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
@@ -481,8 +525,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // The wave's groups: gi = wave + i W of the K range, i < n_items.
   const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
   uint8_t* wl = lds + wave * lay.wave_bytes;
-  StagedRegs<TN, XL> staged;
-  load_staged<TN, XL, W, NORM>(staged, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
+  StagedRegs<TN, XL, kPre> staged;
+  load_staged<TN, XL, W, NORM, kPre>(staged, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
   NormRegs<(NR > 0 ? NR : 1)> nr;
   if constexpr (NORM)
     load_norm_operands<W>(nr, src, make_buffer(nrm.res, nrm.res ? geo.x_bytes : 0u),
@@ -500,10 +544,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // The staged operands go to LDS as soon as they arrive (the ring's loads stay in flight:
   // the compiler waits for each register load individually), then the norm prologue works
   // from its registers and writes the activation slice.
-  store_staged<TN, XL, NORM>(staged, wl, lay, M, n_items, lane);
+  store_staged<TN, XL, NORM, kPre>(staged, wl, lay, M, n_items, lane);
   if constexpr (NORM)
     norm_rows<W>(nr, wl, lay, norm_part, wave, lane, M, K, g_begin + wave, n_items, blockIdx.x == 0 && sidx == 0, nrm);
-  if constexpr (kPre) build_tile_scales<TN>(wl, lay, n_items, lane);
 
   const NibbleConsts nib = nibble_consts();
   for (int base = 0; base < n_items; base += DEPTH) {
@@ -617,11 +660,13 @@ bool decode_stages_x(int M, int K, int split) {
   return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
 }
 
-bool decode_stage_fits(int M, int K, int tn, int waves, int split) {
+bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split) {
   const int G = K / kGroup;
   const int items = ((G + split - 1) / split + waves - 1) / waves;
-  return items * tn * 8 <= 64 * kStageS && items * tn * 2 <= 64 * kStageZ &&
-         (!decode_stages_x(M, K, split) || items * M * 16 <= 64 * kStageX);
+  const bool sz = (tn == 1 && decode_prebuilt_scales(waves, depth))
+                      ? items * 16 <= 64 * kStageE
+                      : items * tn * 8 <= 64 * kStageS && items * tn * 2 <= 64 * kStageZ;
+  return sz && (!decode_stages_x(M, K, split) || items * M * 16 <= 64 * kStageX);
 }
 
 size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
@@ -647,7 +692,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
   const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
-  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, a.split))
+  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split))
     return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated

@@ -37,11 +37,14 @@ constexpr size_t kDecodeMaxStagedX = 32 * 1024;  // activations staged in LDS (M
 // Whether the activations of an (M, K, split) problem are staged in LDS.
 bool decode_stages_x(int M, int K, int split);
 // Register staging of a decode wave's scale words, zero words and (staged rows) activation
-// chunks: at most this many 64-lane loads of each per launch.
+// chunks: at most this many 64-lane loads of each per launch (one-tile workgroups with
+// prebuilt dequant operands: one scale and one zero word per (group, column) entry, at most
+// kStageE loads of each).
 constexpr int kStageS = 3;
 constexpr int kStageZ = 1;
 constexpr int kStageX = 4;
-bool decode_stage_fits(int M, int K, int tn, int waves, int split);
+constexpr int kStageE = 4;
+bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split);
 // Whether a decode configuration builds its dequant operands once per wave in LDS
 // (8 waves and a ring at least two groups deep) instead of per tile and group.
 constexpr bool decode_prebuilt_scales(int waves, int depth) { return waves == 8 && depth >= 2; }
