@@ -237,12 +237,16 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
   if (!o.active || wk != 0) return;
   // Epilogue (slice 0): bf16 through LDS (row-major 16 WM rows x the wave's output columns:
   // rows of CPR 16-byte chunks swizzled by row), then 16-byte coalesced stores.  The stages
-  // are free after the last barrier.
+  // are free after the last barrier.  When they cannot hold every wave's columns at once, a
+  // wave writes and stores its columns in two passes through half the space (wave-local).
   constexpr int WR = 16 * WM;  // rows of a wave
-  constexpr int kStageRows = kStage / (WR * 32 * TW);
+  constexpr int kFull = WR * 32 * TW;
+  constexpr int kParts = (kStage / kFull) * S >= NWG ? 1 : 2;
+  constexpr int kRegion = kFull / kParts;
+  constexpr int kStageRows = kStage / kRegion;
   static_assert(kStageRows >= 1 && kStageRows * S >= NWG, "epilogue staging exceeds the stages");
-  uint8_t* ep = stage(wave_in / kStageRows) + (wave_in % kStageRows) * (WR * 32 * TW);
-  auto store_rows = [&](auto cpr_tag) {
+  uint8_t* ep = stage(wave_in / kStageRows) + (wave_in % kStageRows) * kRegion;
+  auto store_rows = [&](auto cpr_tag, int col0) {
     constexpr int CPR = decltype(cpr_tag)::value;
     constexpr int PITCH = 16 * CPR;
     constexpr int kRowsPerRound = 64 / CPR;
@@ -255,42 +259,54 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
       const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + ((q ^ (r % CPR)) << 4));
       const int row = o.row_w + r;
       if (row < o.M) {
-        const size_t off = static_cast<size_t>(row) * o.n_out + o.col_w + 8 * q;
+        const size_t off = static_cast<size_t>(row) * o.n_out + col0 + 8 * q;
         *reinterpret_cast<uint4*>(o.y + off) = o.res ? add_bf16x8(v, *reinterpret_cast<const uint4*>(o.res + off)) : v;
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);  // the region's reads are done before the next pass writes it
+    __builtin_amdgcn_wave_barrier();
   };
   if (!o.act) {
-    constexpr int CPR = 2 * TW;  // 16-byte chunks per row
+    constexpr int TP = TW / kParts;  // tiles per pass
+    constexpr int CPR = 2 * TP;      // 16-byte chunks per row
     constexpr int PITCH = 16 * CPR;
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
+    for (int part = 0; part < kParts; ++part) {
 #pragma unroll
-      for (int tt = 0; tt < TW; ++tt)
+      for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * mt + 4 * (lane >> 4) + i;
-          const int c = 16 * tt + (lane & 15);
-          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
-          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][tt][i]);
-        }
-    store_rows(std::integral_constant<int, CPR>{});
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mt + 4 * (lane >> 4) + i;
+            const int c = 16 * t + (lane & 15);
+            const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+            *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[mt][part * TP + t][i]);
+          }
+      store_rows(std::integral_constant<int, CPR>{}, o.col_w + 16 * TP * part);
+    }
   } else {
     constexpr int H = TW / 2;
-    constexpr int CPR = TW;  // half the columns
+    constexpr int TP = (H % kParts == 0) ? H / kParts : H;  // gate tiles per pass
+    constexpr int NP = H / TP;
+    constexpr int CPR = 2 * TP;
     constexpr int PITCH = 16 * CPR;
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
+    for (int part = 0; part < NP; ++part) {
 #pragma unroll
-      for (int tt = 0; tt < H; ++tt)
+      for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * mt + 4 * (lane >> 4) + i;
-          const int c = 16 * tt + (lane & 15);
-          const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
-          *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul(acc[mt][tt][i], acc[mt][tt + H][i]));
-        }
-    store_rows(std::integral_constant<int, CPR>{});
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mt + 4 * (lane >> 4) + i;
+            const int c = 16 * t + (lane & 15);
+            const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
+            const int tt = part * TP + t;
+            *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul(acc[mt][tt][i], acc[mt][tt + H][i]));
+          }
+      store_rows(std::integral_constant<int, CPR>{}, o.col_w + 16 * TP * part);
+    }
   }
 }
 

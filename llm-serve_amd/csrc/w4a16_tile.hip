@@ -217,6 +217,7 @@ TileShape tile_shape(int shape) {
     case 5: return TileShape{2, 1, 4, 2};  // 8 waves: 2 K slices x 4 along N, 32 columns each
     case 6: return TileShape{2, 1, 2, 2};  // 4 waves: 2 K slices x 2 along N, 32 columns each
     case 7: return TileShape{2, 1, 1, 4};  // 4 waves: 4 K slices x 32 columns
+    case 8: return TileShape{4, 1, 8, 1};  // 8 waves along N, 64 columns each
     default: return TileShape{4, 1, 4, 1};  // 4 waves along N, 64 columns each
   }
 }
@@ -227,7 +228,7 @@ TileShape tile_shape(int shape) {
   X(4, 4, 1, 4, 1, 1) X(4, 4, 1, 4, 2, 1) X(8, 4, 1, 4, 1, 1) X(4, 4, 2, 4, 2, 1) X(4, 2, 1, 8, 2, 1)  \
   X(8, 2, 1, 8, 2, 1)                                                                         \
   X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
-  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4)
+  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);
