@@ -40,15 +40,22 @@ __device__ __forceinline__ TileCoord tile_coord(int b, int m_blocks, int n_block
   return TileCoord{sidx, grp * kGroupM + in_grp % gm, in_grp / gm};
 }
 
+// The scale pair word and the AutoAWQ zero word holding the lane's column, per tile of a
+// wave, for one group.
+template <int TW>
+struct GroupScales {
+  uint32_t s[TW], zw[TW];
+};
+
 // Raw loads of one group for a wave's TW layout tiles: one 16-byte weight load per tile,
-// and the scale-pair and zero words of the lane's column in each tile.  Decoding waits
+// and (LOAD_SC) the scale-pair and zero words of the lane's column in each tile -- else those
+// come from the workgroup's LDS stage (issue_sz_stage, read_group_scales).  Decoding waits
 // until the group is consumed.  An invalid group (past the K range, or a wave whose columns
 // lie past N) fetches nothing.
 template <int TW>
 struct BGroup {
   u32x4_t w[TW];
-  uint32_t s[TW];   // bf16 scale pair holding the lane's column
-  uint32_t zw[TW];  // AutoAWQ zero word holding the lane's column
+  GroupScales<TW> sc;
 };
 
 struct BSources {
@@ -57,7 +64,7 @@ struct BSources {
 
 // The wave's tiles are t0 + tt, plus dt for tt >= TW / 2 (dt = 0 for the plain GEMM; for
 // the fused gate/up product the second half are the up tiles of the first half's gate tiles).
-template <int TW>
+template <int TW, bool LOAD_SC>
 __device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src, int g, bool valid, int N, int t0,
                                              int dt, int lane) {
   const int NT = N / kTileCols;
@@ -68,10 +75,87 @@ __device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src,
     const int t = t0 + tt + (tt >= TW / 2 ? dt : 0);
     const uint32_t wo = valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : kOutOfRange;
     b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
-    const int col = kTileCols * t + c;
-    b.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
-    b.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u),
-                                                    0, 0);
+    if constexpr (LOAD_SC) {
+      const int col = kTileCols * t + c;
+      b.sc.s[tt] =
+          __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
+      b.sc.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(
+          src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u), 0, 0);
+    }
+  }
+}
+
+// Scale and zero staging of a tile workgroup.  Per group, the workgroup's BN columns are two
+// ranges of BN / 2 columns starting at cs0 and cs1: the gate and up halves of the fused
+// product, or the two halves of a plain column block.  Their bf16 scales (BN / 8 chunks of
+// 16 bytes, range 0 first) go to bytes [0, 2 BN) of the group's LDS stage and their zero
+// words (kSzZeroChunks 16-byte chunks of 32 columns per range) to bytes [1024, 2048), each
+// by one direct-to-LDS load instruction per group for the whole workgroup -- in place of
+// two 4-byte loads per tile and wave, which cost the prefill kernel 16 % of its time.  (With
+// four K slices, each stage serves only two waves, and the per-wave loads measured faster.)
+constexpr int kSzStageBytes = 2048;
+constexpr int kSzZeroBase = 1024;
+template <int BN>
+constexpr int sz_zero_chunks() { return (BN + 63) / 64; }
+
+// Instruction `which` (0: scales, 1: zero words) of group g's stage, on the lanes that have
+// a chunk.  An invalid group fetches nothing (zeros).
+template <int BN>
+__device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz, int g, bool valid, int N, int cs0,
+                                               int cs1, int which, int lane) {
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  static_assert(BN % 32 == 0 && BN / 8 <= 64, "one instruction holds the scales of the column block");
+  if (which == 0) {
+    constexpr int kHalf = BN / 16;  // 16-byte chunks of one range
+    const int r = lane >= kHalf;
+    const int col = (r ? cs1 : cs0) + 8 * (lane - r * kHalf);
+    const uint32_t off = valid ? (static_cast<uint32_t>(g) * N + static_cast<uint32_t>(col)) * 2u : kOutOfRange;
+    if (lane < 2 * kHalf) __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)sz, 16, off, 0, 0, 0);
+  } else {
+    constexpr int kZc = sz_zero_chunks<BN>();
+    const int r = lane >= kZc;
+    const int col = (r ? cs1 : cs0) + 32 * (lane - r * kZc);
+    const uint32_t off =
+        valid ? (static_cast<uint32_t>(g) * (N >> 3) + static_cast<uint32_t>(col >> 3)) * 4u : kOutOfRange;
+    if (lane < 2 * kZc) __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(sz + kSzZeroBase), 16, off, 0, 0, 0);
+  }
+}
+
+// LDS byte offsets, within a group's scale/zero stage, of the scale pair word and the zero
+// word holding the lane's column of each of the wave's tiles.  Plain: the wave's columns are
+// [16 TW wn, 16 TW (wn + 1)) of the block; fused: gate columns [8 TW wn, 8 TW (wn + 1)) of
+// range 0 and the same up columns of range 1.
+template <int TW, int BN>
+struct SzOffsets {
+  uint32_t s[TW], z[TW];
+  __device__ __forceinline__ SzOffsets(bool act, int wn, int lane) {
+    const int c = lane & 15;
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      int r, u;
+      if (act) {
+        r = tt >= TW / 2;
+        u = 8 * TW * wn + 16 * (tt - r * (TW / 2));
+      } else {
+        const int p = 16 * TW * wn + 16 * tt;
+        r = p >= BN / 2;
+        u = p - r * (BN / 2);
+      }
+      s[tt] = static_cast<uint32_t>(BN * r + 2 * u + 2 * (c & ~1));
+      z[tt] = static_cast<uint32_t>(kSzZeroBase + 16 * sz_zero_chunks<BN>() * r + 4 * (u >> 3) + 4 * (c >> 3));
+    }
+  }
+};
+
+// The scale pair and zero words of the lane's columns in one group's stage.  Read right
+// after the batch barrier, ahead of the next batch's load issue, so that their latency is
+// not on the path into the group's first dequant.
+template <int TW, int BN>
+__device__ __forceinline__ void read_group_scales(GroupScales<TW>& gs, const uint8_t* sz, const SzOffsets<TW, BN>& szo) {
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt) {
+    gs.s[tt] = *reinterpret_cast<const uint32_t*>(sz + szo.s[tt]);
+    gs.zw[tt] = *reinterpret_cast<const uint32_t*>(sz + szo.z[tt]);
   }
 }
 
@@ -89,7 +173,7 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
   const int zshift = awq_shift(lane & 7);
   TileScale ts[TW];
 #pragma unroll
-  for (int tt = 0; tt < TW; ++tt) ts[tt] = make_tile_scale(b.s[tt], (b.zw[tt] >> zshift) & 0xFu, lane);
+  for (int tt = 0; tt < TW; ++tt) ts[tt] = make_tile_scale(b.sc.s[tt], (b.sc.zw[tt] >> zshift) & 0xFu, lane);
   auto read_a = [&](bf16x8_t (&a)[WM], int j) {
     const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 15);  // row & 15 == lane & 15
     const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;

@@ -13,8 +13,10 @@
 // buffer loads, one or two groups per batch with the next batch in flight while one is
 // computed, in a row-major layout whose sixteen 16-byte chunks per row are XOR-swizzled by
 // (row & 15): the 16 lanes reading one fragment chunk (16 consecutive rows) then hit 16
-// different chunk positions, i.e. all 64 LDS banks once.  The weights, scales and zeros of
-// those groups travel in a matching ring of registers.
+// different chunk positions, i.e. all 64 LDS banks once.  The scales and zero words of the
+// workgroup's columns for those groups are staged beside them (two direct-to-LDS loads per
+// group for the whole workgroup, issue_sz_stage), and the weights travel in a matching ring
+// of registers.
 //
 // K split inside the workgroup (WK > 1, for short and mid-sized M on narrow layers): the
 // workgroup's waves form WK slices of NWM x NWN waves; slice k computes the groups k, k + WK,
@@ -84,6 +86,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   constexpr int BN = 16 * TW * NWN;
   constexpr int NI = BM / (4 * NW);  // activation-stage instructions per wave
   static_assert(NI * 4 * NW == BM, "the activation stage must split evenly over the waves");
+  static_assert(NW >= 2, "a group's scale and zero loads are issued by two waves");
   constexpr int kStage = BM * kARowBytes;
   constexpr int P = tile_batch(BM, TW, OCC, WK);  // groups per load batch
   constexpr int S = 2 * P;                        // LDS stages: two batches
@@ -104,6 +107,9 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
     return st == 0 ? stage0 : st == 1 ? stage1 : st == 2 ? stage2 : st == 3 ? stage3
          : st == 4 ? stage4 : st == 5 ? stage5 : st == 6 ? stage6 : stage7;
   };
+  // Scales and zero words of stage i's group in LDS (kStageSZ), or in the register ring.
+  constexpr bool kStageSZ = WK <= 2;
+  __shared__ __attribute__((aligned(16))) uint8_t sz_stage[kStageSZ ? S : 1][kStageSZ ? kSzStageBytes : 16];
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63;
@@ -129,6 +135,10 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   const int t0 = col_w / kTileCols;
   const int dt = act ? up_tiles - TW / 2 : 0;
   const bool active = col_w < n_out;  // wave-uniform (n_out % 64 == 0): the last n-block may be partly past it
+  // The workgroup's two column ranges of BN / 2 (scale and zero staging).
+  const int cs0 = act ? nbk * (BN / 2) : nbk * BN;
+  const int cs1 = act ? cs0 + up_tiles * kTileCols : cs0 + BN / 2;
+  const SzOffsets<TW, BN> szo(act, wn, lane);
 
   f32x4_t acc[WM][TW];
 #pragma unroll
@@ -156,12 +166,18 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   BGroup<TW> ring[2 * PW];
   auto issue = [&](int half, int b) {  // batch starting at item b into half `half`
 #pragma unroll
-    for (int q = 0; q < P; ++q)
+    for (int q = 0; q < P; ++q) {
       issue_a_stage<NI, NW>(rx, stage(half * P + q), row0, M, K, g_begin + b + q, b + q < n_items, wave, lane);
+      // the group's scale and zero instructions go to waves 2q and 2q + 1 (mod NW)
+      if (kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
+        issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], g_begin + b + q, b + q < n_items, N, cs0,
+                           cs1, wave == (2 * q) % NW ? 0 : 1, lane);
+    }
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
       const int item = b + wk + WK * j;
-      load_b_group<TW>(ring[half * PW + j], bsrc, g_begin + item, item < n_items && active, N, t0, dt, lane);
+      load_b_group<TW, !kStageSZ>(ring[half * PW + j], bsrc, g_begin + item, item < n_items && active, N, t0, dt,
+                                  lane);
     }
   };
   issue(0, 0);
@@ -176,6 +192,12 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
         __builtin_amdgcn_s_waitcnt(kWaitAll);  // batch b's LDS and register loads have landed
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kStageSZ) {
+#pragma unroll
+          for (int j = 0; j < PW; ++j)  // the wave's groups of the batch: items b + wk + WK j
+            read_group_scales<TW, BN>(ring[h * PW + j].sc, sz_stage[h * P + wk + WK * j], szo);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         issue(1 - h, b + P);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

@@ -123,6 +123,36 @@ def test_every_tile_configuration(gpu_lib, m, n):
             assert int(torch.count_nonzero(ws[:65536])) == 0
 
 
+def test_scales_and_zeros_at_word_alignment(gpu_lib):
+    """The API asks only 4-byte alignment of scales and qzeros, while both kernels fetch them
+    in 16-byte chunks: every tile kernel, and the planner's decode and tile plans, give the
+    same bits for tensors 4 bytes past a 16-byte boundary as for aligned ones."""
+    m, k, n = 200, 1024, 512
+    p = ora.make_problem(seed=77, m=m, k=k, n=n)
+    t = to_gpu(p)
+    packed = awq_mod().repack_awq_qweight(t["qweight"])
+    s_buf = torch.zeros(t["scales"].numel() + 8, dtype=torch.bfloat16, device="cuda")
+    z_buf = torch.zeros(t["qzeros"].numel() + 4, dtype=torch.int32, device="cuda")
+    s_off = s_buf[2:2 + t["scales"].numel()].view(t["scales"].shape)
+    z_off = z_buf[1:1 + t["qzeros"].numel()].view(t["qzeros"].shape)
+    s_off.copy_(t["scales"])
+    z_off.copy_(t["qzeros"])
+    assert s_off.data_ptr() % 16 == 4 and z_off.data_ptr() % 16 == 4
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    for wm, shape, occ in TILE_KERNELS:
+        ys = []
+        for s, z in ((t["scales"], t["qzeros"]), (s_off, z_off)):
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+            gpu_lib.gemm_config(t["x"], packed, z, s, y, k, n, 2, wm, occ, 1, ws, p2=shape)
+            ys.append(y)
+        assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16)), (wm, shape, occ)
+    for rows in (1, 16, 200):
+        x = t["x"][:rows]
+        a = awq_mod().awq_linear(x, packed, t["qzeros"], t["scales"], group_size=128, workspace=ws)
+        b = awq_mod().awq_linear(x, packed, z_off, s_off, group_size=128, workspace=ws)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), rows
+
+
 def test_shared_workspace_across_shapes_and_m(gpu_lib):
     """One workspace reused by calls of different M and N (as the per-stream pool does):
     the counters must always be found re-armed."""
