@@ -156,18 +156,20 @@ GemmPlan plan_mid(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_TILE, wm, 2, shape, split};
 }
 
-// 256 < M <= 1024 (chunked-prefill chunks and mixed batches), 128-row tiles unless they leave
-// too few workgroups: 256 columns (shape 3) when that grid alone has >= 144 workgroups (wide
-// layers only from M = 768), else 128 columns (shape 5, 2 K slices), K split in two or more
-// for long K while the grid is below 144 workgroups; short-K narrow layers switch to 64-row
-// tiles of 128 columns instead of splitting K.  From a sweep of every tile configuration at
-// M = 384, 512, 768, 1024: within 3.5 % of the best at every point, up to 10 % faster than the
-// 256-column tiles with K split used before (O M=512: 25.9 vs 28.8 us, gate_up M=512: 122 vs
-// 128 us).
+// 256 < M <= 1024 (chunked-prefill chunks and mixed batches): wide layers up to M = 768 take
+// 64-row tiles of 256 columns, two workgroups per CU (shape 1; gate_up M = 384 / 512 / 768:
+// 108 / 110 / 173 us against 113 / 117 / 187 us for 128-row tiles); otherwise 128-row tiles
+// unless they leave too few workgroups: 256 columns (shape 3) when that grid alone has >= 144
+// workgroups, else 128 columns (shape 5, 2 K slices), K split in two or more for long K while
+// the grid is below 144 workgroups; short-K narrow layers switch to 64-row tiles of 128
+// columns instead of splitting K.  From sweeps of every tile configuration at M = 384, 512,
+// 768, 1024: within 6 % of the best at every point (K splits that would need more than the
+// 16 MiB of partials of down at M = 512 left out).
 GemmPlan plan_large(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
+  if (N >= 16384 && M <= 768) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   const int t3 = ceil_div(M, 128) * ceil_div(N, 256);
-  if (t3 >= 144 && !(N >= 16384 && M <= 512)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
+  if (t3 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
   const int t5 = ceil_div(M, 128) * ceil_div(N, 128);
   if (t5 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 5, 1};
   int split = 1;
@@ -180,10 +182,11 @@ GemmPlan plan_large(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_TILE, 4, 2, 5, split};
 }
 
-// Beyond M = 1024 (whole prefill chunks): on wide layers, 128-row tiles of 512 columns
-// (shape 8: 8 waves of 128 x 64) when their grid fills the CUs in even rounds -- every
-// activation row is then re-read from L2 by half as many workgroups (gate_up M=2048: 768
-// workgroups, 4.7 % faster than 256 columns, bit-identical); else 128-row tiles of 256
+// Beyond M = 1024 (whole prefill chunks): 128-row tiles of 512 columns (shape 8: 8 waves of
+// 128 x 64) when their grid fills the CUs in even rounds (wide layers: or >= 4 rounds) --
+// every activation row is then re-read from L2 by half as many workgroups (gate_up M=2048:
+// 768 workgroups, 4.7 % faster than 256 columns, bit-identical; O and down at M = 4096: 119
+// and 328 us against 131 and 355 us); else 128-row tiles of 256
 // columns (shape 3: every dequantized weight serves 128 rows) when their grid fills the CUs
 // in even rounds (gate_up at M = 1024, O and down at M = 2048), or fills 144 .. 256 of one
 // round's workgroups once K is split in two or four with >= 16 groups per split; otherwise
@@ -194,7 +197,7 @@ GemmPlan plan_tile(int M, int K, int N) {
   if (M <= 1024) return plan_large(M, K, N);
   const int G = K / w4a16::kGroup;
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
-  if (N >= 16384 && t9 >= 256 && (t9 % 256 == 0 || t9 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
+  if (t9 >= 256 && (t9 % 256 == 0 || (N >= 16384 && t9 >= 1024))) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
   if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
   int s8 = 1;
