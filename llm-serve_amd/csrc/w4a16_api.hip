@@ -138,6 +138,15 @@ GemmPlan plan_decode(int M, int K, int N) {
 // tiles of 256 columns used before; QKV M=64: 12.7 vs 16.1 us for the decode kernel).
 GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
+  // Layers whose width is a multiple of 96 columns (QKV: 6144) above M = 64: 12-wave
+  // workgroups of 96 columns (shape 9: 4 K slices x 3 waves along N, three waves per SIMD),
+  // 32-row tiles up to M = 128 and 64-row tiles beyond, when that grid has >= 192
+  // workgroups (QKV M = 72 .. 128: 16.4 - 16.5 us against 17.9 - 18.1 us; M = 160 .. 256:
+  // 22.9 - 23.2 against 24.7 - 24.9 us).
+  if (N < 16384 && K < 8192 && N % 96 == 0 && M > 64) {
+    const int wm9 = M <= 128 ? 2 : 4;
+    if (ceil_div(M, 16 * wm9) * (N / 96) >= 192) return GemmPlan{W4A16_REGIME_TILE, wm9, 3, 9, 1};
+  }
   int wm, shape, split = 1;
   if (N >= 16384) {
     if (M <= 64) { wm = 4; shape = 5; }
@@ -668,8 +677,8 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
     if (p0 != 2 && p0 != 4 && p0 != 8) return fail(W4A16_ERR_ARG, "tile wm must be 2, 4 or 8");
-    if (p2 < 0 || p2 > 8) return fail(W4A16_ERR_ARG, "tile shape code must be 0..8");
-    if (p1 != 1 && p1 != 2) return fail(W4A16_ERR_ARG, "tile occupancy must be 1 or 2");
+    if (p2 < 0 || p2 > 9) return fail(W4A16_ERR_ARG, "tile shape code must be 0..9");
+    if (p1 < 1 || p1 > 3) return fail(W4A16_ERR_ARG, "tile occupancy must be 1, 2 or 3");
     if (!w4a16::tile_config_compiled(p0, p2, p1))
       return fail(W4A16_ERR_ARG, "tile configuration wm %d, shape %d, occupancy %d is not compiled", p0, p2, p1);
   } else {
@@ -703,7 +712,7 @@ size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split)
   // Tile regime: enough for every tile shape (taller or wider tiles pad more).
   size_t most = workspace_for(GemmPlan{regime, p0, 0, 1, split}, M, N);
   if (regime != W4A16_REGIME_TILE) return most;
-  for (int shape = 2; shape <= 8; ++shape) {
+  for (int shape = 2; shape <= 9; ++shape) {
     const size_t b = workspace_for(GemmPlan{regime, p0, 0, shape, split}, M, N);
     most = b > most ? b : most;
   }

@@ -40,23 +40,28 @@ namespace w4a16 {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Issue the direct-to-LDS loads of activation rows [row0, row0 + 4 NI NW) x group g into
-// `stage` (NW waves, NI instructions each).  Instruction i of wave w fills rows
-// 4 (NW i + w) .. +3 (1 KiB); lane -> (row, physical chunk).  An invalid group (past the
+// Issue the direct-to-LDS loads of activation rows [row0, row0 + BM) x group g into `stage`
+// (NW waves, NI instructions each).  Instruction i of wave w fills rows 4 (NW i + w) .. +3
+// (1 KiB); lane -> (row, physical chunk).  When the BM / 4 row quads do not split evenly over
+// the waves, the instructions past them fetch nothing into `spare` (1 KiB of LDS no one
+// reads), so that every wave issues the same NI loads.  An invalid group (past the
 // workgroup's K range) fetches nothing.
-template <int NI, int NW>
-__device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t* stage, int row0, int M, int K,
-                                              int g, bool valid, int wave, int lane) {
+template <int NI, int NW, int BM>
+__device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t* stage, uint8_t* spare, int row0,
+                                              int M, int K, int g, bool valid, int wave, int lane) {
   const int p = lane & 15;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int r = 4 * (NW * i + wave) + (lane >> 4);
+    const int quad = NW * i + wave;
+    const bool in = NI * NW * 4 == BM || quad < BM / 4;  // wave-uniform
+    const int r = 4 * quad + (lane >> 4);
     const int c = p ^ (r & 15);
     int row = row0 + r;
     row = row < M ? row : M - 1;  // rows past M load a valid row; their outputs are dropped
-    const uint32_t off =
-        valid ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + kGroup * g + 8u * c) * 2u : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(stage + 4 * (NW * i + wave) * kARowBytes), 16, off,
+    const uint32_t off = valid && in
+                             ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + kGroup * g + 8u * c) * 2u
+                             : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(in ? stage + quad * 4 * kARowBytes : spare), 16, off,
                                              0, 0, 0);
   }
 }
@@ -68,8 +73,9 @@ constexpr int tile_batch(int bm, int tw, int occ, int wk) {
   return wk > 1 ? wk : (4 * bm * kARowBytes <= 128 * 1024 && (tw == 2 || occ == 1) ? 2 : 1);
 }
 
-// OCC = waves per SIMD the register allocation must allow (1 or 2; 8-wave workgroups
-// always put two waves on every SIMD).  WK = K slices inside the workgroup.
+// OCC = waves per SIMD the register allocation must allow (1, 2 or 3; 8-wave workgroups
+// always put two waves on every SIMD, 12-wave ones three).  WK = K slices inside the
+// workgroup.
 template <int WM, int TW, int NWM, int NWN, int OCC, int WK>
 __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const uint16_t* __restrict__ x,
                                                                    const uint32_t* __restrict__ packed,
@@ -84,8 +90,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   constexpr int NW = NWG * WK;    // waves per workgroup
   constexpr int BM = 16 * WM * NWM;
   constexpr int BN = 16 * TW * NWN;
-  constexpr int NI = BM / (4 * NW);  // activation-stage instructions per wave
-  static_assert(NI * 4 * NW == BM, "the activation stage must split evenly over the waves");
+  constexpr int NI = (BM / 4 + NW - 1) / NW;  // activation-stage instructions per wave
+  static_assert(BM % 4 == 0, "activation stages hold whole row quads");
   static_assert(NW >= 2, "a group's scale and zero loads are issued by two waves");
   constexpr int kStage = BM * kARowBytes;
   constexpr int P = tile_batch(BM, TW, OCC, WK);  // groups per load batch
@@ -110,6 +116,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   // Scales and zero words of stage i's group in LDS (kStageSZ), or in the register ring.
   constexpr bool kStageSZ = WK <= 2;
   __shared__ __attribute__((aligned(16))) uint8_t sz_stage[kStageSZ ? S : 1][kStageSZ ? kSzStageBytes : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t spare[NI * NW * 4 == BM ? 16 : 1024];  // uneven stage issue
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63;
@@ -167,7 +174,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   auto issue = [&](int half, int b) {  // batch starting at item b into half `half`
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-      issue_a_stage<NI, NW>(rx, stage(half * P + q), row0, M, K, g_begin + b + q, b + q < n_items, wave, lane);
+      issue_a_stage<NI, NW, BM>(rx, stage(half * P + q), spare, row0, M, K, g_begin + b + q, b + q < n_items, wave,
+                                lane);
       // the group's scale and zero instructions go to waves 2q and 2q + 1 (mod NW)
       if (kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
         issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], g_begin + b + q, b + q < n_items, N, cs0,
@@ -240,6 +248,7 @@ TileShape tile_shape(int shape) {
     case 6: return TileShape{2, 1, 2, 2};  // 4 waves: 2 K slices x 2 along N, 32 columns each
     case 7: return TileShape{2, 1, 1, 4};  // 4 waves: 4 K slices x 32 columns
     case 8: return TileShape{4, 1, 8, 1};  // 8 waves along N, 64 columns each
+    case 9: return TileShape{2, 1, 3, 4};  // 12 waves: 4 K slices x 3 along N, 32 columns each
     default: return TileShape{4, 1, 4, 1};  // 4 waves along N, 64 columns each
   }
 }
@@ -250,7 +259,7 @@ TileShape tile_shape(int shape) {
   X(4, 4, 1, 4, 1, 1) X(4, 4, 1, 4, 2, 1) X(8, 4, 1, 4, 1, 1) X(4, 4, 2, 4, 2, 1) X(4, 2, 1, 8, 2, 1)  \
   X(8, 2, 1, 8, 2, 1)                                                                         \
   X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
-  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1)
+  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);

@@ -128,10 +128,10 @@ def test_forced_config_validation(pkg):
     assert f(p, p, p, p, p, 64, 4096, 6144, 128, 1, 3, 4, 4, 1, None, 0, None) == 1  # ring registers
     assert "registers" in L.last_error()
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 12, 1, 2, 1, None, 0, None) == 1  # bad wm
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 3, 2, 1, None, 0, None) == 1  # bad occupancy
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 4, 2, 1, None, 0, None) == 1  # bad occupancy
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 2, 2, 3, 1, None, 0, None) == 1  # wm 2 x shape 3: not compiled
     assert "not compiled" in L.last_error()
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 9, 1, None, 0, None) == 1  # bad tile shape code
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 10, 1, None, 0, None) == 1  # bad tile shape code
     assert "shape" in L.last_error()
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 2, 1, None, 0, None) == 1  # bad regime
     # split > 1 without workspace
