@@ -248,7 +248,8 @@ TileShape tile_shape(int shape) {
     case 6: return TileShape{2, 1, 2, 2};  // 4 waves: 2 K slices x 2 along N, 32 columns each
     case 7: return TileShape{2, 1, 1, 4};  // 4 waves: 4 K slices x 32 columns
     case 8: return TileShape{4, 1, 8, 1};  // 8 waves along N, 64 columns each
-    case 9: return TileShape{2, 1, 3, 4};  // 12 waves: 4 K slices x 3 along N, 32 columns each
+    case 9: return TileShape{2, 1, 3, 4};   // 12 waves: 4 K slices x 3 along N, 32 columns each
+    case 10: return TileShape{2, 1, 6, 2};  // 12 waves: 2 K slices x 6 along N, 32 columns each
     default: return TileShape{4, 1, 4, 1};  // 4 waves along N, 64 columns each
   }
 }
@@ -259,7 +260,8 @@ TileShape tile_shape(int shape) {
   X(4, 4, 1, 4, 1, 1) X(4, 4, 1, 4, 2, 1) X(8, 4, 1, 4, 1, 1) X(4, 4, 2, 4, 2, 1) X(4, 2, 1, 8, 2, 1)  \
   X(8, 2, 1, 8, 2, 1)                                                                         \
   X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
-  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4)
+  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4) \
+  X(4, 2, 1, 6, 3, 2)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);

@@ -101,7 +101,7 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 # (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
-                (4, 9, 3), (2, 9, 3)]
+                (4, 9, 3), (2, 9, 3), (4, 10, 3)]
 TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3, 4)]
 
 
