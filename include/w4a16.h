@@ -219,8 +219,8 @@ int w4a16_split_k(int M, int K, int N);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
  * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,3,4,6} dividing N/16,
- * p1 = waves per workgroup in {4,8}, p2 = 128-row groups in flight per wave in {1,2,4},
- * M <= 64; configurations whose LDS exceeds 156 KiB or whose accumulators and load ring
+ * p1 = waves per workgroup in {4,8} (or 12 with p0 = 1), p2 = 128-row groups in flight per
+ * wave in {1,2,4}, M <= 64; configurations whose LDS exceeds 156 KiB or whose accumulators and load ring
  * exceed 176 registers per lane are rejected) or W4A16_REGIME_TILE (p0 = 16-row tiles per
  * wave, p1 = waves per SIMD the register allocation targets, p2 = wave layout: 0 or 1 =
  * 4 waves of 64 columns, 2 = 2 x 4 waves of 64 columns, 3 = 8 waves of 32 columns,

@@ -72,8 +72,9 @@ int tile_bn(const GemmPlan& p) {
 //  * medium layers (4096 < N < 16384): 16 columns at M = 1, 32 up to M = 8, then 48 with K
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
-//    N = 4096; from M = 5 on, 4 waves with four groups each in flight), then 64 columns with
-//    K in four;
+//    N = 4096; 12 waves up to M = 4 -- O M = 1 / 2 / 4: 4.58 / 4.84 / 5.20 us against 4.78 /
+//    4.96 / 5.37 us with 8 --, from M = 5 on 4 waves with four groups each in flight), then
+//    64 columns with K in four;
 //  * narrow layers with long K: 16 columns at M = 1, 32 with K in two or four up to M = 8,
 //    then 64 columns with K in four.
 GemmPlan plan_decode(int M, int K, int N) {
@@ -91,7 +92,7 @@ GemmPlan plan_decode(int M, int K, int N) {
     else if (M <= 8) tn = 2;
     else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
-    if (M <= 4) tn = 1;
+    if (M <= 4) { tn = 1; waves = 12; }
     else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
     else { tn = 4; depth = 1; split = 4; }
   } else {
@@ -244,6 +245,7 @@ GemmPlan plan_silu_mul(int M, int K, int N) {
   while (tn > 2 && (T % tn != 0 || !w4a16::decode_config_fits(MB, tn, 1, xl))) tn -= 2;
   while (p.p2 > 1 && !w4a16::decode_config_fits(MB, tn, p.p2, xl)) p.p2 /= 2;
   p.p0 = tn;
+  if (p.p1 == 12) p.p1 = 8;  // 12-wave workgroups hold one column tile
   while ((w4a16::decode_lds_bytes(M, K, tn, p.p1, p.p2, p.split) > w4a16::kDecodeMaxLds ||
           !w4a16::decode_stage_fits(M, K, tn, p.p1, p.p2, p.split)) &&
          p.split < G)
@@ -668,7 +670,8 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
     if ((N / 16) % p0) return fail(W4A16_ERR_SHAPE, "N / 16 = %d is not a multiple of %d column tiles", N / 16, p0);
     if (silu_mul && p0 % 2)
       return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs an even decode column tile count");
-    if (p1 != 4 && p1 != 8) return fail(W4A16_ERR_ARG, "decode waves must be 4 or 8");
+    if (p1 != 4 && p1 != 8 && !(p1 == 12 && p0 == 1))
+      return fail(W4A16_ERR_ARG, "decode waves must be 4 or 8, or 12 with one column tile");
     if (p2 != 1 && p2 != 2 && p2 != 4) return fail(W4A16_ERR_ARG, "decode depth must be 1, 2 or 4");
     if (w4a16::decode_lds_bytes(M, K, p0, p1, p2, split) > w4a16::kDecodeMaxLds)
       return fail(W4A16_ERR_ARG, "decode configuration needs %zu bytes of LDS (limit %zu)",

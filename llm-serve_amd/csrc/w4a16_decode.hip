@@ -736,6 +736,9 @@ template <int MB, int TN, int DEPTH>
 static hipError_t launch_decode_w(const DecodeArgs& a, int waves, bool norm, hipStream_t stream) {
   switch (waves) {
     case 4: return launch_decode_x<MB, TN, DEPTH, 4>(a, norm, stream);
+    case 12:  // one-tile workgroups only (checked by the API)
+      if constexpr (TN == 1) return launch_decode_x<MB, TN, DEPTH, 12>(a, norm, stream);
+      return hipErrorInvalidValue;
     default: return launch_decode_x<MB, TN, DEPTH, 8>(a, norm, stream);
   }
 }

@@ -47,7 +47,7 @@ constexpr int kStageE = 4;
 bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split);
 // Whether a decode configuration builds its dequant operands once per wave in LDS
 // (8 waves and a ring at least two groups deep) instead of per tile and group.
-constexpr bool decode_prebuilt_scales(int waves, int depth) { return waves == 8 && depth >= 2; }
+constexpr bool decode_prebuilt_scales(int waves, int depth) { return waves >= 8 && depth >= 2; }
 // LDS bytes of a decode workgroup: staged scales, zeros (and activations, and prebuilt
 // dequant operands), or the cross-wave reduction, whichever is larger.
 size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split);

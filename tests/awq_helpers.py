@@ -125,14 +125,16 @@ def random_x_gpu(m: int, k: int, seed: int, outliers: bool = False) -> torch.Ten
 def decode_config_accepted(m: int, k: int, tn: int, depth: int, waves: int, split: int) -> bool:
     """The library's admission rules for a decode configuration, restated: activations
     staged for M <= 4 within 32 KiB; per wave, its share of the groups' scale pairs and zero
-    words, staged activations and (8 waves with a ring of >= 2 groups) the prebuilt dequant
+    words, staged activations and (8 or 12 waves, a ring of >= 2 groups) the prebuilt dequant
     operands, 384 bytes per tile and group; the workgroup's LDS (those slices or the
     cross-wave reduction) <= 156 KiB; accumulator + ring registers <= 176."""
     mb = (m + 15) // 16
     n_gmax = -(-(k // 128) // split)
     items = -(-n_gmax // waves)
     xl = m <= 4 and n_gmax * m * 256 <= 32 * 1024
-    pre = waves == 8 and depth >= 2
+    if waves == 12 and tn != 1:
+        return False  # 12-wave workgroups hold one column tile
+    pre = waves >= 8 and depth >= 2
     up = lambda v, a: -(-v // a) * a
     wave = up(up(items * tn * 32, 256) + up(items * tn * 8, 256) + (up(items * m * 256, 1024) if xl else 0)
               + (items * tn * 384 if pre else 0), 256)

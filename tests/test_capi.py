@@ -123,6 +123,8 @@ def test_forced_config_validation(pkg):
     assert "depth" in L.last_error()
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 16, 2, 1, None, 0, None) == 1  # 16 waves
     assert "waves" in L.last_error()
+    assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 12, 2, 1, None, 0, None) == 1  # 12 waves, 4 column tiles
+    assert "waves" in L.last_error()
     assert f(p, p, p, p, p, 64, 4096, 6144, 128, 1, 6, 8, 1, 1, None, 0, None) == 1  # 192 KiB of LDS
     assert "LDS" in L.last_error()
     assert f(p, p, p, p, p, 64, 4096, 6144, 128, 1, 3, 4, 4, 1, None, 0, None) == 1  # ring registers

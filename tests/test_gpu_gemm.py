@@ -62,7 +62,7 @@ def test_single_token_wide_gemv_reference_recipe(gpu_lib):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(want), rtol=0.01, atol=0.02)
 
 
-DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4, 6) for w in (4, 8) for d in (1, 2, 4) for s in (1, 3, 8)]
+DECODE_CONFIGS = [(tn, w, d, s) for tn in (1, 2, 3, 4, 6) for w in (4, 8, 12) for d in (1, 2, 4) for s in (1, 3, 8)]
 
 
 @pytest.mark.parametrize("m", [1, 3, 5, 16, 33, 64])
