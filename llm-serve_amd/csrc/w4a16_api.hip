@@ -481,7 +481,15 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
   // Every check that could fail the GEMM runs before the prologue is enqueued.
-  const GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
+  GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
+  // With the norm as a prologue every workgroup repeats it, so one-tile 8-wave plans at M = 1
+  // take two tiles per workgroup when they divide N (half the workgroups: QKV 7.23 against
+  // 7.44 us).
+  if (p.regime == W4A16_REGIME_DECODE && M == 1 && p.p0 == 1 && p.p1 == 8 && (N / 16) % 2 == 0 &&
+      w4a16::decode_config_fits(1, 2, p.p2, w4a16::decode_stages_x(M, K, p.split)) &&
+      w4a16::decode_stage_fits(M, K, 2, p.p1, p.p2, p.split) &&
+      w4a16::decode_norm_lds_bytes(M, K, 2, p.p1, p.p2, p.split) > 0)
+    p.p0 = 2;
   v = check_plan(p, M, K, N, workspace, workspace_bytes);
   if (v != W4A16_OK) return v;
   const hipStream_t s = static_cast<hipStream_t>(stream);
