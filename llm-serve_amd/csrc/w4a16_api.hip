@@ -211,6 +211,10 @@ GemmPlan plan_tile(int M, int K, int N) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N);
   const int G = K / w4a16::kGroup;
+  // Narrow layers whose width is a multiple of 384 (QKV): 128-row tiles of 384 columns, 8
+  // waves of 48 (shape 11, plain GEMM only): QKV M = 1536 / 2048 / 4096 at 85.6 / 95.4 /
+  // 187 us against 102.6 / 110.6 / 190.8 us for 64 x 256 tiles.
+  if (N < 16384 && N % 384 == 0) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (t9 >= 256 && (t9 % 256 == 0 || (N >= 16384 && t9 >= 1024))) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
@@ -232,11 +236,15 @@ GemmPlan plan(int M, int K, int N) {
 }
 
 // The fused SiLU(gate) * up product of a gate|up weight [K, N] runs the plain GEMM's plan,
-// except that a decode workgroup must hold whole gate/up tile pairs: an odd tile count tn
+// except that a workgroup must hold whole gate/up tile pairs: in the decode regime an odd
+// tile count tn
 // becomes 2 tn (measured best for tn = 3 at M = 3..8), or the largest even count below
 // that divides N / 16 and fits the registers (the LDS check may then split K further).
 GemmPlan plan_silu_mul(int M, int K, int N) {
   GemmPlan p = plan(M, K, N);
+  // The fused product pairs gate and up tiles within a wave: tile layouts with an odd tile
+  // count per wave (shape 11) fall back to 64-row tiles of 256 columns.
+  if (p.regime == W4A16_REGIME_TILE && w4a16::tile_shape(p.p2).tw % 2) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   if (p.regime != W4A16_REGIME_DECODE || p.p0 % 2 == 0) return p;
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
@@ -693,7 +701,15 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
     if (p0 != 2 && p0 != 4 && p0 != 8) return fail(W4A16_ERR_ARG, "tile wm must be 2, 4 or 8");
-    if (p2 < 0 || p2 > 10) return fail(W4A16_ERR_ARG, "tile shape code must be 0..10");
+    if (p2 < 0 || p2 > 11) return fail(W4A16_ERR_ARG, "tile shape code must be 0..11");
+    if (silu_mul && w4a16::tile_shape(p2).tw % 2)
+      return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs a tile wave layout with an even tile count");
+    // A wave's output columns must lie wholly inside or wholly past the output width (true for
+    // every layout of 32 or 64 columns per wave whenever N % 64 == 0).
+    const int wave_cols = (silu_mul ? 8 : 16) * w4a16::tile_shape(p2).tw;
+    if ((silu_mul ? N / 2 : N) % wave_cols)
+      return fail(W4A16_ERR_SHAPE, "tile wave layout %d needs an output width that is a multiple of %d (got %d)", p2,
+                  wave_cols, silu_mul ? N / 2 : N);
     if (p1 < 1 || p1 > 3) return fail(W4A16_ERR_ARG, "tile occupancy must be 1, 2 or 3");
     if (!w4a16::tile_config_compiled(p0, p2, p1))
       return fail(W4A16_ERR_ARG, "tile configuration wm %d, shape %d, occupancy %d is not compiled", p0, p2, p1);
@@ -728,7 +744,7 @@ size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split)
   // Tile regime: enough for every tile shape (taller or wider tiles pad more).
   size_t most = workspace_for(GemmPlan{regime, p0, 0, 1, split}, M, N);
   if (regime != W4A16_REGIME_TILE) return most;
-  for (int shape = 2; shape <= 10; ++shape) {
+  for (int shape = 2; shape <= 11; ++shape) {
     const size_t b = workspace_for(GemmPlan{regime, p0, 0, shape, split}, M, N);
     most = b > most ? b : most;
   }

@@ -94,7 +94,9 @@ hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const ui
 // along M x nwn along N, each wave owning tw 16-column layout tiles and 16 wm rows, so the
 // workgroup tile is (16 wm nwm) x (16 tw nwn) and has nwm nwn wk waves.  Codes: 1 (or 0) =
 // {tw 4, 1 x 4}, 2 = {tw 4, 2 x 4}, 3 = {tw 2, 1 x 8}, 4 = {tw 2, 1 x 2, 4 slices},
-// 5 = {tw 2, 1 x 4, 2 slices}, 6 = {tw 2, 1 x 2, 2 slices}, 7 = {tw 2, 1 x 1, 4 slices}.
+// 5 = {tw 2, 1 x 4, 2 slices}, 6 = {tw 2, 1 x 2, 2 slices}, 7 = {tw 2, 1 x 1, 4 slices},
+// 8 = {tw 4, 1 x 8}, 9 = {tw 2, 1 x 3, 4 slices}, 10 = {tw 2, 1 x 6, 2 slices},
+// 11 = {tw 3, 1 x 8} (plain GEMM only: the fused product pairs tiles within a wave).
 struct TileShape {
   int tw, nwm, nwn, wk;
 };
@@ -102,7 +104,7 @@ TileShape tile_shape(int shape);
 // Whether (wm, shape, occ) is compiled; occ = waves per SIMD the register allocation targets.
 // Compiled (wm, shape, occ): (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2), (2,4,2),
 // (4,4,2), (2,5,2), (4,5,2), (8,5,2), (4,6,1), (8,6,1), (2,7,1), (4,7,1), (8,8,2), (4,9,3),
-// (2,9,3), (4,10,3).
+// (2,9,3), (4,10,3), (8,11,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
 // unused when split == 1).  up_tiles and res as for the decode kernel (N % 128 == 0 when

@@ -351,11 +351,12 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
     __builtin_amdgcn_wave_barrier();
   };
   if (!o.act) {
-    constexpr int TP = TW / kParts;  // tiles per pass
-    constexpr int CPR = 2 * TP;      // 16-byte chunks per row
+    constexpr int TP0 = TW / kParts;
+    constexpr int TP = TP0 & -TP0;  // tiles per pass: a power of two, so that rows are whole lane groups
+    constexpr int CPR = 2 * TP;     // 16-byte chunks per row
     constexpr int PITCH = 16 * CPR;
 #pragma unroll
-    for (int part = 0; part < kParts; ++part) {
+    for (int part = 0; part < TW / TP; ++part) {
 #pragma unroll
       for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
@@ -369,9 +370,10 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
           }
       store_rows(std::integral_constant<int, CPR>{}, o.col_w + 16 * TP * part);
     }
-  } else {
+  } else if constexpr (TW % 2 == 0) {  // the fused product pairs the two halves of a wave's tiles
     constexpr int H = TW / 2;
-    constexpr int TP = (H % kParts == 0) ? H / kParts : H;  // gate tiles per pass
+    constexpr int TP0 = (H % kParts == 0) ? H / kParts : H;
+    constexpr int TP = TP0 & -TP0;  // gate tiles per pass (a power of two)
     constexpr int NP = H / TP;
     constexpr int CPR = 2 * TP;
     constexpr int PITCH = 16 * CPR;

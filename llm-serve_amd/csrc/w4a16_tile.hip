@@ -135,7 +135,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   // Plain: the wave computes output columns [col_w, col_w + 16 TW) = layout tiles t0 + tt.
   // Fused SiLU(gate) * up (up_tiles = N / 32): output columns [col_w, col_w + 8 TW) of the
   // [M, N / 2] result, from gate tiles t0 + tt and up tiles t0 + up_tiles + tt, tt < TW / 2.
-  static_assert(TW % 2 == 0, "the fused product pairs the two halves of a wave's tiles");
+  // The fused product pairs the two halves of a wave's tiles: odd TW runs the plain GEMM only
+  // (the API rejects the fused call for it).
   const bool act = up_tiles != 0;
   const int n_out = act ? N / 2 : N;
   const int col_w = act ? nbk * (BN / 2) + 8 * TW * wn : nbk * BN + 16 * TW * wn;  // first output column
@@ -250,6 +251,7 @@ TileShape tile_shape(int shape) {
     case 8: return TileShape{4, 1, 8, 1};  // 8 waves along N, 64 columns each
     case 9: return TileShape{2, 1, 3, 4};   // 12 waves: 4 K slices x 3 along N, 32 columns each
     case 10: return TileShape{2, 1, 6, 2};  // 12 waves: 2 K slices x 6 along N, 32 columns each
+    case 11: return TileShape{3, 1, 8, 1};  // 8 waves along N, 48 columns each (plain GEMM only)
     default: return TileShape{4, 1, 4, 1};  // 4 waves along N, 64 columns each
   }
 }
@@ -261,7 +263,7 @@ TileShape tile_shape(int shape) {
   X(8, 2, 1, 8, 2, 1)                                                                         \
   X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
   X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4) \
-  X(4, 2, 1, 6, 3, 2)
+  X(4, 2, 1, 6, 3, 2) X(8, 3, 1, 8, 2, 1)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);

@@ -133,8 +133,10 @@ def test_forced_config_validation(pkg):
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 4, 2, 1, None, 0, None) == 1  # bad occupancy
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 2, 2, 3, 1, None, 0, None) == 1  # wm 2 x shape 3: not compiled
     assert "not compiled" in L.last_error()
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 11, 1, None, 0, None) == 1  # bad tile shape code
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 12, 1, None, 0, None) == 1  # bad tile shape code
     assert "shape" in L.last_error()
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 2, 11, 1, None, 0, None) == 2  # 48-column waves split
+    assert "multiple of 48" in L.last_error()
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 7, 4, 4, 2, 1, None, 0, None) == 1  # bad regime
     # split > 1 without workspace
     assert f(p, p, p, p, p, 16, 4096, 4096, 128, 1, 4, 4, 2, 4, None, 0, None) == 4

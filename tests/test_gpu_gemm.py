@@ -101,7 +101,10 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 # (wm, tile shape code, occupancy): every compiled tile kernel (see launch_tile_cfg)
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
-                (4, 9, 3), (2, 9, 3), (4, 10, 3)]
+                (4, 9, 3), (2, 9, 3), (4, 10, 3), (8, 11, 2)]
+# output columns of one wave per tile shape code where they are not 32 or 64 (the library
+# rejects an output width that would split a wave)
+WAVE_COLS = {11: 48}
 TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3, 4)]
 
 
@@ -115,6 +118,8 @@ def test_every_tile_configuration(gpu_lib, m, n):
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = ora.awq_linear_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128)
     for wm, shape, occ, split in TILE_CONFIGS:
+        if n % WAVE_COLS.get(shape, 1):
+            continue  # rejected by the library, see test_capi
         ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
         ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
@@ -141,6 +146,8 @@ def test_scales_and_zeros_at_word_alignment(gpu_lib):
     assert s_off.data_ptr() % 16 == 4 and z_off.data_ptr() % 16 == 4
     ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
     for wm, shape, occ in TILE_KERNELS:
+        if n % WAVE_COLS.get(shape, 1):
+            continue
         ys = []
         for s, z in ((t["scales"], t["qzeros"]), (s_off, z_off)):
             y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
