@@ -179,14 +179,19 @@ GemmPlan plan_mid(int M, int K, int N) {
 // the grid is below 144 workgroups; short-K narrow layers switch to 64-row tiles of 128
 // columns instead of splitting K.  From sweeps of every tile configuration at M = 384, 512,
 // 768, 1024: within 6 % of the best at every point (K splits that would need more than the
-// 16 MiB of partials of down at M = 512 left out).
-GemmPlan plan_large(int M, int K, int N) {
+// 16 MiB of partials of down at M = 512 left out).  `fused`: no layout with an odd tile
+// count per wave (the fused SiLU * up product pairs a wave's tiles).
+GemmPlan plan_large(int M, int K, int N, bool fused) {
   const int G = K / w4a16::kGroup;
+  // Plain GEMMs on widths that are multiples of 384 columns: 128 x 384 tiles (shape 11, 8
+  // waves of 48) where they fill one round on wide layers (gate_up M = 384 / 512: 86.6 / 96.1
+  // us against 104.0 / 112.6 us), 64 x 384 tiles on QKV-width layers once 128 x 256 tiles
+  // would fill a round (QKV M = 768 / 1024: 54.7 / 59.4 us against 60.5 / 61.1 us).
+  const bool w384 = !fused && N % 384 == 0;
+  if (w384 && N >= 16384 && ceil_div(M, 128) * (N / 384) <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
   if (N >= 16384 && M <= 768) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   const int t3 = ceil_div(M, 128) * ceil_div(N, 256);
-  // QKV-width layers where 128 x 256 tiles would fill a round: 64-row tiles of 384 columns
-  // (8 waves of 48; QKV M = 768 / 1024: 54.7 / 59.4 us against 60.5 / 61.1 us).
-  if (t3 >= 144 && N < 16384 && N % 384 == 0) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 11, 1};
+  if (t3 >= 144 && N < 16384 && w384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 11, 1};
   if (t3 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
   const int t5 = ceil_div(M, 128) * ceil_div(N, 128);
   if (t5 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 5, 1};
@@ -210,14 +215,17 @@ GemmPlan plan_large(int M, int K, int N) {
 // round's workgroups once K is split in two or four with >= 16 groups per split; otherwise
 // 64-row tiles of 256 columns, two workgroups per CU (shape 1; QKV at M = 2048: 384 vs 768
 // tiles).  Split-K partials are reduced by the last workgroup of each tile.
-GemmPlan plan_tile(int M, int K, int N) {
+GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
-  if (M <= 1024) return plan_large(M, K, N);
+  if (M <= 1024) return plan_large(M, K, N, fused);
   const int G = K / w4a16::kGroup;
-  // Narrow layers whose width is a multiple of 384 (QKV): 128-row tiles of 384 columns, 8
-  // waves of 48 (shape 11, plain GEMM only): QKV M = 1536 / 2048 / 4096 at 85.6 / 95.4 /
-  // 187 us against 102.6 / 110.6 / 190.8 us for 64 x 256 tiles.
-  if (N < 16384 && N % 384 == 0) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
+  // Plain GEMMs on widths that are multiples of 384 columns: 128-row tiles of 384 columns, 8
+  // waves of 48 (shape 11) on narrow layers (QKV M = 1536 / 2048 / 4096 at 85.6 / 95.4 / 187
+  // us against 102.6 / 110.6 / 190.8 us for 64 x 256 tiles), and on wide ones where they fill
+  // two or three rounds (gate_up M = 1536: 277.8 against 301.7 us).
+  const int t11 = ceil_div(M, 128) * (N / 384);
+  if (!fused && N % 384 == 0 && (N < 16384 || (t11 % 256 == 0 && t11 < 1024)))
+    return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (t9 >= 256 && (t9 % 256 == 0 || (N >= 16384 && t9 >= 1024))) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
@@ -232,22 +240,19 @@ GemmPlan plan_tile(int M, int K, int N) {
 // where it still beats the tile kernel (gate_up: 19.2 / 24.5 us at M = 32 / 48 against 27.5 /
 // 28.2 us); the tile kernel beyond (M = 48 on the narrow layers: QKV 12.5 vs 13.8 us, O 10.3
 // vs 12.6 us, down 18.6 vs 20.1 us).
-GemmPlan plan(int M, int K, int N) {
+GemmPlan plan(int M, int K, int N, bool fused = false) {
   if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
-  if (M > (N >= 16384 ? 48 : 32)) return plan_tile(M, K, N);
+  if (M > (N >= 16384 ? 48 : 32)) return plan_tile(M, K, N, fused);
   return plan_decode(M, K, N);
 }
 
 // The fused SiLU(gate) * up product of a gate|up weight [K, N] runs the plain GEMM's plan,
-// except that a workgroup must hold whole gate/up tile pairs: in the decode regime an odd
-// tile count tn
+// except that a wave must hold whole gate/up tile pairs: the tile regime leaves out the
+// layouts with an odd tile count per wave, and in the decode regime an odd tile count tn
 // becomes 2 tn (measured best for tn = 3 at M = 3..8), or the largest even count below
 // that divides N / 16 and fits the registers (the LDS check may then split K further).
 GemmPlan plan_silu_mul(int M, int K, int N) {
-  GemmPlan p = plan(M, K, N);
-  // The fused product pairs gate and up tiles within a wave: tile layouts with an odd tile
-  // count per wave (shape 11) fall back to 64-row tiles of 256 columns.
-  if (p.regime == W4A16_REGIME_TILE && w4a16::tile_shape(p.p2).tw % 2) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
+  GemmPlan p = plan(M, K, N, true);
   if (p.regime != W4A16_REGIME_DECODE || p.p0 % 2 == 0) return p;
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
