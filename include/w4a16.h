@@ -222,7 +222,7 @@ int w4a16_split_k(int M, int K, int N);
  * p1 = waves per workgroup in {4,8} (or 12 with p0 = 1), p2 = 128-row groups in flight per
  * wave in {1,2,4}, M <= 64; configurations whose LDS exceeds 156 KiB or whose accumulators and load ring
  * exceed 176 registers per lane are rejected) or W4A16_REGIME_TILE (p0 = 16-row tiles per
- * wave, p1 = waves per SIMD the register allocation targets, p2 = wave layout: 0 or 1 =
+ * wave in {2,4,6,8}, p1 = waves per SIMD the register allocation targets, p2 = wave layout: 0 or 1 =
  * 4 waves of 64 columns, 2 = 2 x 4 waves of 64 columns, 3 = 8 waves of 32 columns,
  * 4 = 4 K slices x 2 waves of 32 columns, 5 = 2 K slices x 4 waves of 32 columns,
  * 6 = 2 K slices x 2 waves of 32 columns, 7 = 4 K slices x 1 wave of 32 columns,
@@ -231,7 +231,7 @@ int w4a16_split_k(int M, int K, int N);
  * columns (plain GEMM only, N a multiple of 48); the compiled (p0, p2, p1) are (4,1,1),
  * (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2), (2,4,2), (4,4,2), (2,5,2), (4,5,2), (8,5,2),
  * (4,6,1), (8,6,1), (2,7,1), (4,7,1), (8,8,2), (4,9,3), (2,9,3), (4,10,3), (8,11,2),
- * (4,11,2));
+ * (4,11,2), (6,3,2), (6,8,2));
  * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises
  * every split-K reduction path at small sizes). */
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,

@@ -81,7 +81,7 @@ def test_every_fused_decode_configuration(gpu_lib, m):
 
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
-                (4, 9, 3), (2, 9, 3), (4, 10, 3)]
+                (4, 9, 3), (2, 9, 3), (4, 10, 3), (6, 3, 2), (6, 8, 2)]
 
 
 @pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 384), (513, 256)])
