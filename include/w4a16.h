@@ -231,7 +231,7 @@ int w4a16_split_k(int M, int K, int N);
  * columns (plain GEMM only, N a multiple of 48); the compiled (p0, p2, p1) are (4,1,1),
  * (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2), (2,4,2), (4,4,2), (2,5,2), (4,5,2), (8,5,2),
  * (4,6,1), (8,6,1), (2,7,1), (4,7,1), (8,8,2), (4,9,3), (2,9,3), (4,10,3), (8,11,2),
- * (4,11,2), (6,3,2), (6,8,2));
+ * (4,11,2), (6,3,2), (6,8,2), (6,11,2));
  * 1 <= split <= K/128.  No reference counterpart: a tuning and testing hook (it exercises
  * every split-K reduction path at small sizes). */
 int w4a16_gemm_config(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,

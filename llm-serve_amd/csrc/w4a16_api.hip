@@ -223,9 +223,15 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   // waves of 48 (shape 11) on narrow layers (QKV M = 1536 / 2048 / 4096 at 85.6 / 95.4 / 187
   // us against 102.6 / 110.6 / 190.8 us for 64 x 256 tiles), and on wide ones where they fill
   // two or three rounds (gate_up M = 1536: 277.8 against 301.7 us).
+  // On narrow layers the row block is 128 or 96, whichever fills its last round of 256
+  // workgroups better (QKV M = 1536 / 2560 / 3072 with 96 rows: 76.8 / 140.2 / 151.0 us
+  // against 85.9 / 170.9 / 171.9 us).
   const int t11 = ceil_div(M, 128) * (N / 384);
-  if (!fused && N % 384 == 0 && (N < 16384 || (t11 % 256 == 0 && t11 < 1024)))
-    return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
+  if (!fused && N % 384 == 0 && (N < 16384 || (t11 % 256 == 0 && t11 < 1024))) {
+    const int t11b = ceil_div(M, 96) * (N / 384);
+    auto fill = [](int t) { return static_cast<double>(t) / (ceil_div(t, 256) * 256); };
+    return GemmPlan{W4A16_REGIME_TILE, N < 16384 && fill(t11b) > fill(t11) ? 6 : 8, 2, 11, 1};
+  }
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (t9 >= 256 && (t9 % 256 == 0 || (N >= 16384 && t9 >= 1024))) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   // 96-row tiles where they fill whole rounds and 128-row ones do not (O and down at M =

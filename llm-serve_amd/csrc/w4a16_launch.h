@@ -104,7 +104,7 @@ TileShape tile_shape(int shape);
 // Whether (wm, shape, occ) is compiled; occ = waves per SIMD the register allocation targets.
 // Compiled (wm, shape, occ): (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2), (2,4,2),
 // (4,4,2), (2,5,2), (4,5,2), (8,5,2), (4,6,1), (8,6,1), (2,7,1), (4,7,1), (8,8,2), (4,9,3),
-// (2,9,3), (4,10,3), (8,11,2), (4,11,2), (6,3,2), (6,8,2).
+// (2,9,3), (4,10,3), (8,11,2), (4,11,2), (6,3,2), (6,8,2), (6,11,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
 // unused when split == 1).  up_tiles and res as for the decode kernel (N % 128 == 0 when

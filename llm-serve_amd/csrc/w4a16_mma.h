@@ -278,7 +278,7 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
     float* partials = o.partials;
     int* counters = o.counters;
     constexpr int kFrags = WM * TW;
-    constexpr int KC = kFrags % 8 == 0 ? 8 : 4;
+    constexpr int KC = kFrags % 8 == 0 ? 8 : kFrags % 4 == 0 ? 4 : 2;
     static_assert(kFrags % KC == 0, "fragments must split into chunks");
     const __amdgpu_buffer_rsrc_t rp =
         make_buffer(partials, static_cast<uint32_t>(split) * ntiles * NWG * kFrags * 1024u);

@@ -263,7 +263,7 @@ TileShape tile_shape(int shape) {
   X(8, 2, 1, 8, 2, 1)                                                                         \
   X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
   X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4) \
-  X(4, 2, 1, 6, 3, 2) X(8, 3, 1, 8, 2, 1) X(4, 3, 1, 8, 2, 1) X(6, 2, 1, 8, 2, 1) X(6, 4, 1, 8, 2, 1)
+  X(4, 2, 1, 6, 3, 2) X(8, 3, 1, 8, 2, 1) X(4, 3, 1, 8, 2, 1) X(6, 2, 1, 8, 2, 1) X(6, 4, 1, 8, 2, 1) X(6, 3, 1, 8, 2, 1)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);
