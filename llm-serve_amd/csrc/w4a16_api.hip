@@ -205,16 +205,12 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
   return GemmPlan{W4A16_REGIME_TILE, 4, 2, 5, split};
 }
 
-// Beyond M = 1024 (whole prefill chunks): 128-row tiles of 512 columns (shape 8: 8 waves of
-// 128 x 64) when their grid fills the CUs in even rounds (wide layers: or >= 4 rounds) --
-// every activation row is then re-read from L2 by half as many workgroups (gate_up M=2048:
-// 768 workgroups, 4.7 % faster than 256 columns, bit-identical; O and down at M = 4096: 119
-// and 328 us against 131 and 355 us); else 128-row tiles of 256
-// columns (shape 3: every dequantized weight serves 128 rows) when their grid fills the CUs
-// in even rounds (gate_up at M = 1024, O and down at M = 2048), or fills 144 .. 256 of one
-// round's workgroups once K is split in two or four with >= 16 groups per split; otherwise
-// 64-row tiles of 256 columns, two workgroups per CU (shape 1; QKV at M = 2048: 384 vs 768
-// tiles).  Split-K partials are reduced by the last workgroup of each tile.
+// Beyond M = 1024 (whole prefill chunks): 128 x 512 tiles (shape 8: 8 waves of 128 x 64)
+// on wide layers from four rounds of workgroups on -- every activation row is then re-read
+// from L2 by half as many workgroups as with 256 columns (gate_up M=2048: 4.7 % faster,
+// bit-identical); else the best-filling of four tile sizes (below); for small grids, K split
+// in two or four over 128 x 256 tiles, or 64-row tiles of 256 columns, two workgroups per
+// CU (shape 1).  Split-K partials are reduced by the last workgroup of each tile.
 GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N, fused);
@@ -233,16 +229,30 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
     return GemmPlan{W4A16_REGIME_TILE, N < 16384 && fill(t11b) > fill(t11) ? 6 : 8, 2, 11, 1};
   }
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
-  if (t9 >= 256 && (t9 % 256 == 0 || (N >= 16384 && t9 >= 1024))) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
-  // 96-row tiles where they fill whole rounds and 128-row ones do not (O and down at M =
-  // 1536 / 3072: 54.3 / 95.6 and 150.6 / 270.6 us against 61.2 / 111.3 and 169.6 / 320.1
-  // us; the fused gate_up at M = 1536: 280.3 against 301.5 us).
-  const int t9b = ceil_div(M, 96) * ceil_div(N, 512);
-  if (t9b >= 256 && t9b % 256 == 0) return GemmPlan{W4A16_REGIME_TILE, 6, 2, 8, 1};
+  if (N >= 16384 && t9 >= 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
+  // Otherwise the tile of 128 or 96 rows by 512 or 256 columns whose grid fills its last
+  // round of 256 workgroups best, weighted by the measured efficiency of the tile (the
+  // same work in 128 x 256, 96 x 512 and 96 x 256 tiles takes 1 / 0.955, 1 / 0.91 and
+  // 1 / 0.87 the time of 128 x 512 tiles); ties go to the larger tile.  From sweeps at M =
+  // 1280 ... 4096: O and down at M = 1280 / 2304 / 3584 50.9 / 88.0 / 110.0 and 140.6 /
+  // 249.8 / 310.0 us against 60.8 / 104.7 / 136.4 and 169.5 / 297.6 / 389.2 us with 128-row
+  // tiles only; the fused gate_up at M = 1280 / 1536 / 1792 222.8 / 280.3 / 326.4 against
+  // 268.7 / 301.5 / 369.5 us.
+  struct Cand {
+    int wm, shape, bm, bn;
+    double eff;
+  };
+  constexpr Cand kCands[] = {{8, 8, 128, 512, 1.0}, {8, 3, 128, 256, 0.955}, {6, 8, 96, 512, 0.91}, {6, 3, 96, 256, 0.87}};
+  const Cand* best = nullptr;
+  double best_score = 0.0;
+  for (const Cand& c : kCands) {
+    const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+    const double score = c.eff * t / (ceil_div(t, 256) * 256.0);
+    if (score > best_score + 1e-9) best = &c, best_score = score;
+  }
+  if (best_score >= 0.5) return GemmPlan{W4A16_REGIME_TILE, best->wm, 2, best->shape, 1};
+  // Small grids: K split in two or four over 128 x 256 tiles, or 64-row tiles.
   const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
-  if (t8 >= 256 && (t8 % 256 == 0 || t8 >= 1024)) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
-  const int t8b = ceil_div(M, 96) * ceil_div(N, 256);
-  if (t8b >= 256 && t8b % 256 == 0) return GemmPlan{W4A16_REGIME_TILE, 6, 2, 3, 1};
   int s8 = 1;
   while (s8 < 4 && t8 * s8 * 2 <= 256 && 16 * s8 * 2 <= G) s8 *= 2;
   if (t8 * s8 >= 144 && t8 * s8 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, s8};
