@@ -171,16 +171,51 @@ GemmPlan plan_mid(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_TILE, wm, 2, shape, split};
 }
 
-// 256 < M <= 1024 (chunked-prefill chunks and mixed batches): wide layers up to M = 768 take
-// 64-row tiles of 256 columns, two workgroups per CU (shape 1; gate_up M = 384 / 512 / 768:
-// 108 / 110 / 173 us against 113 / 117 / 187 us for 128-row tiles); otherwise 128-row tiles
-// unless they leave too few workgroups: 256 columns (shape 3) when that grid alone has >= 144
-// workgroups, else 128 columns (shape 5, 2 K slices), K split in two or more for long K while
-// the grid is below 144 workgroups; short-K narrow layers switch to 64-row tiles of 128
-// columns instead of splitting K.  From sweeps of every tile configuration at M = 384, 512,
-// 768, 1024: within 6 % of the best at every point (K splits that would need more than the
-// 16 MiB of partials of down at M = 512 left out).  `fused`: no layout with an odd tile
-// count per wave (the fused SiLU * up product pairs a wave's tiles).
+// Tile candidates of the fill score below: rows x columns of one workgroup's tile, and the
+// measured efficiency of the tile relative to 128 x 512 tiles (the same work in 128 x 256,
+// 96 x 512, 96 x 256 and 128 x 128 tiles takes 1 / 0.955, 1 / 0.91, 1 / 0.87 and 1 / 0.73
+// the time).  Wide layers choose among the first four; narrow layers, whose 512-column
+// tiles leave too few workgroups, among 256 and 128 columns.
+struct TileCand {
+  int wm, shape, bm, bn;
+  double eff;
+};
+constexpr TileCand kWideTiles[] = {{8, 8, 128, 512, 1.0}, {8, 3, 128, 256, 0.955}, {6, 8, 96, 512, 0.91}, {6, 3, 96, 256, 0.87}};
+constexpr TileCand kNarrowTiles[] = {{8, 3, 128, 256, 0.955}, {6, 3, 96, 256, 0.87}, {8, 5, 128, 128, 0.73}};
+
+// The candidate whose grid fills its last round of 256 workgroups best, weighted by its
+// efficiency; ties go to the earlier (larger) tile.  Regime NONE when no candidate fills
+// half its last round.
+template <size_t C>
+GemmPlan best_filling_tile(int M, int N, const TileCand (&cands)[C]) {
+  const TileCand* best = nullptr;
+  double best_score = 0.0;
+  for (const TileCand& c : cands) {
+    const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+    const double score = c.eff * t / (ceil_div(t, 256) * 256.0);
+    if (score > best_score + 1e-9) best = &c, best_score = score;
+  }
+  if (best_score < 0.5) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
+  return GemmPlan{W4A16_REGIME_TILE, best->wm, 2, best->shape, 1};
+}
+
+// 256 < M <= 1024 (chunked-prefill chunks and mixed batches).  Wide layers: below M = 384,
+// 64-row tiles of 256 columns, two workgroups per CU (shape 1); from M = 384 on, the
+// best-filling wide tile (fused gate_up M = 384 / 448 / 512 / 640 / 768 / 896: 87.7 / 94.9 /
+// 106.5 / 116.8 / 161.6 / 186.6 us against 106.4 / 108.0 / 115.4 / 146.7 / 174.8 / 189.3 us
+// with 64-row tiles up to M = 768 and 128 x 256 beyond).  Narrow layers above M = 512: 96 x
+// 256 tiles with K split in two where that grid fills one round (O / down M = 640: 34.1 /
+// 78.9 us against 37.7 / 99.5 us), 128 x 256 tiles with K split in two for long K where
+// that grid fills three quarters of a round or more (down M = 832 / 1024: 96.0 / 102.1
+// against 100.2 / 105.3 us), else the best-filling narrow tile (QKV M = 704 / 896 / 960:
+// 49.8 / 52.3 / 52.6 against 54.4 / 56.3 / 57.5 us), except that QKV-width layers keep 64 x
+// 384 tiles when 128 x 256 tiles would fill more than half a round and 96-row tiles do not
+// win.  Up to M = 512: 128-row tiles unless they leave too few workgroups: 256 columns
+// (shape 3) when that grid alone has >= 144 workgroups, else 128 columns (shape 5, 2 K
+// slices), K split in two or more for long K while the grid is below 144 workgroups;
+// short-K narrow layers switch to 64-row tiles of 128 columns instead of splitting K.  From
+// sweeps of every tile configuration at M = 320 ... 1024.  `fused`: no layout with an odd
+// tile count per wave (the fused SiLU * up product pairs a wave's tiles).
 GemmPlan plan_large(int M, int K, int N, bool fused) {
   const int G = K / w4a16::kGroup;
   // Plain GEMMs on widths that are multiples of 384 columns: 128 x 384 tiles (shape 11, 8
@@ -189,8 +224,18 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
   // would fill a round (QKV M = 768 / 1024: 54.7 / 59.4 us against 60.5 / 61.1 us).
   const bool w384 = !fused && N % 384 == 0;
   if (w384 && N >= 16384 && ceil_div(M, 128) * (N / 384) <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
-  if (N >= 16384 && M <= 768) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
+  if (N >= 16384 && M < 384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
+  if (N >= 16384) {
+    const GemmPlan p = best_filling_tile(M, N, kWideTiles);
+    if (p.regime == W4A16_REGIME_TILE) return p;
+  }
   const int t3 = ceil_div(M, 128) * ceil_div(N, 256);
+  if (N < 16384 && M > 512) {
+    if (ceil_div(M, 96) * ceil_div(N, 256) * 2 <= 256 && G >= 32) return GemmPlan{W4A16_REGIME_TILE, 6, 2, 3, 2};
+    if (K >= 8192 && t3 * 2 >= 192 && t3 * 2 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 2};
+    const GemmPlan p = best_filling_tile(M, N, kNarrowTiles);
+    if (p.regime == W4A16_REGIME_TILE) return w384 && t3 >= 144 && p.p0 != 6 ? GemmPlan{W4A16_REGIME_TILE, 4, 2, 11, 1} : p;
+  }
   if (t3 >= 144 && N < 16384 && w384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 11, 1};
   if (t3 >= 144) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 3, 1};
   const int t5 = ceil_div(M, 128) * ceil_div(N, 128);
@@ -230,27 +275,12 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   }
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (N >= 16384 && t9 >= 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
-  // Otherwise the tile of 128 or 96 rows by 512 or 256 columns whose grid fills its last
-  // round of 256 workgroups best, weighted by the measured efficiency of the tile (the
-  // same work in 128 x 256, 96 x 512 and 96 x 256 tiles takes 1 / 0.955, 1 / 0.91 and
-  // 1 / 0.87 the time of 128 x 512 tiles); ties go to the larger tile.  From sweeps at M =
-  // 1280 ... 4096: O and down at M = 1280 / 2304 / 3584 50.9 / 88.0 / 110.0 and 140.6 /
-  // 249.8 / 310.0 us against 60.8 / 104.7 / 136.4 and 169.5 / 297.6 / 389.2 us with 128-row
-  // tiles only; the fused gate_up at M = 1280 / 1536 / 1792 222.8 / 280.3 / 326.4 against
-  // 268.7 / 301.5 / 369.5 us.
-  struct Cand {
-    int wm, shape, bm, bn;
-    double eff;
-  };
-  constexpr Cand kCands[] = {{8, 8, 128, 512, 1.0}, {8, 3, 128, 256, 0.955}, {6, 8, 96, 512, 0.91}, {6, 3, 96, 256, 0.87}};
-  const Cand* best = nullptr;
-  double best_score = 0.0;
-  for (const Cand& c : kCands) {
-    const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn);
-    const double score = c.eff * t / (ceil_div(t, 256) * 256.0);
-    if (score > best_score + 1e-9) best = &c, best_score = score;
-  }
-  if (best_score >= 0.5) return GemmPlan{W4A16_REGIME_TILE, best->wm, 2, best->shape, 1};
+  // Otherwise the best-filling tile (above).  From sweeps at M = 1280 ... 4096: O and down
+  // at M = 1280 / 2304 / 3584 50.9 / 88.0 / 110.0 and 140.6 / 249.8 / 310.0 us against 60.8
+  // / 104.7 / 136.4 and 169.5 / 297.6 / 389.2 us with 128-row tiles only; the fused gate_up
+  // at M = 1280 / 1536 / 1792 222.8 / 280.3 / 326.4 against 268.7 / 301.5 / 369.5 us.
+  const GemmPlan best = best_filling_tile(M, N, kWideTiles);
+  if (best.regime == W4A16_REGIME_TILE) return best;
   // Small grids: K split in two or four over 128 x 256 tiles, or 64-row tiles.
   const int t8 = ceil_div(M, 128) * ceil_div(N, 256);
   int s8 = 1;
