@@ -76,8 +76,8 @@ int tile_bn(const GemmPlan& p) {
 //    4.96 / 5.37 us with 8 --, from M = 5 on 4 waves with four groups each in flight), then
 //    64 columns with K in four;
 //  * narrow layers with long K: 16 columns at M = 1 (12 waves, four groups each in flight:
-//    down 8.3 - 8.6 us against 8.7 - 8.9 us with 8), 32 with K in two or four up to M = 8,
-//    then 64 columns with K in four.
+//    down 8.3 - 8.6 us against 8.7 - 8.9 us with 8), 32 with K in two up to M = 8 (down
+//    M = 4: 9.96 us against 10.27 us with K in four), then 64 columns with K in four.
 GemmPlan plan_decode(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   const int MB = (M + 15) / 16;
@@ -98,8 +98,6 @@ GemmPlan plan_decode(int M, int K, int N) {
     else { tn = 4; depth = 1; split = 4; }
   } else {
     if (M <= 1) { tn = 1; depth = 4; waves = 12; }
-    else if (M <= 2) { tn = 2; split = 2; }
-    else if (M <= 4) { tn = 2; split = 4; }
     else if (M <= 8) { tn = 2; split = 2; }
     else { tn = 4; depth = 1; split = 4; if (M > 32) waves = 4; }
   }
