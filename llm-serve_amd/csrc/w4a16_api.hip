@@ -73,8 +73,9 @@ int tile_bn(const GemmPlan& p) {
 //    in two;
 //  * narrow layers (N <= 4096), K < 8192: 16 columns up to M = 16 (one workgroup per CU for
 //    N = 4096; 12 waves up to M = 4 -- O M = 1 / 2 / 4: 4.58 / 4.84 / 5.20 us against 4.78 /
-//    4.96 / 5.37 us with 8 --, from M = 5 on 4 waves with four groups each in flight), then
-//    64 columns with K in four;
+//    4.96 / 5.37 us with 8 --, one group each in flight at M = 3, 4 -- O M = 3 / 4: 4.97 /
+//    5.05 against 5.13 / 5.19 us with two --, from M = 5 on 4 waves with four groups each in
+//    flight), then 64 columns with K in four;
 //  * narrow layers with long K: 16 columns at M = 1 (12 waves, four groups each in flight:
 //    down 8.3 - 8.6 us against 8.7 - 8.9 us with 8), 32 with K in two up to M = 8 (down
 //    M = 4: 9.96 us against 10.27 us with K in four), then 64 columns with K in four.
@@ -93,7 +94,7 @@ GemmPlan plan_decode(int M, int K, int N) {
     else if (M <= 8) tn = 2;
     else { tn = 3; depth = 1; split = 2; if (M > 32) waves = 4; }
   } else if (K < 8192) {
-    if (M <= 4) { tn = 1; waves = 12; }
+    if (M <= 4) { tn = 1; waves = 12; if (M > 2) depth = 1; }
     else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
     else { tn = 4; depth = 1; split = 4; }
   } else {
