@@ -128,9 +128,9 @@ GemmPlan plan_decode(int M, int K, int N) {
 // exchange between workgroups; short rows blocks (32 rows) re-dequantize the weights per
 // row block but read each activation stage once per 64 columns:
 //  * wide layers (N >= 16384): 64-row tiles of 128 columns up to M = 64, then 128-row
-//    tiles of 128 columns, then (M > 128) of 256 columns, K not split;
+//    tiles of 128 columns, then (M > 128) 96- or 128-row tiles of 256 columns, K not split;
 //  * long K (>= 8192): 32-row tiles up to M = 64 (64 columns up to M = 32, then 128),
-//    64 rows up to M = 128, 128 rows beyond, 128 columns, K split in four;
+//    then 64 rows of 128 columns, K split until the grid has 144 workgroups;
 //  * otherwise 32-row tiles of 64 columns up to M = 64 (up to M = 128 for N <= 4096), then
 //    64-row tiles (128 columns above M = 128 when N > 4096); K split in powers of two only
 //    until the grid has 144 workgroups, with >= 8 groups per split.
@@ -142,8 +142,16 @@ GemmPlan plan_mid(int M, int K, int N) {
   // Layers whose width is a multiple of 96 columns (QKV: 6144) above M = 64: 12-wave
   // workgroups of 96 columns (shape 9: 4 K slices x 3 waves along N, three waves per SIMD),
   // 32-row tiles up to M = 128 and 64-row tiles beyond, when that grid has >= 192
-  // workgroups (QKV M = 72 .. 128: 16.4 - 16.5 us against 17.9 - 18.1 us; M = 160 .. 256:
+  // workgroups (QKV M = 72 .. 128: 16.4 - 16.5 us against 17.9 - 18.1 us; M = 176 .. 256:
   // 22.9 - 23.2 against 24.7 - 24.9 us).
+  // Above M = 128, 32-row tiles while they fill one round: of 128 columns on QKV-width layers
+  // (shape 5; QKV M = 160: 19.0 us against 22.9 us for 64 x 96 tiles), of 96 columns on
+  // narrow ones (shape 9; O M = 160: 16.4 against 17.9 us for 64 x 64 tiles) -- 64-row tiles
+  // would compute 192 rows for 160.
+  if (N < 16384 && K < 8192 && M > 128 && N % 96 == 0 && ceil_div(M, 32) * ceil_div(N, 128) <= 256)
+    return GemmPlan{W4A16_REGIME_TILE, 2, 2, 5, 1};
+  if (N <= 4096 && K < 8192 && M > 128 && ceil_div(M, 32) * ceil_div(N, 96) <= 256)
+    return GemmPlan{W4A16_REGIME_TILE, 2, 3, 9, 1};
   if (N < 16384 && K < 8192 && N % 96 == 0 && M > 64) {
     const int wm9 = M <= 128 ? 2 : 4;
     if (ceil_div(M, 16 * wm9) * (N / 96) >= 192) return GemmPlan{W4A16_REGIME_TILE, wm9, 3, 9, 1};
@@ -153,11 +161,16 @@ GemmPlan plan_mid(int M, int K, int N) {
   // 2 K slices x 6 waves along N, three waves per SIMD), one round of 256 workgroups for
   // gate_up (34.2 - 35.6 us against 37.9 - 39.2 us for 128 x 128 tiles on 192 workgroups).
   if (N >= 16384 && M > 64 && M <= 128 && N % 192 == 0) return GemmPlan{W4A16_REGIME_TILE, 4, 3, 10, 1};
+  // Wide layers above M = 128: 96 x 256 tiles while they fill one round (gate_up M = 160 /
+  // 192: 51.1 / 52.1 us against 60.7 / 61.3 us for 128 x 256 tiles, which compute 256 rows).
+  if (N >= 16384 && M > 128 && ceil_div(M, 96) * ceil_div(N, 256) <= 256) return GemmPlan{W4A16_REGIME_TILE, 6, 2, 3, 1};
   if (N >= 16384) {
     if (M <= 64) { wm = 4; shape = 5; }
     else { wm = 8; shape = M <= 128 ? 5 : 3; }
   } else if (K >= 8192) {
-    wm = M <= 64 ? 2 : M <= 128 ? 4 : 8;
+    // 64-row tiles up to M = 256 (down M = 160 / 192: 37.0 / 37.3 us against 37.6 / 38.3 us
+    // with 128-row tiles split in four)
+    wm = M <= 64 ? 2 : 4;
     shape = M <= 32 ? 4 : 5;
   } else {
     wm = (M <= 64 || (M <= 128 && N <= 4096)) ? 2 : 4;
