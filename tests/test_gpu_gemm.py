@@ -233,12 +233,18 @@ def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
 
 @pytest.mark.parametrize("shape,m", [("qkv", 768), ("o", 768), ("gate_up", 256), ("down", 384), ("down", 768),
                                      ("gate_up", 48), ("gate_up", 49), ("o", 32), ("o", 33), ("qkv", 33),
-                                     ("down", 33), ("down", 257), ("qkv", 257)])
+                                     ("down", 33), ("down", 257), ("qkv", 257),
+                                     ("gate_up", 160), ("qkv", 160), ("o", 160), ("down", 192), ("o", 640),
+                                     ("down", 640), ("qkv", 704), ("down", 896), ("gate_up", 640), ("down", 4)])
 def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
     (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundaries
-    (decode up to M = 32, up to 48 on the wide layer) and the end of the mid-range plans
-    (M = 257), at full shapes."""
+    (decode up to M = 32, up to 48 on the wide layer), the end of the mid-range plans
+    (M = 257), the mid-range row blocks that follow M (96 x 256 tiles on gate_up, 32-row
+    tiles on QKV / O, 64-row tiles split in K on down at M = 160 / 192), the plans above M =
+    512 (96 x 256 tiles with K in two on O / down at 640, the best-filling narrow and wide
+    tiles at QKV 704, gate_up 640, down 896 with 128 x 256 tiles and K in two) and the long-K
+    decode split at M = 4, at full shapes."""
     k, n = QWEN3_SHAPES[shape]
     qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
     packed = awq_mod().repack_awq_qweight(qw)

@@ -123,7 +123,7 @@ def test_full_gate_up_fused_matches_two_step_path(gpu_lib):
     qw, qz, s = random_awq_gpu(k, n, seed=31)
     awq = awq_mod()
     packed = awq.repack_awq_qweight(qw)
-    for m in (1, 4, 8, 16, 32, 64, 512, 2048):
+    for m in (1, 4, 8, 16, 32, 64, 160, 384, 512, 640, 2048):
         print(f"fused gate_up m={m}", flush=True)
         x = random_x_gpu(m, k, seed=40 + m, outliers=m >= 512)
         y = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
