@@ -194,6 +194,11 @@ struct TileCand {
 };
 constexpr TileCand kWideTiles[] = {{8, 8, 128, 512, 1.0}, {8, 3, 128, 256, 0.955}, {6, 8, 96, 512, 0.91}, {6, 3, 96, 256, 0.87}};
 constexpr TileCand kNarrowTiles[] = {{8, 3, 128, 256, 0.955}, {6, 3, 96, 256, 0.87}, {8, 5, 128, 128, 0.73}};
+// Plain GEMMs on narrow widths that are multiples of 384 also weigh 384-column tiles (shape
+// 11: 128 x 384 at 0.93, 96 x 384 at 0.89 of 128 x 512); on these layers (QKV) 128 x 256
+// tiles measure 0.86 (M = 4096: 198.0 against 184.5 us for 128 x 384 at full rounds).
+constexpr TileCand kNarrow384Tiles[] = {{8, 8, 128, 512, 1.0}, {8, 11, 128, 384, 0.93}, {6, 8, 96, 512, 0.91},
+                                        {6, 11, 96, 384, 0.89}, {6, 3, 96, 256, 0.87}, {8, 3, 128, 256, 0.86}};
 
 // The candidate whose grid fills its last round of 256 workgroups best, weighted by its
 // efficiency; ties go to the earlier (larger) tile.  Regime NONE when no candidate fills
@@ -272,19 +277,18 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N, fused);
   const int G = K / w4a16::kGroup;
-  // Plain GEMMs on widths that are multiples of 384 columns: 128-row tiles of 384 columns, 8
-  // waves of 48 (shape 11) on narrow layers (QKV M = 1536 / 2048 / 4096 at 85.6 / 95.4 / 187
-  // us against 102.6 / 110.6 / 190.8 us for 64 x 256 tiles), and on wide ones where they fill
-  // two or three rounds (gate_up M = 1536: 277.8 against 301.7 us).
-  // On narrow layers the row block is 128 or 96, whichever fills its last round of 256
-  // workgroups better (QKV M = 1536 / 2560 / 3072 with 96 rows: 76.8 / 140.2 / 151.0 us
-  // against 85.9 / 170.9 / 171.9 us).
+  // Plain GEMMs on widths that are multiples of 384 columns: on narrow layers the best-filling
+  // of the 384-, 512- and 256-column tiles of 96 or 128 rows (QKV M = 1536 / 2048 / 3072 on
+  // 384-column tiles: 76.8 / 95.4 / 151.0 us against 85.9 / 110.6 / 171.9 us; M = 5120 /
+  // 8192 on 128 x 512 tiles: 220.4 / 339.2 us against 275.6 / 365.4 us on 384 columns); on
+  // wide ones 128 x 384 tiles where they fill two or three rounds (gate_up M = 1536: 277.8
+  // against 301.7 us).
   const int t11 = ceil_div(M, 128) * (N / 384);
-  if (!fused && N % 384 == 0 && (N < 16384 || (t11 % 256 == 0 && t11 < 1024))) {
-    const int t11b = ceil_div(M, 96) * (N / 384);
-    auto fill = [](int t) { return static_cast<double>(t) / (ceil_div(t, 256) * 256); };
-    return GemmPlan{W4A16_REGIME_TILE, N < 16384 && fill(t11b) > fill(t11) ? 6 : 8, 2, 11, 1};
+  if (!fused && N % 384 == 0 && N < 16384) {
+    const GemmPlan p = best_filling_tile(M, N, kNarrow384Tiles);
+    if (p.regime == W4A16_REGIME_TILE) return p;
   }
+  if (!fused && N % 384 == 0 && N >= 16384 && t11 % 256 == 0 && t11 < 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (N >= 16384 && t9 >= 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   // Otherwise the best-filling tile (above).  From sweeps at M = 1280 ... 4096: O and down
