@@ -64,23 +64,29 @@ struct BSources {
 
 // The wave's tiles are t0 + tt, plus dt for tt >= TW / 2 (dt = 0 for the plain GEMM; for
 // the fused gate/up product the second half are the up tiles of the first half's gate tiles).
+// g is a group of the weights (callers clamp a prefetch past their range to its last group);
+// an inactive wave (columns past N) fetches nothing.  The group's part of each offset is the
+// instruction's scalar offset and the lane's part is the same for every group, so the loop
+// spends no vector instructions on addresses; every lane offset plus its group offset stays
+// inside its buffer (the wave's tiles lie below N / 16).
 template <int TW, bool LOAD_SC>
-__device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src, int g, bool valid, int N, int t0,
+__device__ __forceinline__ void load_b_group(BGroup<TW>& b, const BSources& src, int g, bool active, int N, int t0,
                                              int dt, int lane) {
   const int NT = N / kTileCols;
   const int c = lane & 15;
-  const uint32_t oob = valid ? 0u : kOutOfRange;
+  const uint32_t oob = active ? 0u : kOutOfRange;
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt) {
     const int t = t0 + tt + (tt >= TW / 2 ? dt : 0);
-    const uint32_t wo = valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : kOutOfRange;
-    b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
+    const uint32_t wo = oob | (static_cast<uint32_t>(t * 64 + lane) * 16u);
+    b.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, static_cast<int>(static_cast<uint32_t>(g) * NT * 1024u),
+                                                     0);
     if constexpr (LOAD_SC) {
       const int col = kTileCols * t + c;
-      b.sc.s[tt] =
-          __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(g * N + (col & ~1)) * 2u), 0, 0);
-      b.sc.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(
-          src.z, oob | (static_cast<uint32_t>(g * (N >> 3) + (col >> 3)) * 4u), 0, 0);
+      b.sc.s[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.s, oob | (static_cast<uint32_t>(col & ~1) * 2u),
+                                                        static_cast<int>(static_cast<uint32_t>(g) * N * 2u), 0);
+      b.sc.zw[tt] = __builtin_amdgcn_raw_buffer_load_b32(src.z, oob | (static_cast<uint32_t>(col >> 3) * 4u),
+                                                         static_cast<int>(static_cast<uint32_t>(g) * (N >> 3) * 4u), 0);
     }
   }
 }

@@ -44,11 +44,13 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // (NW waves, NI instructions each).  Instruction i of wave w fills rows 4 (NW i + w) .. +3
 // (1 KiB); lane -> (row, physical chunk).  When the BM / 4 row quads do not split evenly over
 // the waves, the instructions past them fetch nothing into `spare` (1 KiB of LDS no one
-// reads), so that every wave issues the same NI loads.  An invalid group (past the
-// workgroup's K range) fetches nothing.
+// reads), so that every wave issues the same NI loads.  g is a group of the activations
+// (callers clamp a prefetch past their K range to its last group); the group's part of the
+// offset is the instruction's scalar offset, the lane's part the same for every group, and
+// their sum stays inside the activations (rows past M read row M - 1).
 template <int NI, int NW, int BM>
 __device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t* stage, uint8_t* spare, int row0,
-                                              int M, int K, int g, bool valid, int wave, int lane) {
+                                              int M, int K, int g, int wave, int lane) {
   const int p = lane & 15;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -58,11 +60,9 @@ __device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t
     const int c = p ^ (r & 15);
     int row = row0 + r;
     row = row < M ? row : M - 1;  // rows past M load a valid row; their outputs are dropped
-    const uint32_t off = valid && in
-                             ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + kGroup * g + 8u * c) * 2u
-                             : kOutOfRange;
+    const uint32_t off = in ? (static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + 8u * c) * 2u : kOutOfRange;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(in ? stage + quad * 4 * kARowBytes : spare), 16, off,
-                                             0, 0, 0);
+                                             static_cast<int>(static_cast<uint32_t>(g) * kGroup * 2u), 0, 0);
   }
 }
 
@@ -172,11 +172,13 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   constexpr int kWaitAll = 0x0F70;  // vmcnt(0); expcnt and lgkmcnt not waited for
   const int n_items = g_end - g_begin;
   BGroup<TW> ring[2 * PW];
+  // A prefetch past the workgroup's last item reloads that item's group (never consumed);
+  // ranges are never empty (split <= K / 128).
+  auto group_of = [&](int item) { return g_begin + (item < n_items ? item : n_items - 1); };
   auto issue = [&](int half, int b) {  // batch starting at item b into half `half`
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-      issue_a_stage<NI, NW, BM>(rx, stage(half * P + q), spare, row0, M, K, g_begin + b + q, b + q < n_items, wave,
-                                lane);
+      issue_a_stage<NI, NW, BM>(rx, stage(half * P + q), spare, row0, M, K, group_of(b + q), wave, lane);
       // the group's scale and zero instructions go to waves 2q and 2q + 1 (mod NW)
       if (kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
         issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], g_begin + b + q, b + q < n_items, N, cs0,
@@ -185,8 +187,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
       const int item = b + wk + WK * j;
-      load_b_group<TW, !kStageSZ>(ring[half * PW + j], bsrc, g_begin + item, item < n_items && active, N, t0, dt,
-                                  lane);
+      load_b_group<TW, !kStageSZ>(ring[half * PW + j], bsrc, group_of(item), active, N, t0, dt, lane);
     }
   };
   issue(0, 0);
