@@ -234,16 +234,23 @@ struct TileScale {
   f32x4_t cin;
 };
 
+// Byte selectors of v_perm_b32 over (0, s_pair) for the lane's scale (bytes 0-1 for an even
+// column, 2-3 for an odd one): kept in its own half (the diagonal element), moved to the high
+// half (its fp32 value), or zero.  They depend on the lane only, so loops hoist them.
 __device__ __forceinline__ TileScale make_tile_scale(uint32_t s_pair, uint32_t z, int lane) {
   TileScale t;
   const bool hi = (lane & 1) != 0;
-  const uint32_t mine = s_pair & (hi ? 0xFFFF0000u : 0x0000FFFFu);
   const bool upper = (lane & 2) != 0;  // element j in 32-bit register j / 2
+  constexpr uint32_t kZero = 0x0C0C0C0Cu;
+  const uint32_t sel_own = hi ? 0x03020C0Cu : 0x0C0C0100u;
+  const uint32_t sel_f32 = hi ? 0x03020C0Cu : 0x01000C0Cu;
   u32x2_t d;
-  d[0] = upper ? 0u : mine;
-  d[1] = upper ? mine : 0u;
+  d[0] = __builtin_amdgcn_perm(0u, s_pair, upper ? kZero : sel_own);
+  d[1] = __builtin_amdgcn_perm(0u, s_pair, upper ? sel_own : kZero);
   t.diag = __builtin_bit_cast(s16x4_t, d);
-  const float c = -((128.0f + static_cast<float>(z)) * __uint_as_float(hi ? mine : (mine << 16)));
+  // 128 + z (z < 16) is exact in fp32 as 0x43000000 | z << 16; the product has 16 significant
+  // bits at most, so it is exact too.
+  const float c = -(__uint_as_float(0x43000000u | (z << 16)) * __uint_as_float(__builtin_amdgcn_perm(0u, s_pair, sel_f32)));
   t.cin = f32x4_t{c, c, c, c};
   return t;
 }
