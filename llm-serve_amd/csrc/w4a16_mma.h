@@ -50,8 +50,7 @@ struct GroupScales {
 // Raw loads of one group for a wave's TW layout tiles: one 16-byte weight load per tile,
 // and (LOAD_SC) the scale-pair and zero words of the lane's column in each tile -- else those
 // come from the workgroup's LDS stage (issue_sz_stage, read_group_scales).  Decoding waits
-// until the group is consumed.  An invalid group (past the K range, or a wave whose columns
-// lie past N) fetches nothing.
+// until the group is consumed.  A wave whose columns lie past N fetches nothing.
 template <int TW>
 struct BGroup {
   u32x4_t w[TW];
@@ -105,25 +104,29 @@ template <int BN>
 constexpr int sz_zero_chunks() { return (BN + 63) / 64; }
 
 // Instruction `which` (0: scales, 1: zero words) of group g's stage, on the lanes that have
-// a chunk.  An invalid group fetches nothing (zeros).
+// a chunk.  g is a group of the weights (callers clamp a prefetch past their K range to its
+// last group): its part of the offset is the instruction's scalar offset, the lane's part
+// (the column) the same for every group.
 template <int BN>
-__device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz, int g, bool valid, int N, int cs0,
-                                               int cs1, int which, int lane) {
+__device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz, int g, int N, int cs0, int cs1,
+                                               int which, int lane) {
   typedef __attribute__((address_space(3))) void lds_void_t;
   static_assert(BN % 32 == 0 && BN / 8 <= 64, "one instruction holds the scales of the column block");
   if (which == 0) {
     constexpr int kHalf = BN / 16;  // 16-byte chunks of one range
     const int r = lane >= kHalf;
     const int col = (r ? cs1 : cs0) + 8 * (lane - r * kHalf);
-    const uint32_t off = valid ? (static_cast<uint32_t>(g) * N + static_cast<uint32_t>(col)) * 2u : kOutOfRange;
-    if (lane < 2 * kHalf) __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)sz, 16, off, 0, 0, 0);
+    if (lane < 2 * kHalf)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.s, (lds_void_t*)sz, 16, static_cast<uint32_t>(col) * 2u,
+                                               static_cast<int>(static_cast<uint32_t>(g) * N * 2u), 0, 0);
   } else {
     constexpr int kZc = sz_zero_chunks<BN>();
     const int r = lane >= kZc;
     const int col = (r ? cs1 : cs0) + 32 * (lane - r * kZc);
-    const uint32_t off =
-        valid ? (static_cast<uint32_t>(g) * (N >> 3) + static_cast<uint32_t>(col >> 3)) * 4u : kOutOfRange;
-    if (lane < 2 * kZc) __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(sz + kSzZeroBase), 16, off, 0, 0, 0);
+    if (lane < 2 * kZc)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.z, (lds_void_t*)(sz + kSzZeroBase), 16,
+                                               static_cast<uint32_t>(col >> 3) * 4u,
+                                               static_cast<int>(static_cast<uint32_t>(g) * (N >> 3) * 4u), 0, 0);
   }
 }
 
@@ -172,17 +175,30 @@ __device__ __forceinline__ void read_group_scales(GroupScales<TW>& gs, const uin
 // the VALU dequant of one step can hide under the matrix work of the previous one.  The
 // order within a step is left to the compiler: explicit scheduling groups (one main MFMA,
 // then two VALU and one LDS read) measured 1.3-2.5 % slower on MI355X at M = 512 and 2048.
+// Lane byte offsets, within an activation stage, of the wave's first fragment of each of a
+// group's four 32-deep steps: row 16 WM wm + (lane & 15), the step's physical chunk.  The
+// stage's own address is then a constant, which the LDS reads carry in their offset field.
+template <int WM>
+struct AOffsets {
+  uint32_t o[4];
+  __device__ __forceinline__ AOffsets(int wm, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 15);  // row & 15 == lane & 15
+      o[j] = static_cast<uint32_t>((16 * WM * wm + (lane & 15)) * kARowBytes + pchunk * 16);
+    }
+  }
+};
+
 template <int WM, int TW>
-__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const BGroup<TW>& b,
-                                          const NibbleConsts& nib, int lane) {
-  const int arow = lane & 15;
+__device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const AOffsets<WM>& ao,
+                                          const BGroup<TW>& b, const NibbleConsts& nib, int lane) {
   const int zshift = awq_shift(lane & 7);
   TileScale ts[TW];
 #pragma unroll
   for (int tt = 0; tt < TW; ++tt) ts[tt] = make_tile_scale(b.sc.s[tt], (b.sc.zw[tt] >> zshift) & 0xFu, lane);
   auto read_a = [&](bf16x8_t (&a)[WM], int j) {
-    const int pchunk = (4 * j + (lane >> 4)) ^ (lane & 15);  // row & 15 == lane & 15
-    const uint8_t* base = stage + arow * kARowBytes + pchunk * 16;
+    const uint8_t* base = stage + ao.o[j];
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt) a[mt] = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
   };

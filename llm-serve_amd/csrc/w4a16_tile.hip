@@ -147,6 +147,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   const int cs0 = act ? nbk * (BN / 2) : nbk * BN;
   const int cs1 = act ? cs0 + up_tiles * kTileCols : cs0 + BN / 2;
   const SzOffsets<TW, BN> szo(act, wn, lane);
+  const AOffsets<WM> ao(wm, lane);
 
   f32x4_t acc[WM][TW];
 #pragma unroll
@@ -181,8 +182,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
       issue_a_stage<NI, NW, BM>(rx, stage(half * P + q), spare, row0, M, K, group_of(b + q), wave, lane);
       // the group's scale and zero instructions go to waves 2q and 2q + 1 (mod NW)
       if (kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
-        issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], g_begin + b + q, b + q < n_items, N, cs0,
-                           cs1, wave == (2 * q) % NW ? 0 : 1, lane);
+        issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], group_of(b + q), N, cs0, cs1,
+                           wave == (2 * q) % NW ? 0 : 1, lane);
     }
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
         for (int q = 0; q < P; ++q) {
           // q is a constant, so the stage is a known LDS object; the slice test is uniform
           if (q % WK == wk && b + q < n_items && active)
-            mma_group<WM, TW>(acc, stage(h * P + q) + wm * 16 * WM * kARowBytes, ring[h * PW + q / WK], nib, lane);
+            mma_group<WM, TW>(acc, stage(h * P + q), ao, ring[h * PW + q / WK], nib, lane);
         }
       }
     }
