@@ -260,18 +260,31 @@ __device__ __forceinline__ f32x4_t mfma4(s16x4_t a, s16x4_t b, f32x4_t c) {
 }
 
 // One tile word of step js -> the B fragment of the main MFMA for the lane's column,
-// bf16_rne((q - z) s) for rows 8 (lane / 16) .. +7.  2 scaling MFMAs, 7 + 4 VALU ops.
-__device__ __forceinline__ bf16x8_t dequant_step(uint32_t w, const TileScale& ts, const NibbleConsts& k) {
+// bf16_rne((q - z) s) for rows 8 (lane / 16) .. +7.  2 scaling MFMAs, 7 + 4 VALU ops, in two
+// phases: the unpack and the scaling MFMAs (dequant_scale), then the rounding to bf16
+// (dequant_pack), which a caller may place after other matrix work so that it does not wait
+// for the scaling MFMAs' results.
+struct ScaledStep {
+  f32x4_t d0, d1;
+};
+
+__device__ __forceinline__ ScaledStep dequant_scale(uint32_t w, const TileScale& ts, const NibbleConsts& k) {
   s16x4_t a[2];
   unpack_biased(a, w, k);
-  const f32x4_t d0 = mfma4(a[0], ts.diag, ts.cin);
-  const f32x4_t d1 = mfma4(a[1], ts.diag, ts.cin);
+  return ScaledStep{mfma4(a[0], ts.diag, ts.cin), mfma4(a[1], ts.diag, ts.cin)};
+}
+
+__device__ __forceinline__ bf16x8_t dequant_pack(const ScaledStep& d) {
   u32x4_t r;
-  r[0] = pack_bf16x2(d0[0], d0[1]);
-  r[1] = pack_bf16x2(d0[2], d0[3]);
-  r[2] = pack_bf16x2(d1[0], d1[1]);
-  r[3] = pack_bf16x2(d1[2], d1[3]);
+  r[0] = pack_bf16x2(d.d0[0], d.d0[1]);
+  r[1] = pack_bf16x2(d.d0[2], d.d0[3]);
+  r[2] = pack_bf16x2(d.d1[0], d.d1[1]);
+  r[3] = pack_bf16x2(d.d1[2], d.d1[3]);
   return __builtin_bit_cast(bf16x8_t, r);
+}
+
+__device__ __forceinline__ bf16x8_t dequant_step(uint32_t w, const TileScale& ts, const NibbleConsts& k) {
+  return dequant_pack(dequant_scale(w, ts, k));
 }
 
 // Word offset of lane `lane`'s 4 words in tile (g, t) of the group-tile layout

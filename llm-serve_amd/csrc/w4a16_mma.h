@@ -229,20 +229,39 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = j & 1;
+    if constexpr (WM >= 6) {
+      // Step j + 1's unpack, scaling MFMAs and fragment reads, free to interleave with step
+      // j's main MFMAs; step j + 1's rounding to bf16 only after them, when its inputs are
+      // ready, so that it does not hold back the main MFMAs queued behind it.  Measured on
+      // MI355X 1-3.7 % faster with 96- and 128-row wave tiles (M = 256 - 2048), and 1-3 %
+      // slower with 32- and 64-row ones, which keep the compiler's order.  (Raising the
+      // wave's issue priority over the main MFMAs, which helped the unphased order at
+      // M = 2048, no longer does.)
+      ScaledStep sd[TW];
+      if (j < 3) {
+        read_a(a[c ^ 1], j + 1);
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) sd[tt] = dequant_scale(b.w[tt][j + 1], ts[tt], nib);
+      }
+#pragma unroll
+      for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[c][mt], bf[c][tt], acc[mt][tt]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < 3) {
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) bf[c ^ 1][tt] = dequant_pack(sd[tt]);
+      }
+      continue;
+    }
     if (j < 3) {
       read_a(a[c ^ 1], j + 1);
       dequant(bf[c ^ 1], j + 1);
     }
-    // 128-row waves raise their issue priority while they issue the step's main MFMAs, so
-    // that the SIMD's other wave (in its dequant or LDS reads) does not starve the matrix
-    // pipe: measured on MI355X 2-3 % faster at M = 2048 (gate_up, down, O), while the
-    // 64-row configurations ran 3-4 % slower with it.
-    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
       for (int tt = 0; tt < TW; ++tt) acc[mt][tt] = mfma16(a[c][mt], bf[c][tt], acc[mt][tt]);
-    if constexpr (WM >= 8) __builtin_amdgcn_s_setprio(0);
   }
 }
 
