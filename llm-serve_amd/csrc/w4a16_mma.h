@@ -207,8 +207,10 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
     for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
   };
   if constexpr (WM * TW > 16) {
-    // Large wave tiles: no register double-buffering (the accumulators fill the AGPRs);
-    // the WM x TW independent MFMAs of a step leave the scheduler enough work to overlap.
+    // Large wave tiles: no register double-buffering (the 128 x 64 tile's accumulators
+    // take half of the 256 registers a wave has at two waves per SIMD, and the kernel uses
+    // 250 of them); the WM x TW independent MFMAs of a step leave the scheduler enough
+    // work to overlap.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       bf16x8_t a[WM];
