@@ -168,13 +168,6 @@ __device__ __forceinline__ void read_group_scales(GroupScales<TW>& gs, const uin
   }
 }
 
-// One 128-deep group: per 32-row step, the matrix-core dequant of the wave's TW weight
-// tiles (2 TW scaling MFMAs), then WM x TW main MFMAs against the wave's 16 WM rows of the
-// LDS activation tile (`stage` points at the first of them).  Software-pipelined: step
-// j + 1's fragments are read and its weights dequantized while step j's main MFMAs run, so
-// the VALU dequant of one step can hide under the matrix work of the previous one.  The
-// order within a step is left to the compiler: explicit scheduling groups (one main MFMA,
-// then two VALU and one LDS read) measured 1.3-2.5 % slower on MI355X at M = 512 and 2048.
 // Lane byte offsets, within an activation stage, of the wave's first fragment of each of a
 // group's four 32-deep steps: row 16 WM wm + (lane & 15), the step's physical chunk.  The
 // stage's own address is then a constant, which the LDS reads carry in their offset field.
@@ -190,6 +183,17 @@ struct AOffsets {
   }
 };
 
+// One 128-deep group: per 32-row step, the matrix-core dequant of the wave's TW weight
+// tiles (2 TW scaling MFMAs), then WM x TW main MFMAs against the wave's 16 WM rows of the
+// LDS activation tile (`stage` is the activation stage, `ao` the lane's offsets of the
+// wave's rows in it).  Software-pipelined: step j + 1's fragments are read and its weights
+// dequantized while step j's main MFMAs run, so the VALU dequant of one step can hide under
+// the matrix work of the previous one.  The
+// order within a step is left to the compiler (except the split of the dequant for wave
+// tiles of 96 and 128 rows, below): explicit scheduling groups (one main MFMA, then two VALU
+// and one LDS read) measured 1.3-2.5 % slower on MI355X at M = 512 and 2048, and with 32-
+// and 64-row wave tiles (the LDS reads, then one MFMA and one to three VALU at a time)
+// 1-7 % slower at M = 48 - 256.
 template <int WM, int TW>
 __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t* stage, const AOffsets<WM>& ao,
                                           const BGroup<TW>& b, const NibbleConsts& nib, int lane) {
