@@ -1,6 +1,6 @@
-"""The reference-side binding shown in INTEGRATION.md, run exactly as written
-(tests/reference_awq_hip.py is that file; tests/test_host_api.py checks that INTEGRATION.md
-holds it verbatim): layers processed by its process_weights_after_loading branch reserve the
+"""The reference-side binding shown in the integration guide, run exactly as written
+(tests/reference_awq_hip.py is that file; tests/test_host_api.py checks that the guide holds
+it verbatim): layers processed by its process_weights_after_loading branch reserve the
 shared workspace for the engine's largest packed M at load time, so chunked-prefill calls
 (down at M = 512, QKV at M = 384, both split-K plans) and a HIP graph capture run without any
 allocation, and agree with the reference (fp32 matmul over the oracle-pinned dequant)."""

@@ -249,15 +249,15 @@ def test_rmsnorm_module_mirrors_the_reference_interface_and_has_no_cpu_path():
 
 
 def test_integration_stub_is_the_tested_file():
-    """INTEGRATION.md's binding stub is tests/reference_awq_hip.py byte for byte, so the code
-    a maintainer copies is the code tests/test_gpu_reference_binding.py runs."""
+    """The integration guide's binding stub is tests/reference_awq_hip.py byte for byte, so
+    the code a maintainer copies is the code tests/test_gpu_reference_binding.py runs."""
     import os
     import re
 
     repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     doc = open(os.path.join(repo, "INTEGRATION.md")).read()
     m = re.search(r"<!-- stub: tests/reference_awq_hip.py -->\n```python\n(.*?)```\n", doc, flags=re.S)
-    assert m, "INTEGRATION.md has no stub block"
+    assert m, "the integration guide has no stub block"
     assert m.group(1) == open(os.path.join(repo, "tests", "reference_awq_hip.py")).read()
 
 
