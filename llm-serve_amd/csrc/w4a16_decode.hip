@@ -209,11 +209,17 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 #pragma unroll
       for (int js = 0; js < 4; ++js) a[mb][js] = st.a[mb][js];
   }
+  // Per 32-row step: every tile's unpack and scaling MFMAs first, then each tile's rounding
+  // to bf16 and main MFMAs, so that a rounding does not wait on the scaling MFMA issued just
+  // before it (the tile-by-tile order measured 3-5 % slower for gate_up at M = 8 and 16).
 #pragma unroll
   for (int js = 0; js < 4; ++js) {
+    ScaledStep sd[TN];
+#pragma unroll
+    for (int tt = 0; tt < TN; ++tt) sd[tt] = dequant_scale(st.w[tt][js], ts[tt], nib);
 #pragma unroll
     for (int tt = 0; tt < TN; ++tt) {
-      const bf16x8_t frag = dequant_step(st.w[tt][js], ts[tt], nib);
+      const bf16x8_t frag = dequant_pack(sd[tt]);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         acc[mb][tt] = mfma16(__builtin_bit_cast(bf16x8_t, a[mb][js]), frag, acc[mb][tt]);
