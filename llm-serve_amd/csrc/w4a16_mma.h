@@ -206,9 +206,14 @@ __device__ __forceinline__ void mma_group(f32x4_t (&acc)[WM][TW], const uint8_t*
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt) a[mt] = *reinterpret_cast<const bf16x8_t*>(base + mt * 16 * kARowBytes);
   };
+  // A step's dequant issues every tile's scaling MFMAs before the first rounding reads one
+  // (tile by tile, each rounding waits on the MFMA just issued: 0.3-2.3 % slower at M >= 128).
   auto dequant = [&](bf16x8_t (&bf)[TW], int j) {
+    ScaledStep sd[TW];
 #pragma unroll
-    for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_step(b.w[tt][j], ts[tt], nib);
+    for (int tt = 0; tt < TW; ++tt) sd[tt] = dequant_scale(b.w[tt][j], ts[tt], nib);
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) bf[tt] = dequant_pack(sd[tt]);
   };
   if constexpr (WM * TW > 16) {
     // Large wave tiles: no register double-buffering (the 128 x 64 tile's accumulators
