@@ -137,7 +137,8 @@ int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
  * tight serving loops, harnesses that forbid allocation): no workspace argument; the split-K
  * workspace is a 48 MiB device array of the library itself, one per GPU, held until the
  * process ends, set up on the first call on each device (symbol lookup, its counters
- * cleared by a kernel on `stream`).  Allocates nothing.  Problems whose plan needs more
+ * cleared by a kernel on `stream`): that first call must not be under graph capture
+ * (W4A16_ERR_LAUNCH, nothing enqueued); later calls may be.  Allocates nothing.  Problems whose plan needs more
  * than 48 MiB of workspace (w4a16_workspace_bytes) are rejected with W4A16_ERR_WORKSPACE
  * before anything is enqueued (every Qwen3-8B projection at M <= 16384 fits).  Calls that
  * overlap on one GPU (two streams at once) share the array and race: serialize them.
@@ -195,10 +196,11 @@ int w4a16_rmsnorm_strided(const uint16_t* x, int rows_inner, int64_t stride_oute
  * the same call, by w4a16_gemm (silu_mul == 0) or w4a16_gemm_silu_mul (silu_mul == 1) of
  * x_norm: y = x_norm @ W, or SiLU(g) * u of it.  x_norm [M, K] (a caller buffer) and
  * residual_out receive the norm's outputs.  At M <= 2 on decode plans without a K split
- * (the Qwen3-8B QKV and gate|up shapes) and with x_norm / residual_out distinct from x and
- * residual, the norm runs inside the GEMM kernel (one launch); otherwise the norm kernel
+ * (the Qwen3-8B QKV and gate|up shapes) and with x_norm / residual_out overlapping neither x
+ * nor residual, the norm runs inside the GEMM kernel (one launch); otherwise the norm kernel
  * writes x_norm and the GEMM reads it back (from L2 at decode sizes).  Arguments as for
- * those two calls; the workspace is w4a16_workspace_bytes(M, K, N, 128).  Argument, shape
+ * those two calls; y must overlap none of x, residual, x_norm and residual_out
+ * (W4A16_ERR_ARG).  The workspace is w4a16_workspace_bytes(M, K, N, 128).  Argument, shape
  * and workspace errors are reported before anything is enqueued.
  * Replaces input_layernorm / post_attention_layernorm followed by qkv_proj / gate_up_proj
  * (qwen3.py:166-173 with layernorm.py:28-40, qwen3.py:126-130). */

@@ -37,6 +37,13 @@ int check_launch(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte (a null pointer: no range).
+bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+  if (!a || !b || na == 0 || nb == 0) return false;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + nb && pb < pa + na;
+}
+
 constexpr int kDecodeMaxM = 64;
 // Both GEMM kernels address their inputs through buffer descriptors with 32-bit byte
 // offsets and use offsets >= 2^31 as "fetch nothing".
@@ -488,13 +495,27 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
     return fail(W4A16_ERR_LAUNCH, "no current HIP device (or device index >= %d)", kScratchDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
+    // The clear must run now: captured into a graph, it would only run at the graph's
+    // replays, and eager calls before that would find the counters uncleared.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(stream, &cap);
+    if (ce != hipSuccess || cap != hipStreamCaptureStatusNone)
+      return fail(W4A16_ERR_LAUNCH,
+                  "the first w4a16_gemm_noalloc call on device %d sets up the library scratch and must not be "
+                  "captured into a graph: make one call outside capture first",
+                  dev);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr)
       return fail(W4A16_ERR_LAUNCH, "hipGetSymbolAddress of the library scratch failed on device %d: %s", dev,
                   hipGetErrorString(e));
-    clear_words<<<16, 256, 0, stream>>>(static_cast<uint32_t*>(ptr), static_cast<int>(kCounterBytes / 4));
-    const hipError_t le = hipGetLastError();
+    // hipLaunchKernel returns this launch's own status (hipGetLastError after a <<<>>> launch
+    // would also report an earlier, unrelated error of the thread).
+    uint32_t* words = static_cast<uint32_t*>(ptr);
+    int n_words = static_cast<int>(kCounterBytes / 4);
+    void* args[] = {&words, &n_words};
+    const hipError_t le =
+        hipLaunchKernel(reinterpret_cast<const void*>(clear_words), dim3(16), dim3(256), args, 0, stream);
     if (le != hipSuccess)
       return fail(W4A16_ERR_LAUNCH, "clearing the library scratch failed on device %d: %s", dev, hipGetErrorString(le));
     g_scratch_ptr[dev] = ptr;
@@ -565,35 +586,46 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
   v = validate_gemm(x_norm, packed, qzeros, scales, y, M, K, N, group_size, silu_mul != 0);
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
+  // y is written while the inputs and the norm's outputs are still being read (by other
+  // workgroups, or by the GEMM that follows the norm kernel): it must overlap none of them.
+  const size_t row_bytes = static_cast<size_t>(M) * K * 2;
+  const size_t y_bytes = static_cast<size_t>(M) * (silu_mul ? N / 2 : N) * 2;
+  if (overlap(y, y_bytes, x, row_bytes) || overlap(y, y_bytes, residual, row_bytes) ||
+      overlap(y, y_bytes, x_norm, row_bytes) || overlap(y, y_bytes, residual_out, row_bytes))
+    return fail(W4A16_ERR_ARG, "y must not overlap x, residual, x_norm or residual_out");
   // Every check that could fail the GEMM runs before the prologue is enqueued.
   GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
-  // With the norm as a prologue every workgroup repeats it, so one-tile 8-wave plans at M = 1
-  // take two tiles per workgroup when they divide N (half the workgroups: QKV 7.23 against
-  // 7.44 us).
-  if (p.regime == W4A16_REGIME_DECODE && M == 1 && p.p0 == 1 && p.p1 == 8 && (N / 16) % 2 == 0 &&
-      w4a16::decode_config_fits(1, 2, p.p2, w4a16::decode_stages_x(M, K, p.split)) &&
-      w4a16::decode_stage_fits(M, K, 2, p.p1, p.p2, p.split) &&
-      w4a16::decode_norm_lds_bytes(M, K, 2, p.p1, p.p2, p.split) > 0)
-    p.p0 = 2;
-  v = check_plan(p, M, K, N, workspace, workspace_bytes);
-  if (v != W4A16_OK) return v;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int up_tiles = silu_mul ? N / 32 : 0;
   // A decode plan with M <= 2 rows staged in LDS, no K split and at most 4 groups per wave
   // (M = 1, 2 at the Qwen3-8B QKV and gate|up shapes) takes the norm as a prologue of the
   // GEMM kernel: one launch, and x_norm is written once by the first workgroup, never read
-  // back.  Its outputs must not alias the inputs (other workgroups still read x and
+  // back.  Its outputs must not overlap the inputs (other workgroups still read x and
   // residual while the first one writes).
-  const bool distinct = x_norm != x && x_norm != residual && (residual_out == nullptr ||
-                                                               (residual_out != x && residual_out != residual));
-  if (p.regime == W4A16_REGIME_DECODE && distinct) {
-    const size_t lds = w4a16::decode_norm_lds_bytes(M, K, p.p0, p.p1, p.p2, p.split);
+  const bool disjoint = !overlap(x_norm, row_bytes, x, row_bytes) && !overlap(x_norm, row_bytes, residual, row_bytes) &&
+                        !overlap(residual_out, row_bytes, x, row_bytes) &&
+                        !overlap(residual_out, row_bytes, residual, row_bytes);
+  if (p.regime == W4A16_REGIME_DECODE && disjoint) {
+    // With the norm as a prologue every workgroup repeats it, so one-tile 8-wave plans at
+    // M = 1 take two tiles per workgroup when they divide N (half the workgroups: QKV 7.23
+    // against 7.44 us).
+    GemmPlan q = p;
+    if (M == 1 && q.p0 == 1 && q.p1 == 8 && (N / 16) % 2 == 0 &&
+        w4a16::decode_config_fits(1, 2, q.p2, w4a16::decode_stages_x(M, K, q.split)) &&
+        w4a16::decode_stage_fits(M, K, 2, q.p1, q.p2, q.split) &&
+        w4a16::decode_norm_lds_bytes(M, K, 2, q.p1, q.p2, q.split) > 0)
+      q.p0 = 2;
+    const size_t lds = w4a16::decode_norm_lds_bytes(M, K, q.p0, q.p1, q.p2, q.split);
     if (lds > 0 && lds <= w4a16::kDecodeMaxLds) {
+      v = check_plan(q, M, K, N, workspace, workspace_bytes);
+      if (v != W4A16_OK) return v;
       const w4a16::DecodeNorm nrm{residual, norm_weight, residual_out, x_norm, eps};
-      return run_plan(p, x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s, up_tiles, nullptr,
+      return run_plan(q, x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes, s, up_tiles, nullptr,
                       &nrm);
     }
   }
+  v = check_plan(p, M, K, N, workspace, workspace_bytes);
+  if (v != W4A16_OK) return v;
   // Otherwise the norm kernel writes x_norm and the GEMM reads it back (from L2 at decode sizes).
   v = check_launch(w4a16::launch_add_rmsnorm(x, residual, norm_weight, x_norm, residual_out, M, K, eps, s),
                    "add_rmsnorm");
@@ -697,12 +729,31 @@ size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
   return fused > plain ? fused : plain;
 }
 
+// The maximum runs the planner at every M <= M_max; a model asks for it once per layer with
+// the same few shapes, so recent answers are kept (a small table, replaced round-robin).
 size_t w4a16_workspace_bytes_max(int M_max, int K, int N, int group_size) {
+  struct Entry {
+    int m_max, k, n, group;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static Entry cache[16];
+  static int used = 0, next = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+      if (cache[i].m_max == M_max && cache[i].k == K && cache[i].n == N && cache[i].group == group_size)
+        return cache[i].bytes;
+  }
   size_t most = 0;
   for (int m = 1; m <= M_max; ++m) {
     const size_t b = w4a16_workspace_bytes(m, K, N, group_size);
     most = b > most ? b : most;
   }
+  std::lock_guard<std::mutex> lock(mu);
+  cache[next] = Entry{M_max, K, N, group_size, most};
+  next = (next + 1) % 16;
+  used = used < 16 ? used + 1 : 16;
   return most;
 }
 

@@ -27,6 +27,7 @@ group-tile layout (``awq_qweight``); ``qzeros`` and ``scales`` are consumed as s
 """
 from __future__ import annotations
 
+import functools
 import threading
 from collections.abc import Mapping
 from dataclasses import dataclass
@@ -98,36 +99,45 @@ class AWQRuntimeConfig:
 
 # ------------------------------------------------------------------ workspace
 class _WorkspacePool:
-    """Split-K workspace shared by all layers issuing on one (device, stream).
+    """Split-K workspace shared by all layers on one device.
 
-    Kernels on one stream run in order, so one buffer per stream serves every layer; it
-    is zero-filled when (re)allocated and the kernels re-arm their counters to zero.
-    ``reserve`` (called by ``process_weights_after_loading`` for the largest M the engine
-    packs) allocates outside the hot path; ``get`` never allocates while the current stream
-    is capturing a HIP graph -- it raises instead, since an allocation there would become
-    part of the graph.  A buffer that is outgrown stays referenced for the life of the
-    pool: a graph captured earlier may still address it, so its memory must not return to
-    the allocator."""
+    One buffer per device serves every layer and every stream: kernels of one stream run in
+    order, and the engine issues its layers on one stream at a time -- eagerly on its
+    current stream, or under ``torch.cuda.graph(graph, pool)`` on torch's capture stream,
+    which waits for the current stream before capturing and is waited for after it
+    (model_runner.py:395-406).  Two GEMMs that may run at the same time on different
+    streams must not share it: pass each its own ``workspace=``.  The buffer is zero-filled
+    when (re)allocated and the kernels re-arm their counters to zero.  ``reserve`` (called
+    by ``process_weights_after_loading`` for the largest M the engine packs) allocates
+    outside the hot path, so that every later call up to that M -- on any stream, captured
+    or not -- finds it big enough; ``get`` never allocates while the current stream is
+    capturing a HIP graph (the allocation would become part of the graph): a request beyond
+    the reservation raises there.  A buffer that is outgrown stays referenced for the life
+    of the pool: a graph captured earlier may still address it, so its memory must not
+    return to the allocator."""
 
     def __init__(self):
         self._lock = threading.Lock()
-        self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+        self._buffers: dict[int, torch.Tensor] = {}
         self._retired: list[torch.Tensor] = []
+
+    @staticmethod
+    def _key(device: torch.device) -> int:
+        return device.index if device.index is not None else torch.cuda.current_device()
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
         if nbytes <= 0:
             return None
-        stream = torch.cuda.current_stream(device).cuda_stream
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        key = self._key(device)
         with self._lock:
             buf = self._buffers.get(key)
             if buf is None or buf.numel() < nbytes:
                 if torch.cuda.is_current_stream_capturing():
                     have = 0 if buf is None else buf.numel()
                     raise RuntimeError(
-                        f"AWQ split-K workspace of {nbytes} bytes needed during HIP graph capture, but this "
-                        f"stream's workspace holds {have}: reserve it before capturing (process the layers on "
-                        f"this stream, or call WORKSPACE.reserve)")
+                        f"AWQ split-K workspace of {nbytes} bytes needed during HIP graph capture, but the "
+                        f"device's workspace holds {have}: reserve it before capturing (raise "
+                        f"max_batched_tokens, or call WORKSPACE.reserve)")
                 if buf is not None:
                     self._retired.append(buf)
                 size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
@@ -139,18 +149,19 @@ class _WorkspacePool:
         self.get(device, nbytes)
 
     def reserved_bytes(self, device: torch.device) -> int:
-        stream = torch.cuda.current_stream(device).cuda_stream
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
         with self._lock:
-            buf = self._buffers.get(key)
+            buf = self._buffers.get(self._key(device))
             return 0 if buf is None else buf.numel()
 
 
 WORKSPACE = _WorkspacePool()
 
 
+@functools.lru_cache(maxsize=256)
 def max_workspace_bytes(k: int, n: int, max_tokens: int, group_size: int = 128) -> int:
-    """Largest workspace any call with M <= max_tokens needs at this shape."""
+    """Largest workspace any call with M <= max_tokens needs at this shape (the library
+    evaluates its planner at every such M, so the result is kept per shape: a model loads
+    the same four shapes once per layer)."""
     return lib().workspace_bytes_max(max_tokens, k, n, group_size)
 
 

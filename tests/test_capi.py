@@ -225,14 +225,20 @@ def test_rmsnorm_entry_points_validate_without_launching(pkg):
     fused = L.dll.w4a16_gemm_rmsnorm
     # (x, residual, weight, eps, x_norm, residual_out, packed, qzeros, scales, y, M, K, N, group,
     #  silu_mul, workspace, workspace_bytes, stream)
-    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 0, 4096, 4096, 128, 0, None, 0, None) == 0
-    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4096, 128, 2, None, 0, None) == 1
-    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4160, 128, 1, None, 0, None) == 2
-    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, 4, 4096, 4096, 64, 0, None, 0, None) == 2
+    # validation never dereferences a pointer: y gets an address far from the other operands
+    y = p + (1 << 30)
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, y, 0, 4096, 4096, 128, 0, None, 0, None) == 0
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, y, 4, 4096, 4096, 128, 2, None, 0, None) == 1
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, y, 4, 4096, 4160, 128, 1, None, 0, None) == 2
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, y, 4, 4096, 4096, 64, 0, None, 0, None) == 2
+    # y overlapping an input or a norm output: rejected (x_norm here starts inside y's range)
+    assert fused(p, None, p, 1e-6, y + 4096, None, p, p, p, y, 4, 4096, 4096, 128, 0, None, 0, None) == 1
+    assert "overlap" in L.last_error()
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, p + 4096, 4, 4096, 4096, 128, 0, None, 0, None) == 1
     # a planned K split needs the workspace: reported before the norm is enqueued
     m, k, n = 32, 4096, 4096
     assert L.split_k(m, k, n) > 1
-    assert fused(p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0, None, 0, None) == 4
+    assert fused(p, None, p, 1e-6, p, None, p, p, p, y, m, k, n, 128, 0, None, 0, None) == 4
 
 
 def test_workspace_bytes_max_covers_every_m(pkg):
@@ -276,7 +282,7 @@ def test_plan_errors_come_before_anything_is_enqueued(pkg):
     need = L.workspace_bytes(m, k, n)
     assert need > 0
     fused = L.dll.w4a16_gemm_rmsnorm
-    args = (p, None, p, 1e-6, p, None, p, p, p, p, m, k, n, 128, 0)
+    args = (p, None, p, 1e-6, p, None, p, p, p, p + (1 << 30), m, k, n, 128, 0)  # y apart from the inputs
     assert fused(*args, p, need - 1, None) == 4 and "workspace" in L.last_error()
     assert fused(*args, p + 16, need, None) == 3 and "256-byte" in L.last_error()
 

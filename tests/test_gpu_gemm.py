@@ -109,10 +109,11 @@ WAVE_COLS = {11: 48}
 TILE_CONFIGS = [(wm, shape, occ, split) for wm, shape, occ in TILE_KERNELS for split in (1, 2, 3, 4)]
 
 
-@pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256)])
+@pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 320), (513, 256), (200, 576)])
 def test_every_tile_configuration(gpu_lib, m, n):
     """Every compiled tile kernel and split: partial m-blocks (rows clamped and dropped),
-    n-blocks partly past N (waves with no columns), uneven K splits."""
+    n-blocks partly past N (waves with no columns; n = 576 puts the last 384-column block of
+    the 48-column-wave shape half past N), uneven K splits."""
     k = 1024
     p = ora.make_problem(seed=200 + m, m=m, k=k, n=n)
     t = to_gpu(p)
