@@ -171,14 +171,20 @@ GemmPlan plan_mid(int M, int K, int N) {
   // Wide layers above M = 128: 96 x 256 tiles while they fill one round (gate_up M = 160 /
   // 192: 51.1 / 52.1 us against 60.7 / 61.3 us for 128 x 256 tiles, which compute 256 rows).
   if (N >= 16384 && M > 128 && ceil_div(M, 96) * ceil_div(N, 256) <= 256) return GemmPlan{W4A16_REGIME_TILE, 6, 2, 3, 1};
+  // Wide layers up to M = 64: 12-wave workgroups of 96 columns (shape 9: 4 K slices x 3 waves
+  // along N), one round of 256 workgroups for gate_up, 32-row tiles up to M = 32 and 64-row
+  // ones beyond (gate_up M = 32 / 48 / 64: 16.9 / 21.0 / 21.4 us against 18.9 / 23.6 / 24.0 us
+  // for 128-column tiles of 2 K slices).
+  if (N >= 16384 && M <= 64 && N % 96 == 0) return GemmPlan{W4A16_REGIME_TILE, M <= 32 ? 2 : 4, 3, 9, 1};
   if (N >= 16384) {
     if (M <= 64) { wm = 4; shape = 5; }
     else { wm = 8; shape = M <= 128 ? 5 : 3; }
   } else if (K >= 8192) {
-    // 64-row tiles up to M = 256 (down M = 160 / 192: 37.0 / 37.3 us against 37.6 / 38.3 us
-    // with 128-row tiles split in four)
-    wm = M <= 64 ? 2 : 4;
-    shape = M <= 32 ? 4 : 5;
+    // 64-row tiles from M = 33 up to M = 256 (down M = 48 / 64: 16.4 / 17.4 us in 4 K slices
+    // against 17.7 / 17.7 us for two 32-row blocks; M = 160 / 192: 37.0 / 37.3 us against
+    // 37.6 / 38.3 us with 128-row tiles split in four)
+    wm = M <= 32 ? 2 : 4;
+    shape = M <= 64 ? 4 : 5;
   } else {
     wm = (M <= 64 || (M <= 128 && N <= 4096)) ? 2 : 4;
     shape = (M > 128 && N > 4096) ? 5 : 4;
@@ -312,13 +318,12 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
 }
 
-// Regime: the decode kernel up to M = 32, and up to M = 48 for wide layers (N >= 16384),
-// where it still beats the tile kernel (gate_up: 19.2 / 24.5 us at M = 32 / 48 against 27.5 /
-// 28.2 us); the tile kernel beyond (M = 48 on the narrow layers: QKV 12.5 vs 13.8 us, O 10.3
-// vs 12.6 us, down 18.6 vs 20.1 us).
+// Regime: the decode kernel below M = 32, the tile kernel from M = 32 on, where its 32-row
+// tiles beat the decode kernel on every Qwen3-8B shape (M = 32: QKV 9.80 / 9.87, O 8.90 /
+// 9.04, gate_up 16.88 / 17.63, down 13.29 / 13.72 us; M = 48: gate_up 21.02 / 22.50 us).
 GemmPlan plan(int M, int K, int N, bool fused = false) {
   if (M == 0) return GemmPlan{W4A16_REGIME_NONE, 0, 0, 0, 1};
-  if (M > (N >= 16384 ? 48 : 32)) return plan_tile(M, K, N, fused);
+  if (M >= 32) return plan_tile(M, K, N, fused);
   return plan_decode(M, K, N);
 }
 
@@ -829,7 +834,8 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
                   w4a16::decode_ring_regs((M + 15) / 16, p0, p2, w4a16::decode_stages_x(M, K, split)));
   } else if (regime == W4A16_REGIME_TILE) {
     if (p0 != 2 && p0 != 4 && p0 != 6 && p0 != 8) return fail(W4A16_ERR_ARG, "tile wm must be 2, 4, 6 or 8");
-    if (p2 < 0 || p2 > 11) return fail(W4A16_ERR_ARG, "tile shape code must be 0..11");
+    if (p2 < 0 || p2 > w4a16::kTileShapeMax)
+      return fail(W4A16_ERR_ARG, "tile shape code must be 0..%d", w4a16::kTileShapeMax);
     if (silu_mul && w4a16::tile_shape(p2).tw % 2)
       return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs a tile wave layout with an even tile count");
     // A wave's output columns must lie wholly inside or wholly past the output width (true for
@@ -872,7 +878,7 @@ size_t w4a16_workspace_bytes_config(int M, int N, int regime, int p0, int split)
   // Tile regime: enough for every tile shape (taller or wider tiles pad more).
   size_t most = workspace_for(GemmPlan{regime, p0, 0, 1, split}, M, N);
   if (regime != W4A16_REGIME_TILE) return most;
-  for (int shape = 2; shape <= 11; ++shape) {
+  for (int shape = 2; shape <= w4a16::kTileShapeMax; ++shape) {
     const size_t b = workspace_for(GemmPlan{regime, p0, 0, shape, split}, M, N);
     most = b > most ? b : most;
   }

@@ -9,6 +9,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "w4a16_common.h"
 
@@ -128,6 +129,35 @@ __device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz,
                                                static_cast<uint32_t>(col >> 3) * 4u,
                                                static_cast<int>(static_cast<uint32_t>(g) * (N >> 3) * 4u), 0, 0);
   }
+}
+
+// The same two instructions for a deep ring of load batches, where every wave must issue the
+// same loads whatever the path: wave w < 2P issues group (w / 2)'s scale (w even) or zero
+// (w odd) instruction into `sz` (that group's stage), every other wave one that fetches
+// nothing into `spare`.  Branch-free: the choices are scalar selects, and lanes without a
+// chunk fetch nothing -- the hardware writes their zeros into bytes of the stage no one
+// reads ([2 BN, 1024) after the scales, past the zero words up to 2048).
+template <int BN>
+__device__ __forceinline__ void issue_sz_uniform(const BSources& src, uint8_t* sz, uint8_t* spare, int g, int N,
+                                                 int cs0, int cs1, bool real, int which, int lane) {
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  static_assert(BN % 32 == 0 && BN / 8 <= 64, "one instruction holds the scales of the column block");
+  constexpr int kHalf = BN / 16;
+  constexpr int kZc = sz_zero_chunks<BN>();
+  uint32_t off;
+  if (which == 0) {
+    const int r = lane >= kHalf;
+    const int col = (r ? cs1 : cs0) + 8 * (lane - r * kHalf);
+    off = lane < 2 * kHalf ? static_cast<uint32_t>(col) * 2u : kOutOfRange;
+  } else {
+    const int r = lane >= kZc;
+    const int col = (r ? cs1 : cs0) + 32 * (lane - r * kZc);
+    off = lane < 2 * kZc ? static_cast<uint32_t>(col >> 3) * 4u : kOutOfRange;
+  }
+  const uint32_t soff = which == 0 ? static_cast<uint32_t>(g) * N * 2u : static_cast<uint32_t>(g) * (N >> 3) * 4u;
+  uint8_t* dst = real ? sz + (which == 0 ? 0 : kSzZeroBase) : spare;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(which == 0 ? src.s : src.z, (lds_void_t*)dst, 16, real ? off : kOutOfRange,
+                                           static_cast<int>(soff), 0, 0);
 }
 
 // LDS byte offsets, within a group's scale/zero stage, of the scale pair word and the zero
@@ -289,6 +319,16 @@ struct TileOut {
   bool active;          // the wave has output columns (col_w < n_out)
 };
 
+// f(std::integral_constant<int, i>{}) for i = 0 .. N - 1, unrolled at compile time.
+template <int N, class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
 // After the K loop: the sum of the workgroup's K slices (WK > 1), the split-K exchange
 // between workgroups (split > 1) and the epilogue.  stage(i), i < S, is LDS region i of
 // kStage bytes; all of them are free here.  Every wave of the workgroup calls this (the
@@ -298,23 +338,43 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
                                             const TileOut& o, int wave_in, int wk, int lane) {
   if constexpr (WK > 1) {
     // Sum the slices' tiles in slice order: slices 1 .. WK - 1 park theirs in the stages
-    // (lane-major fragments, 1 KiB each), slice 0 adds them to its own.
+    // (lane-major fragments, 1 KiB each), slice 0 adds them to its own.  Parking slot
+    // (k2 - 1) kFragsW + f holds fragment f of every wave of slice k2, wave-major, so its
+    // stage and offset are compile-time constants once the slice is known (a uniform switch):
+    // only the wave's index within its slice is added at run time.  (A stage chosen at run
+    // time compiles to a chain of scalar compares, which all waves of a CU queue for on its
+    // shared scalar unit: 1.4 us of the O M=64 launch on MI355X.)
     constexpr int kFragsW = WM * TW;
-    constexpr int kPerStage = kStage / 1024;  // 1 KiB fragments per stage
-    static_assert((WK - 1) * NWG * kFragsW <= S * kPerStage, "slice tiles exceed the stages");
-    auto park = [&](int k2, int f) {  // fragment f of wave wave_in of slice k2 >= 1
-      const int fi = ((k2 - 1) * NWG + wave_in) * kFragsW + f;
-      return reinterpret_cast<f32x4_t*>(stage(fi / kPerStage)) + (fi % kPerStage) * 64 + lane;
+    constexpr int kSlotBytes = NWG * 1024;
+    constexpr int kSlotsPerStage = kStage / kSlotBytes;
+    static_assert(kSlotsPerStage >= 1 && (WK - 1) * kFragsW <= S * kSlotsPerStage, "slice tiles exceed the stages");
+    const uint32_t lane_off = static_cast<uint32_t>(wave_in) * 1024u + static_cast<uint32_t>(lane) * 16u;
+    auto slot_ptr = [&](auto slot_tag) -> f32x4_t* {
+      constexpr int slot = decltype(slot_tag)::value;
+      return reinterpret_cast<f32x4_t*>(stage(slot / kSlotsPerStage) + (slot % kSlotsPerStage) * kSlotBytes + lane_off);
+    };
+    auto park_slice = [&](auto k2_tag) {
+      constexpr int k2 = decltype(k2_tag)::value;
+      static_for<kFragsW>([&](auto f_tag) {
+        constexpr int f = decltype(f_tag)::value;
+        *slot_ptr(std::integral_constant<int, (k2 - 1) * kFragsW + f>{}) = acc[f / TW][f % TW];
+      });
     };
     if (wk > 0) {
-#pragma unroll
-      for (int f = 0; f < kFragsW; ++f) *park(wk, f) = acc[f / TW][f % TW];
+      static_for<WK - 1>([&](auto i_tag) {
+        constexpr int k2 = decltype(i_tag)::value + 1;
+        if (wk == k2) park_slice(std::integral_constant<int, k2>{});
+      });
     }
     __syncthreads();
     if (wk == 0) {
-      for (int k2 = 1; k2 < WK; ++k2)
-#pragma unroll
-        for (int f = 0; f < kFragsW; ++f) acc[f / TW][f % TW] += *park(k2, f);
+      static_for<WK - 1>([&](auto i_tag) {
+        constexpr int k2 = decltype(i_tag)::value + 1;
+        static_for<kFragsW>([&](auto f_tag) {
+          constexpr int f = decltype(f_tag)::value;
+          acc[f / TW][f % TW] += *slot_ptr(std::integral_constant<int, (k2 - 1) * kFragsW + f>{});
+        });
+      });
     }
     __syncthreads();
   }
@@ -381,7 +441,14 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
   constexpr int kRegion = kFull / kParts;
   constexpr int kStageRows = kStage / kRegion;
   static_assert(kStageRows >= 1 && kStageRows * S >= NWG, "epilogue staging exceeds the stages");
-  uint8_t* ep = stage(wave_in / kStageRows) + (wave_in % kStageRows) * kRegion;
+  // the wave's region: stage wave_in / kStageRows, chosen with compile-time stage addresses
+  uint8_t* ep = stage(0) + (wave_in % kStageRows) * kRegion;
+  if constexpr (kStageRows < NWG) {
+    static_for<(NWG + kStageRows - 1) / kStageRows>([&](auto i_tag) {
+      constexpr int i = decltype(i_tag)::value;
+      if (i > 0 && wave_in / kStageRows == i) ep = stage(i) + (wave_in % kStageRows) * kRegion;
+    });
+  }
   auto store_rows = [&](auto cpr_tag, int col0) {
     constexpr int CPR = decltype(cpr_tag)::value;
     constexpr int PITCH = 16 * CPR;

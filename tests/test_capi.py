@@ -87,9 +87,9 @@ def test_regime_boundary_and_split_limits(pkg):
     L = pkg.lib()
     for k, n in QWEN3.values():
         assert L.regime(0, k, n) == 0
-        for m in (1, 4, 8, 16, 32, 33, 48, 49, 64):
-            # decode kernel up to M = 32, and up to M = 48 on wide layers (tile kernel beyond)
-            assert L.regime(m, k, n) == (1 if m <= (48 if n >= 16384 else 32) else 2)
+        for m in (1, 4, 8, 16, 31, 32, 33, 48, 49, 64):
+            # decode kernel below M = 32, the tile kernel from M = 32 on
+            assert L.regime(m, k, n) == (1 if m < 32 else 2)
             assert 1 <= L.split_k(m, k, n) <= k // 128
         for m in (65, 128, 512, 2048, 4096):
             assert L.regime(m, k, n) == 2
@@ -133,7 +133,7 @@ def test_forced_config_validation(pkg):
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 4, 2, 1, None, 0, None) == 1  # bad occupancy
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 2, 2, 3, 1, None, 0, None) == 1  # wm 2 x shape 3: not compiled
     assert "not compiled" in L.last_error()
-    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 12, 1, None, 0, None) == 1  # bad tile shape code
+    assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 4, 2, 18, 1, None, 0, None) == 1  # bad tile shape code
     assert "shape" in L.last_error()
     assert f(p, p, p, p, p, 256, 4096, 4096, 128, 2, 8, 2, 11, 1, None, 0, None) == 2  # 48-column waves split
     assert "multiple of 48" in L.last_error()

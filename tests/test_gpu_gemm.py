@@ -102,7 +102,10 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
                 (4, 9, 3), (2, 9, 3), (4, 10, 3), (8, 11, 2),
-                (4, 11, 2), (6, 3, 2), (6, 8, 2), (6, 11, 2)]
+                (4, 11, 2), (6, 3, 2), (6, 8, 2), (6, 11, 2),
+                # deep rings: four load batches, three in flight while one is computed
+                (2, 12, 2), (4, 12, 2), (2, 13, 2), (4, 13, 2), (8, 13, 2), (2, 14, 1), (4, 14, 1),
+                (4, 15, 3), (2, 15, 3), (2, 16, 1), (4, 16, 1), (8, 16, 1), (4, 17, 1), (8, 17, 1)]
 # output columns of one wave per tile shape code where they are not 32 or 64 (the library
 # rejects an output width that would split a wave)
 WAVE_COLS = {11: 48}
@@ -199,8 +202,8 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
     k, n = QWEN3_SHAPES[shape]
     qw, qz, s = random_awq_gpu(k, n, seed=11)
     packed = awq_mod().repack_awq_qweight(qw)
-    for m in (1, 4, 8, 16, 32, 64):
-        assert pkg().awq_regime(m, k, n) == ("decode" if m <= (48 if n >= 16384 else 32) else "tile")
+    for m in (1, 4, 8, 16, 31, 32, 64):
+        assert pkg().awq_regime(m, k, n) == ("decode" if m < 32 else "tile")
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
         assert_gemm_close(y, full_reference(x, qw, qz, s), (m))
@@ -233,14 +236,15 @@ def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
 
 
 @pytest.mark.parametrize("shape,m", [("qkv", 768), ("o", 768), ("gate_up", 256), ("down", 384), ("down", 768),
-                                     ("gate_up", 48), ("gate_up", 49), ("o", 32), ("o", 33), ("qkv", 33),
+                                     ("gate_up", 31), ("gate_up", 32), ("gate_up", 48), ("gate_up", 49),
+                                     ("o", 31), ("o", 32), ("o", 33), ("qkv", 33), ("down", 31), ("down", 48),
                                      ("down", 33), ("down", 257), ("qkv", 257),
                                      ("gate_up", 160), ("qkv", 160), ("o", 160), ("down", 192), ("o", 640),
                                      ("down", 640), ("qkv", 704), ("down", 896), ("gate_up", 640), ("down", 4)])
 def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
-    (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundaries
-    (decode up to M = 32, up to 48 on the wide layer), the end of the mid-range plans
+    (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundary
+    (decode below M = 32, the tile kernel's 32- and 64-row plans above), the end of the mid-range plans
     (M = 257), the mid-range row blocks that follow M (96 x 256 tiles on gate_up, 32-row
     tiles on QKV / O, 64-row tiles split in K on down at M = 160 / 192), the plans above M =
     512 (96 x 256 tiles with K in two on O / down at 640, the best-filling narrow and wide
@@ -250,7 +254,7 @@ def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
     packed = awq_mod().repack_awq_qweight(qw)
     x = random_x_gpu(m, k, seed=m, outliers=True)
-    assert pkg().awq_regime(m, k, n) == ("decode" if m <= (48 if n >= 16384 else 32) else "tile")
+    assert pkg().awq_regime(m, k, n) == ("decode" if m < 32 else "tile")
     y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
     assert_gemm_close(y, full_reference(x, qw, qz, s), (shape, m))
 
