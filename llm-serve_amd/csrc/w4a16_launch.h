@@ -96,22 +96,16 @@ hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const ui
 // {tw 4, 1 x 4}, 2 = {tw 4, 2 x 4}, 3 = {tw 2, 1 x 8}, 4 = {tw 2, 1 x 2, 4 slices},
 // 5 = {tw 2, 1 x 4, 2 slices}, 6 = {tw 2, 1 x 2, 2 slices}, 7 = {tw 2, 1 x 1, 4 slices},
 // 8 = {tw 4, 1 x 8}, 9 = {tw 2, 1 x 3, 4 slices}, 10 = {tw 2, 1 x 6, 2 slices},
-// 11 = {tw 3, 1 x 8} (plain GEMM only: the fused product pairs tiles within a wave); these
-// keep two load batches in their ring.  Deep rings of four batches: 12 = {tw 2, 1 x 4, 2
-// slices}, 13 = {tw 2, 1 x 8}, 14 = {tw 2, 1 x 2, 2 slices}, 15 = {tw 2, 1 x 6, 2 slices},
-// 16 = {tw 2, 1 x 4}, 17 = {tw 4, 1 x 4}.
-constexpr int kTileShapeMax = 17;
+// 11 = {tw 3, 1 x 8} (plain GEMM only: the fused product pairs tiles within a wave).
+constexpr int kTileShapeMax = 11;
 struct TileShape {
   int tw, nwm, nwn, wk;
-  int db;  // load batches in the ring (2: one in flight while one is computed)
 };
 TileShape tile_shape(int shape);
 // Whether (wm, shape, occ) is compiled; occ = waves per SIMD the register allocation targets.
 // Compiled (wm, shape, occ): (4,1,1), (4,1,2), (8,1,1), (4,2,2), (4,3,2), (8,3,2), (2,4,2),
 // (4,4,2), (2,5,2), (4,5,2), (8,5,2), (4,6,1), (8,6,1), (2,7,1), (4,7,1), (8,8,2), (4,9,3),
-// (2,9,3), (4,10,3), (8,11,2), (4,11,2), (6,3,2), (6,8,2), (6,11,2); deep rings (2,12,2),
-// (4,12,2), (2,13,2), (4,13,2), (8,13,2), (2,14,1), (4,14,1), (4,15,3), (2,15,3), (2,16,1),
-// (4,16,1), (8,16,1), (4,17,1), (8,17,1).
+// (2,9,3), (4,10,3), (8,11,2), (4,11,2), (6,3,2), (6,8,2), (6,11,2).
 bool tile_config_compiled(int wm, int shape, int occ);
 // `partials` holds the split-K fp32 fragments and `counters` one int per output tile (both
 // unused when split == 1).  up_tiles and res as for the decode kernel (N % 128 == 0 when

@@ -131,35 +131,6 @@ __device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz,
   }
 }
 
-// The same two instructions for a deep ring of load batches, where every wave must issue the
-// same loads whatever the path: wave w < 2P issues group (w / 2)'s scale (w even) or zero
-// (w odd) instruction into `sz` (that group's stage), every other wave one that fetches
-// nothing into `spare`.  Branch-free: the choices are scalar selects, and lanes without a
-// chunk fetch nothing -- the hardware writes their zeros into bytes of the stage no one
-// reads ([2 BN, 1024) after the scales, past the zero words up to 2048).
-template <int BN>
-__device__ __forceinline__ void issue_sz_uniform(const BSources& src, uint8_t* sz, uint8_t* spare, int g, int N,
-                                                 int cs0, int cs1, bool real, int which, int lane) {
-  typedef __attribute__((address_space(3))) void lds_void_t;
-  static_assert(BN % 32 == 0 && BN / 8 <= 64, "one instruction holds the scales of the column block");
-  constexpr int kHalf = BN / 16;
-  constexpr int kZc = sz_zero_chunks<BN>();
-  uint32_t off;
-  if (which == 0) {
-    const int r = lane >= kHalf;
-    const int col = (r ? cs1 : cs0) + 8 * (lane - r * kHalf);
-    off = lane < 2 * kHalf ? static_cast<uint32_t>(col) * 2u : kOutOfRange;
-  } else {
-    const int r = lane >= kZc;
-    const int col = (r ? cs1 : cs0) + 32 * (lane - r * kZc);
-    off = lane < 2 * kZc ? static_cast<uint32_t>(col >> 3) * 4u : kOutOfRange;
-  }
-  const uint32_t soff = which == 0 ? static_cast<uint32_t>(g) * N * 2u : static_cast<uint32_t>(g) * (N >> 3) * 4u;
-  uint8_t* dst = real ? sz + (which == 0 ? 0 : kSzZeroBase) : spare;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(which == 0 ? src.s : src.z, (lds_void_t*)dst, 16, real ? off : kOutOfRange,
-                                           static_cast<int>(soff), 0, 0);
-}
-
 // LDS byte offsets, within a group's scale/zero stage, of the scale pair word and the zero
 // word holding the lane's column of each of the wave's tiles.  Plain: the wave's columns are
 // [16 TW wn, 16 TW (wn + 1)) of the block; fused: gate columns [8 TW wn, 8 TW (wn + 1)) of

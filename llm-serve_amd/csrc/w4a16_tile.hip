@@ -66,25 +66,17 @@ __device__ __forceinline__ void issue_a_stage(__amdgpu_buffer_rsrc_t rx, uint8_t
   }
 }
 
-// Groups per load batch: with a K split inside the workgroup, one per slice (WK); otherwise,
-// in a ring of two batches, two when four BM-row activation stages fit in 128 KiB of LDS and
-// the register ring of four groups fits the occupancy (always for 32-column waves), else
-// one; in a deeper ring (DB > 2 batches), one.
-constexpr int tile_batch(int bm, int tw, int occ, int wk, int db) {
-  return wk > 1 ? wk : db > 2 ? 1 : (4 * bm * kARowBytes <= 128 * 1024 && (tw == 2 || occ == 1) ? 2 : 1);
+// Groups per load batch: with a K split inside the workgroup, one per slice (WK); otherwise
+// two when four BM-row activation stages fit in 128 KiB of LDS and the register ring of four
+// groups fits the occupancy (always for 32-column waves), else one.
+constexpr int tile_batch(int bm, int tw, int occ, int wk) {
+  return wk > 1 ? wk : (4 * bm * kARowBytes <= 128 * 1024 && (tw == 2 || occ == 1) ? 2 : 1);
 }
-
-// s_waitcnt immediates: wait until at most n vector-memory loads of the wave are
-// outstanding (vmcnt(n), 0 <= n < 64) and for nothing else (expcnt 7, lgkmcnt 15), or also
-// for every LDS access (lgkmcnt(0)).
-constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-constexpr int vmcnt_lgkm0_imm(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 
 // OCC = waves per SIMD the register allocation must allow (1, 2 or 3; 8-wave workgroups
 // always put two waves on every SIMD, 12-wave ones three).  WK = K slices inside the
-// workgroup.  DB = load batches in the ring (LDS stages and register slots): DB - 1 batches
-// are in flight while one is computed.
-template <int WM, int TW, int NWM, int NWN, int OCC, int WK, int DB>
+// workgroup.
+template <int WM, int TW, int NWM, int NWN, int OCC, int WK>
 __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const uint16_t* __restrict__ x,
                                                                    const uint32_t* __restrict__ packed,
                                                                    const uint32_t* __restrict__ qzeros,
@@ -102,11 +94,10 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   static_assert(BM % 4 == 0, "activation stages hold whole row quads");
   static_assert(NW >= 2, "a group's scale and zero loads are issued by two waves");
   constexpr int kStage = BM * kARowBytes;
-  constexpr int P = tile_batch(BM, TW, OCC, WK, DB);  // groups per load batch
-  constexpr int S = DB * P;                           // LDS stages: DB batches
-  constexpr int PW = P / WK;                          // groups of a batch each wave computes
-  static_assert(DB >= 2 && PW * WK == P && S <= 8, "load batches hold whole slices, at most 8 stages");
-  static_assert(S * kStage <= 144 * 1024, "the activation stages exceed the LDS");
+  constexpr int P = tile_batch(BM, TW, OCC, WK);  // groups per load batch
+  constexpr int S = 2 * P;                        // LDS stages: two batches
+  constexpr int PW = P / WK;                      // groups of a batch each wave computes
+  static_assert(PW * WK == P && S <= 8, "load batches hold whole slices, at most 8 stages");
   // One LDS object per stage: the compiler then knows that a direct-to-LDS load into one
   // stage does not alias the reads of another, and does not wait for the loads just issued
   // (the next batch's stages) before reading the current one.
@@ -125,8 +116,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   // Scales and zero words of stage i's group in LDS (kStageSZ), or in the register ring.
   constexpr bool kStageSZ = WK <= 2;
   __shared__ __attribute__((aligned(16))) uint8_t sz_stage[kStageSZ ? S : 1][kStageSZ ? kSzStageBytes : 16];
-  // uneven stage issue; the no-op scale / zero instructions of a deep ring
-  __shared__ __attribute__((aligned(1024))) uint8_t spare[NI * NW * 4 == BM && !(kStageSZ && DB > 2) ? 16 : 1024];
+  __shared__ __attribute__((aligned(1024))) uint8_t spare[NI * NW * 4 == BM ? 16 : 1024];  // uneven stage issue
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63;
@@ -167,42 +157,33 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
 
   // Batched pipeline over the workgroup's groups (item i = group g_begin + i).  Items travel
   // in batches of P: batch b (items b .. b + P - 1) lives in LDS stages P h .. P h + P - 1,
-  // h = (b / P) % DB; a wave of slice wk computes items b + wk + WK j (j < PW) of the batch,
-  // whose weights sit in its register slots PW h + j.  The first DB - 1 batches are issued
-  // up front.  At the start of batch b every wave waits until its own loads of batch b have
-  // landed -- vector-memory loads complete in issue order, direct-to-LDS ones included, so
-  // vmcnt((DB - 2) L) leaves the L loads of each of the DB - 2 later batches in flight -- and
-  // passes one barrier, after which batch b's data is visible and every wave has finished
-  // batch b - P; it then issues batch b + (DB - 1) P into the stages batch b - P used and
-  // computes batch b.  Each load therefore has DB - 1 batches of compute to land, and there
-  // is one wait and one barrier per batch.
+  // h = (b / P) % 2; a wave of slice wk computes items b + wk + WK j (j < PW) of the batch,
+  // whose weights sit in its register slots PW h + j.  At the start of batch b every wave
+  // waits for all of its outstanding loads (direct-to-LDS loads may complete out of order
+  // with the register loads issued after them, so only a full wait covers them) and passes
+  // one barrier -- after which batch b's data is visible and every wave has finished batch
+  // b - P -- then issues batch b + P into the other half and computes batch b.  Each load
+  // therefore has a batch of compute to land, and there is one wait and one barrier per
+  // batch.
   const NibbleConsts nib = nibble_consts();
   const __amdgpu_buffer_rsrc_t rx = make_buffer(x, static_cast<uint32_t>(M) * K * 2u);
   const BSources bsrc{make_buffer(packed, static_cast<uint32_t>(K) * (N / 2)),
                       make_buffer(scales, static_cast<uint32_t>(G) * N * 2u),
                       make_buffer(qzeros, static_cast<uint32_t>(G) * (N / 8) * 4u)};
+  constexpr int kWaitAll = 0x0F70;  // vmcnt(0); expcnt and lgkmcnt not waited for
   const int n_items = g_end - g_begin;
-  BGroup<TW> ring[DB * PW];
+  BGroup<TW> ring[2 * PW];
   // A prefetch past the workgroup's last item reloads that item's group (never consumed);
   // ranges are never empty (split <= K / 128).
   auto group_of = [&](int item) { return g_begin + (item < n_items ? item : n_items - 1); };
-  auto issue = [&](int half, int b) {  // batch starting at item b into ring slot `half`
+  auto issue = [&](int half, int b) {  // batch starting at item b into half `half`
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       issue_a_stage<NI, NW, BM>(rx, stage(half * P + q), spare, row0, M, K, group_of(b + q), wave, lane);
       // the group's scale and zero instructions go to waves 2q and 2q + 1 (mod NW)
-      if (DB == 2 && kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
+      if (kStageSZ && (wave == (2 * q) % NW || wave == (2 * q + 1) % NW))
         issue_sz_stage<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], group_of(b + q), N, cs0, cs1,
                            wave == (2 * q) % NW ? 0 : 1, lane);
-    }
-    // In a deep ring every wave issues the same loads per batch, with no branch around any
-    // of them: one scale or zero instruction each (NW >= 2P), see issue_sz_uniform.
-    if constexpr (kStageSZ && DB > 2) {
-      static_assert(NW >= 2 * P, "one scale or zero instruction per wave and batch");
-      const bool real = wave < 2 * P;
-      const int q = real ? wave >> 1 : 0;
-      issue_sz_uniform<BN>(bsrc, sz_stage[kStageSZ ? half * P + q : 0], spare, group_of(b + q), N, cs0, cs1, real,
-                           wave & 1, lane);
     }
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
@@ -210,83 +191,35 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
       load_b_group<TW, !kStageSZ>(ring[half * PW + j], bsrc, group_of(item), active, N, t0, dt, lane);
     }
   };
-  // the wave's groups of batch b (items b + wk + WK j) against its stages: q is a constant,
-  // so the stage is a known LDS object; the slice test is uniform.  (Staged scales are read
-  // before the next batch's loads are issued: see read_group_scales.)
-  auto compute = [&](int h, int b) {
+  issue(0, 0);
+  for (int b0 = 0; b0 < n_items; b0 += 2 * P) {
 #pragma unroll
-    for (int q = 0; q < P; ++q)
-      if (q % WK == wk && b + q < n_items && active)
-        mma_group<WM, TW>(acc, stage(h * P + q), ao, ring[h * PW + q / WK], nib, lane);
-  };
-  if constexpr (DB == 2) {
-    issue(0, 0);
-    for (int b0 = 0; b0 < n_items; b0 += 2 * P) {
+    for (int h = 0; h < 2; ++h) {  // two batches per trip, so every stage index is a constant
+      const int b = b0 + h * P;
+      // Past the last item nothing is waited for or issued: no barrier would separate
+      // those loads from other waves still reading the other half, and an out-of-range
+      // direct-to-LDS load may still write its zeros there.
+      if (b < n_items) {
+        __builtin_amdgcn_s_waitcnt(kWaitAll);  // batch b's LDS and register loads have landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kStageSZ) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {  // two batches per trip, so every stage index is a constant
-        const int b = b0 + h * P;
-        // Past the last item nothing is waited for or issued: no barrier would separate
-        // those loads from other waves still reading the other half, and an out-of-range
-        // direct-to-LDS load may still write its zeros there.
-        if (b < n_items) {
-          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // batch b's LDS and register loads have landed
-          __syncthreads();
+          for (int j = 0; j < PW; ++j)  // the wave's groups of the batch: items b + wk + WK j
+            read_group_scales<TW, BN>(ring[h * PW + j].sc, sz_stage[h * P + wk + WK * j], szo);
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (kStageSZ) {
+        }
+        // nothing past the last item (the full wait at the next batch would wait for it)
+        if (b + P < n_items) issue(1 - h, b + P);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < PW; ++j)
-              read_group_scales<TW, BN>(ring[h * PW + j].sc, sz_stage[h * P + wk + WK * j], szo);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          // nothing past the last item (the full wait at the next batch would wait for it)
-          if (b + P < n_items) issue(1 - h, b + P);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < P; ++q) {
-            if (q % WK == wk && b + q < n_items && active)
-              mma_group<WM, TW>(acc, stage(h * P + q), ao, ring[h * PW + q / WK], nib, lane);
-          }
+        for (int q = 0; q < P; ++q) {
+          // q is a constant, so the stage is a known LDS object; the slice test is uniform
+          if (q % WK == wk && b + q < n_items && active)
+            mma_group<WM, TW>(acc, stage(h * P + q), ao, ring[h * PW + q / WK], nib, lane);
         }
       }
     }
-  } else {
-    // Every batch issues L loads per wave, so vmcnt((DB - 2) L) leaves the DB - 2 later
-    // batches in flight.  The barrier orders LDS alone: the wave's own wait has covered its
-    // direct-to-LDS loads of batch b and, with lgkmcnt(0), its reads of batch b - P (whose
-    // stages are refilled next); a workgroup release fence here would also wait for the
-    // later batches' direct-to-LDS loads.  The loop is left at the first batch past the
-    // last item, so every path through its body has issued the same loads (the compiler's
-    // own waits for the ring registers are then exact).
-    constexpr int L = P * NI + PW * TW * (kStageSZ ? 1 : 3) + (kStageSZ ? 1 : 0);
-    static_assert((DB - 2) * L < 64, "the loads in flight exceed what vmcnt counts");
-#pragma unroll
-    for (int d = 0; d + 1 < DB; ++d) {
-      issue(d, d * P);
-      __builtin_amdgcn_sched_barrier(0);  // in ring order, so slot d's loads are the older ones
-    }
-    [&] {
-      for (int b0 = 0;; b0 += DB * P) {
-#pragma unroll
-        for (int h = 0; h < DB; ++h) {  // DB batches per trip, so every stage index is a constant
-          const int b = b0 + h * P;
-          if (b >= n_items) return;
-          __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm((DB - 2) * L));
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_sched_barrier(0);
-          if constexpr (kStageSZ) {
-#pragma unroll
-            for (int j = 0; j < PW; ++j)
-              read_group_scales<TW, BN>(ring[h * PW + j].sc, sz_stage[h * P + wk + WK * j], szo);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          issue((h + DB - 1) % DB, b + (DB - 1) * P);
-          __builtin_amdgcn_sched_barrier(0);
-          compute(h, b);
-        }
-      }
-    }();
   }
   __builtin_amdgcn_s_waitcnt(0);  // trailing (empty) loads, before the stages are reused
   __syncthreads();
@@ -296,7 +229,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   finish_tile<WM, TW, NWG, WK, S, kStage>(acc, stage, &is_last, out, wave_in, wk, lane);
 }
 
-template <int WM, int TW, int NWM, int NWN, int OCC, int WK, int DB>
+template <int WM, int TW, int NWM, int NWN, int OCC, int WK>
 static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                                 const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
                                 int* counters, int M, int K, int N, int split, int up_tiles, hipStream_t stream) {
@@ -305,55 +238,40 @@ static hipError_t launch_tile_t(const uint16_t* x, const uint32_t* packed, const
   const int m_blocks = (M + BM - 1) / BM;
   const int n_blocks = (N + BN - 1) / BN;
   const unsigned grid = static_cast<unsigned>(m_blocks * n_blocks * split);
-  tile_kernel<WM, TW, NWM, NWN, OCC, WK, DB><<<grid, 64 * NWM * NWN * WK, 0, stream>>>(
+  tile_kernel<WM, TW, NWM, NWN, OCC, WK><<<grid, 64 * NWM * NWN * WK, 0, stream>>>(
       x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, m_blocks, n_blocks, up_tiles);
   return hipGetLastError();
 }
 
 TileShape tile_shape(int shape) {
   switch (shape) {
-    case 2: return TileShape{4, 2, 4, 1, 2};  // 8 waves: 2 along M x 4 along N, 64 columns each
-    case 3: return TileShape{2, 1, 8, 1, 2};  // 8 waves along N, 32 columns each
-    case 4: return TileShape{2, 1, 2, 4, 2};  // 8 waves: 4 K slices x 2 along N, 32 columns each
-    case 5: return TileShape{2, 1, 4, 2, 2};  // 8 waves: 2 K slices x 4 along N, 32 columns each
-    case 6: return TileShape{2, 1, 2, 2, 2};  // 4 waves: 2 K slices x 2 along N, 32 columns each
-    case 7: return TileShape{2, 1, 1, 4, 2};  // 4 waves: 4 K slices x 32 columns
-    case 8: return TileShape{4, 1, 8, 1, 2};  // 8 waves along N, 64 columns each
-    case 9: return TileShape{2, 1, 3, 4, 2};   // 12 waves: 4 K slices x 3 along N, 32 columns each
-    case 10: return TileShape{2, 1, 6, 2, 2};  // 12 waves: 2 K slices x 6 along N, 32 columns each
-    case 11: return TileShape{3, 1, 8, 1, 2};  // 8 waves along N, 48 columns each (plain GEMM only)
-    // Deep rings (four batches, three in flight while one is computed):
-    case 12: return TileShape{2, 1, 4, 2, 4};  // shape 5's waves
-    case 13: return TileShape{2, 1, 8, 1, 4};  // shape 3's waves, one group per batch
-    case 14: return TileShape{2, 1, 2, 2, 4};  // shape 6's waves
-    case 15: return TileShape{2, 1, 6, 2, 4};  // shape 10's waves
-    case 16: return TileShape{2, 1, 4, 1, 4};  // 4 waves along N, 32 columns each, one group per batch
-    case 17: return TileShape{4, 1, 4, 1, 4};  // shape 1's waves, one group per batch
-    default: return TileShape{4, 1, 4, 1, 2};  // 4 waves along N, 64 columns each
+    case 2: return TileShape{4, 2, 4, 1};  // 8 waves: 2 along M x 4 along N, 64 columns each
+    case 3: return TileShape{2, 1, 8, 1};  // 8 waves along N, 32 columns each
+    case 4: return TileShape{2, 1, 2, 4};  // 8 waves: 4 K slices x 2 along N, 32 columns each
+    case 5: return TileShape{2, 1, 4, 2};  // 8 waves: 2 K slices x 4 along N, 32 columns each
+    case 6: return TileShape{2, 1, 2, 2};  // 4 waves: 2 K slices x 2 along N, 32 columns each
+    case 7: return TileShape{2, 1, 1, 4};  // 4 waves: 4 K slices x 32 columns
+    case 8: return TileShape{4, 1, 8, 1};  // 8 waves along N, 64 columns each
+    case 9: return TileShape{2, 1, 3, 4};   // 12 waves: 4 K slices x 3 along N, 32 columns each
+    case 10: return TileShape{2, 1, 6, 2};  // 12 waves: 2 K slices x 6 along N, 32 columns each
+    case 11: return TileShape{3, 1, 8, 1};  // 8 waves along N, 48 columns each (plain GEMM only)
+    default: return TileShape{4, 1, 4, 1};  // 4 waves along N, 64 columns each
   }
 }
 
 // The compiled (wm, tile shape, occupancy) combinations, in one list for the launcher and
-// for tile_config_compiled: X(WM, TW, NWM, NWN, OCC, WK, DB).
-#define W4A16_TILE_CONFIGS(X)                                                                                   \
-  X(4, 4, 1, 4, 1, 1, 2) X(4, 4, 1, 4, 2, 1, 2) X(8, 4, 1, 4, 1, 1, 2) X(4, 4, 2, 4, 2, 1, 2)                   \
-  X(4, 2, 1, 8, 2, 1, 2) X(8, 2, 1, 8, 2, 1, 2)                                                                 \
-  X(2, 2, 1, 2, 2, 4, 2) X(4, 2, 1, 2, 2, 4, 2) X(2, 2, 1, 4, 2, 2, 2) X(4, 2, 1, 4, 2, 2, 2)                   \
-  X(8, 2, 1, 4, 2, 2, 2) X(4, 2, 1, 2, 1, 2, 2) X(8, 2, 1, 2, 1, 2, 2) X(2, 2, 1, 1, 1, 4, 2)                   \
-  X(4, 2, 1, 1, 1, 4, 2) X(8, 4, 1, 8, 2, 1, 2) X(4, 2, 1, 3, 3, 4, 2) X(2, 2, 1, 3, 3, 4, 2)                   \
-  X(4, 2, 1, 6, 3, 2, 2) X(8, 3, 1, 8, 2, 1, 2) X(4, 3, 1, 8, 2, 1, 2) X(6, 2, 1, 8, 2, 1, 2)                   \
-  X(6, 4, 1, 8, 2, 1, 2) X(6, 3, 1, 8, 2, 1, 2)                                                                 \
-  X(2, 2, 1, 4, 2, 2, 4) X(4, 2, 1, 4, 2, 2, 4) X(2, 2, 1, 8, 2, 1, 4) X(4, 2, 1, 8, 2, 1, 4)                   \
-  X(8, 2, 1, 8, 2, 1, 4) X(2, 2, 1, 2, 1, 2, 4) X(4, 2, 1, 2, 1, 2, 4) X(4, 2, 1, 6, 3, 2, 4)                   \
-  X(2, 2, 1, 6, 3, 2, 4) X(2, 2, 1, 4, 1, 1, 4) X(4, 2, 1, 4, 1, 1, 4) X(8, 2, 1, 4, 1, 1, 4)                   \
-  X(4, 4, 1, 4, 1, 1, 4) X(8, 4, 1, 4, 1, 1, 4)
+// for tile_config_compiled: X(WM, TW, NWM, NWN, OCC, WK).
+#define W4A16_TILE_CONFIGS(X)                                                                 \
+  X(4, 4, 1, 4, 1, 1) X(4, 4, 1, 4, 2, 1) X(8, 4, 1, 4, 1, 1) X(4, 4, 2, 4, 2, 1) X(4, 2, 1, 8, 2, 1)  \
+  X(8, 2, 1, 8, 2, 1)                                                                         \
+  X(2, 2, 1, 2, 2, 4) X(4, 2, 1, 2, 2, 4) X(2, 2, 1, 4, 2, 2) X(4, 2, 1, 4, 2, 2) X(8, 2, 1, 4, 2, 2)  \
+  X(4, 2, 1, 2, 1, 2) X(8, 2, 1, 2, 1, 2) X(2, 2, 1, 1, 1, 4) X(4, 2, 1, 1, 1, 4) X(8, 4, 1, 8, 2, 1) X(4, 2, 1, 3, 3, 4) X(2, 2, 1, 3, 3, 4) \
+  X(4, 2, 1, 6, 3, 2) X(8, 3, 1, 8, 2, 1) X(4, 3, 1, 8, 2, 1) X(6, 2, 1, 8, 2, 1) X(6, 4, 1, 8, 2, 1) X(6, 3, 1, 8, 2, 1)
 
 bool tile_config_compiled(int wm, int shape, int occ) {
   const TileShape ts = tile_shape(shape);
-#define W4A16_TILE_MATCH(WM_, TW_, NWM_, NWN_, OCC_, WK_, DB_)                                     \
-  if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_ && ts.wk == WK_ && \
-      ts.db == DB_)                                                                               \
-    return true;
+#define W4A16_TILE_MATCH(WM_, TW_, NWM_, NWN_, OCC_, WK_) \
+  if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_ && ts.wk == WK_) return true;
   W4A16_TILE_CONFIGS(W4A16_TILE_MATCH)
 #undef W4A16_TILE_MATCH
   return false;
@@ -364,10 +282,10 @@ hipError_t launch_tile_cfg(const uint16_t* x, const uint32_t* packed, const uint
                            int M, int K, int N, int wm, int shape, int occ, int split, int up_tiles,
                            hipStream_t stream) {
   const TileShape ts = tile_shape(shape);
-#define W4A16_TILE_LAUNCH(WM_, TW_, NWM_, NWN_, OCC_, WK_, DB_)                                                     \
-  if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_ && ts.wk == WK_ && ts.db == DB_) \
-    return launch_tile_t<WM_, TW_, NWM_, NWN_, OCC_, WK_, DB_>(x, packed, qzeros, scales, y, res, partials, counters, \
-                                                               M, K, N, split, up_tiles, stream);
+#define W4A16_TILE_LAUNCH(WM_, TW_, NWM_, NWN_, OCC_, WK_)                                                       \
+  if (wm == WM_ && ts.tw == TW_ && ts.nwm == NWM_ && ts.nwn == NWN_ && occ == OCC_ && ts.wk == WK_)              \
+    return launch_tile_t<WM_, TW_, NWM_, NWN_, OCC_, WK_>(x, packed, qzeros, scales, y, res, partials, counters, M, \
+                                                          K, N, split, up_tiles, stream);
   W4A16_TILE_CONFIGS(W4A16_TILE_LAUNCH)
 #undef W4A16_TILE_LAUNCH
   return hipErrorInvalidValue;

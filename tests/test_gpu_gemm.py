@@ -102,10 +102,7 @@ def test_decode_long_k_stays_within_lds(gpu_lib, m):
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
                 (4, 9, 3), (2, 9, 3), (4, 10, 3), (8, 11, 2),
-                (4, 11, 2), (6, 3, 2), (6, 8, 2), (6, 11, 2),
-                # deep rings: four load batches, three in flight while one is computed
-                (2, 12, 2), (4, 12, 2), (2, 13, 2), (4, 13, 2), (8, 13, 2), (2, 14, 1), (4, 14, 1),
-                (4, 15, 3), (2, 15, 3), (2, 16, 1), (4, 16, 1), (8, 16, 1), (4, 17, 1), (8, 17, 1)]
+                (4, 11, 2), (6, 3, 2), (6, 8, 2), (6, 11, 2)]
 # output columns of one wave per tile shape code where they are not 32 or 64 (the library
 # rejects an output width that would split a wave)
 WAVE_COLS = {11: 48}
