@@ -64,6 +64,9 @@ Also reported (not part of `value`):
     input_layernorm + QKV and post_attention_layernorm + gate|up + SiLU * up (the residual
     alternating between two buffers), plain O and down -- 144 GEMM launches per step, plus 72
     norm launches where M > 2 (at M <= 2 the norm runs inside the decode kernel), one graph;
+    `norm_stats` (M < 32): the same step with each norm split across the GEMMs around it
+    (O and down through w4a16_gemm_residual_stats, gate|up and QKV through
+    w4a16_gemm_rmsnorm_stats) -- 144 GEMM launches and no norm launch after layer 0's;
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
     in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
 
@@ -429,6 +432,44 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
 
         ms = time_graph(step, stream, reps)
         out[f"M={m}"] = {"step_us": round(ms * 1e3, 1), "us_per_token": round(ms * 1e3 / m, 2)}
+        if m >= 32:
+            continue
+        # Decode sizes: the norms split across the GEMMs around them.  O and down add the
+        # residual in place and leave the fp32 sum s and its tile sums of squares; gate|up and
+        # the next layer's QKV normalize s in their fragment loads.  Layer 0's QKV keeps
+        # w4a16_gemm_rmsnorm (its norm input comes from outside the stack).
+        s_buf = torch.empty((m, kq), dtype=torch.float32, device=dev)
+        ssq = torch.empty((m, kq // 16), dtype=torch.float32, device=dev)
+
+        def producer(x, w, k, n, sp):
+            packed, qzeros, scales = w
+            if lib.dll.w4a16_gemm_residual_stats(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                 scales.data_ptr(), res2.data_ptr(), s_buf.data_ptr(),
+                                                 res2.data_ptr(), ssq.data_ptr(), m, k, n, 128, wsp, ws_len,
+                                                 sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def consumer(w, y, k, n, silu, sp):
+            packed, qzeros, scales = w
+            if lib.dll.w4a16_gemm_rmsnorm_stats(s_buf.data_ptr(), ssq.data_ptr(), nw.data_ptr(), 1e-6, None,
+                                                packed.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(),
+                                                m, k, n, 128, silu, wsp, ws_len, sp) != 0:
+                raise RuntimeError(lib.last_error())
+
+        def step_stats():
+            sp = torch.cuda.current_stream(dev).cuda_stream
+            for li, layer in enumerate(layers):
+                if li == 0:
+                    normed(layer["qkv"], qkv, kq, nq, 0, res, res2, sp)
+                else:
+                    consumer(layer["qkv"], qkv, kq, nq, 0, sp)
+                attn.copy_(qkv[:, :kq])
+                producer(attn, layer["o"], *SHAPES["o"], sp)
+                consumer(layer["gate_up"], act, ki, ni, 1, sp)
+                producer(act, layer["down"], *SHAPES["down"], sp)
+
+        ms_s = time_graph(step_stats, stream, reps)
+        out[f"M={m}"]["norm_stats"] = {"step_us": round(ms_s * 1e3, 1), "us_per_token": round(ms_s * 1e3 / m, 2)}
     return out
 
 
@@ -685,8 +726,9 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
     rotating weights.  SHAPE+silu:M
     launches the fused SiLU * up GEMM of that (gate|up) shape, a trailing +norm the
     RMSNorm(+residual) prologue with it (w4a16_gemm_rmsnorm); quantize:0 launches the
-    quantizer over a [24576, 4096] bf16 weight."""
-    name, m = spec.split(":")
+    quantizer over a [24576, 4096] bf16 weight.  SHAPE:M:decode forces the decode kernel
+    with its own plan (w4a16_plan entry 4) where the planner picks the tile kernel."""
+    name, m, *force = spec.split(":")
     m = int(m)
     if name == "quantize":
         q = quantize_throughput(lib, dev, torch.cuda.Stream(dev), steps)
@@ -718,6 +760,18 @@ def profile_point(lib, spec: str, steps: int, dev) -> int:
     x = torch.randn((m, k), device=dev).to(torch.bfloat16)
     p = Point(lib, name, m, k, n, weights, x)
     stream = torch.cuda.current_stream(dev)
+    if force:
+        if force != ["decode"] or normed or fused:
+            raise ValueError(f"unknown profile point {spec}")
+        regime, p0, p1, p2, split = lib.plan(m, k, n, 4)
+        p.regime, p.split = "decode", split
+        ws_len = max(lib.workspace_bytes_config(m, n, regime, p0, split), 256)
+        p.ws = torch.zeros(ws_len, dtype=torch.uint8, device=dev)
+        p.ws_len = ws_len
+
+        def entry(xp, pp, zp, sp_, yp, m_, k_, n_, g, wsp, wsl, stp):
+            return lib.dll.w4a16_gemm_config(xp, pp, zp, sp_, yp, m_, k_, n_, g, regime, p0, p1, p2, split, wsp, wsl,
+                                             stp)
 
     def launch_all():
         for packed, qzeros, scales in weights:

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define W4A16_ABI_VERSION 4
+#define W4A16_ABI_VERSION 5
 
 enum w4a16_status {
   W4A16_OK = 0,
@@ -53,7 +53,7 @@ enum w4a16_dtype {
 
 enum w4a16_regime_id {
   W4A16_REGIME_NONE = 0,   /* M == 0: nothing to launch */
-  W4A16_REGIME_DECODE = 1, /* M <= 32 (M <= 48 when N >= 16384): split-K, HBM-bound kernel */
+  W4A16_REGIME_DECODE = 1, /* M < 32: split-K, HBM-bound kernel */
   W4A16_REGIME_TILE = 2    /* larger M: LDS-tiled bf16 MFMA GEMM */
 };
 
@@ -210,6 +210,40 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
                        int group_size, int silu_mul, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* The RMSNorm that follows the O or down projection, split across that GEMM and the next
+ * one so that no norm launch sits between them (decode sizes, 0 <= M < 32; M >= 32 is
+ * W4A16_ERR_SHAPE: use w4a16_gemm_residual / w4a16_gemm and w4a16_gemm_rmsnorm there).
+ * Producer: h = bf16(x[M, K] @ W) is added to residual [M, N] in fp32 in the epilogue, as
+ * the reference's add_rms_forward does (layernorm.py:35-36): s_out[M, N] (fp32) =
+ * float(h) + float(residual), residual_out = bf16(s_out) (may be residual itself, in place),
+ * and ssq_out[M, N / 16] (fp32) holds, per row, the sum of s^2 over each 16-column tile.  h
+ * itself is not stored.  x, W, workspace as w4a16_gemm; every pointer 16-byte aligned; the
+ * outputs overlap neither each other (but for residual_out == residual) nor the inputs.
+ * Replaces o_proj / down_proj followed by the residual add and the sum of squares of the
+ * next RMSNorm (qwen3.py:170-174 with layernorm.py:35-38). */
+int w4a16_gemm_residual_stats(const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
+                              const uint16_t* scales, const uint16_t* residual, float* s_out,
+                              uint16_t* residual_out, float* ssq_out, int M, int K, int N,
+                              int group_size, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* Consumer of w4a16_gemm_residual_stats: the norm's scaling and the QKV GEMM (silu_mul == 0)
+ * or the gate|up GEMM with SiLU * up (silu_mul == 1) in one decode kernel.  s [M, K] and
+ * ssq [M, K / 16] are the producer's s_out and ssq_out (K its N); per row, rstd =
+ * 1 / sqrt(sum(ssq) / K + eps) with the K / 16 tile sums added in a fixed order (rsqrt in
+ * fp64, rounded once), then x_norm = bf16(float(bf16(s * rstd)) * float(norm_weight)) and
+ * y = x_norm @ W (or SiLU(g) * u of it).  x_norm (may be NULL) receives the normalized
+ * activations.  The sum of squares is added in another order than w4a16_add_rmsnorm's, so
+ * x_norm can differ from it by one bf16 unit where s * rstd lies next to a rounding
+ * boundary.  0 <= M < 32, eps in [0, 1], every pointer 16-byte aligned; y overlaps none of
+ * the inputs; workspace as w4a16_gemm (w4a16_workspace_bytes(M, K, N, 128) suffices).
+ * Replaces post_attention_layernorm / input_layernorm followed by gate_up_proj / qkv_proj
+ * (qwen3.py:166-173 with layernorm.py:28-40). */
+int w4a16_gemm_rmsnorm_stats(const float* s, const float* ssq, const uint16_t* norm_weight, float eps,
+                             uint16_t* x_norm, const int32_t* packed, const int32_t* qzeros,
+                             const uint16_t* scales, uint16_t* y, int M, int K, int N, int group_size,
+                             int silu_mul, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Kernel family w4a16_gemm launches for (M, K, N): a w4a16_regime_id.
  * Replaces the dispatch rule of select_awq_cuda_split_k (awq_cuda.py:17-26) and
  * AWQLinearMethod.apply (awq.py:115-154) as the thing a caller can query. */
@@ -218,6 +252,14 @@ int w4a16_regime(int M, int K, int N);
 /* Number of K splits w4a16_gemm uses for (M, K, N) (1 = no cross-workgroup reduction).
  * Counterpart of select_awq_cuda_split_k (awq_cuda.py:17-26). */
 int w4a16_split_k(int M, int K, int N);
+
+/* The kernel configuration an entry point chooses for (M, K, N), written to out[5] as
+ * {regime, p0, p1, p2, split} in w4a16_gemm_config's terms.  entry: 0 = w4a16_gemm (and
+ * w4a16_gemm_residual, w4a16_gemm_residual_stats), 1 = w4a16_gemm_silu_mul, 2 and 3 =
+ * w4a16_gemm_rmsnorm_stats without and with silu_mul (M < 32), 4 = the decode kernel's own
+ * plan (M <= 64), which w4a16_gemm runs below M = 32.  No reference counterpart: an
+ * introspection hook for tuning and benchmarks. */
+int w4a16_plan(int M, int K, int N, int entry, int* out);
 
 /* w4a16_gemm with the kernel configuration forced instead of chosen: regime
  * W4A16_REGIME_DECODE (p0 = 16-column tiles per workgroup in {1,2,3,4,6} dividing N/16,

@@ -9,10 +9,14 @@ from ._lib import REGIME_DECODE, REGIME_NONE, REGIME_TILE, W4A16Error, W4A16Libr
 from .layers.quantization.awq import (
     AWQLinearMethod,
     AWQRuntimeConfig,
+    FUSED_NORM_MAX_M,
+    NormInput,
     add_rms_norm,
     awq_linear,
     awq_linear_residual,
+    awq_linear_residual_stats,
     awq_linear_rmsnorm,
+    awq_linear_rmsnorm_stats,
     awq_linear_silu_mul,
     awq_regime,
     dequantize_awq_gemm,
@@ -23,6 +27,8 @@ from .layers.quantization.awq import (
 __all__ = (
     "AWQLinearMethod",
     "AWQRuntimeConfig",
+    "FUSED_NORM_MAX_M",
+    "NormInput",
     "REGIME_DECODE",
     "REGIME_NONE",
     "REGIME_TILE",
@@ -31,7 +37,9 @@ __all__ = (
     "add_rms_norm",
     "awq_linear",
     "awq_linear_residual",
+    "awq_linear_residual_stats",
     "awq_linear_rmsnorm",
+    "awq_linear_rmsnorm_stats",
     "awq_linear_silu_mul",
     "awq_regime",
     "dequantize_awq_gemm",

@@ -38,6 +38,7 @@ _SIGNATURES = {
                                     _c_ptr]),
     "w4a16_regime": (_c_int, [_c_int, _c_int, _c_int]),
     "w4a16_split_k": (_c_int, [_c_int, _c_int, _c_int]),
+    "w4a16_plan": (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(ctypes.c_int)]),
     "w4a16_gemm_config": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
     "w4a16_workspace_bytes_config": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -55,8 +56,12 @@ _SIGNATURES = {
                                        _c_ptr, _c_int, _c_int, _c_ptr]),
     "w4a16_gemm_rmsnorm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                     _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+    "w4a16_gemm_residual_stats": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
+                                           _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+    "w4a16_gemm_rmsnorm_stats": (_c_int, [_c_ptr, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                          _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def _ptr(t: torch.Tensor | None):
@@ -118,6 +123,13 @@ class W4A16Library:
 
     def split_k(self, m: int, k: int, n: int) -> int:
         return int(self.dll.w4a16_split_k(m, k, n))
+
+    def plan(self, m: int, k: int, n: int, entry: int = 0) -> tuple[int, int, int, int, int]:
+        """(regime, p0, p1, p2, split) the entry point chooses (0 plain, 1 SiLU * up, 2 / 3
+        the fused-RMSNorm consumer without / with SiLU * up, 4 the decode kernel's own plan)."""
+        out = (ctypes.c_int * 5)()
+        self.check(self.dll.w4a16_plan(m, k, n, entry, out), "w4a16_plan")
+        return tuple(int(v) for v in out)
 
     # ---------------------------------------------------------- tensor methods
     def unpack_int4(self, packed: torch.Tensor) -> torch.Tensor:
@@ -256,6 +268,34 @@ class W4A16Library:
                                                    qzeros.data_ptr(), scales.data_ptr(), y.data_ptr(), m, k, n,
                                                    group_size, int(silu_mul), ws_ptr, ws_len, self._stream(x)),
                        "w4a16_gemm_rmsnorm")
+        return y
+
+    def gemm_residual_stats(self, x, packed, qzeros, scales, residual, s_out, residual_out, ssq_out, k: int, n: int,
+                            workspace: torch.Tensor | None, group_size: int = 128) -> None:
+        """Producer half of a fused RMSNorm: s_out = float(bf16(x @ W)) + float(residual),
+        residual_out = bf16(s_out), ssq_out = per-row sums of s_out^2 per 16-column tile."""
+        m = x.shape[0]
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(x.device):
+            self.check(self.dll.w4a16_gemm_residual_stats(x.data_ptr(), packed.data_ptr(), qzeros.data_ptr(),
+                                                          scales.data_ptr(), residual.data_ptr(), s_out.data_ptr(),
+                                                          residual_out.data_ptr(), ssq_out.data_ptr(), m, k, n,
+                                                          group_size, ws_ptr, ws_len, self._stream(x)),
+                       "w4a16_gemm_residual_stats")
+
+    def gemm_rmsnorm_stats(self, s, ssq, weight, eps: float, x_norm, packed, qzeros, scales, y, n: int,
+                           workspace: torch.Tensor | None, group_size: int = 128, silu_mul: bool = False):
+        """Consumer half: y = bf16(bf16(s * rstd) * weight) @ W (or SiLU(g) * u), rstd from ssq."""
+        m, k = s.shape
+        ws_ptr = workspace.data_ptr() if workspace is not None else None
+        ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        with torch.cuda.device(s.device):
+            self.check(self.dll.w4a16_gemm_rmsnorm_stats(s.data_ptr(), ssq.data_ptr(), weight.data_ptr(), float(eps),
+                                                         _ptr(x_norm), packed.data_ptr(), qzeros.data_ptr(),
+                                                         scales.data_ptr(), y.data_ptr(), m, k, n, group_size,
+                                                         int(silu_mul), ws_ptr, ws_len, self._stream(s)),
+                       "w4a16_gemm_rmsnorm_stats")
         return y
 
     def gemm_config(self, x, packed, qzeros, scales, y, k: int, n: int, regime: int, p0: int, p1: int,

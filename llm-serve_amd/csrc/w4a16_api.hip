@@ -45,6 +45,9 @@ bool overlap(const void* a, size_t na, const void* b, size_t nb) {
 }
 
 constexpr int kDecodeMaxM = 64;
+// The fused RMSNorm across two GEMMs (w4a16_gemm_residual_stats, w4a16_gemm_rmsnorm_stats)
+// runs in the decode kernel, below the tile regime.
+constexpr int kRowStatsMaxM = 32;
 // Both GEMM kernels address their inputs through buffer descriptors with 32-bit byte
 // offsets and use offsets >= 2^31 as "fetch nothing".
 constexpr size_t kMaxTensorBytes = size_t(1) << 31;
@@ -371,6 +374,29 @@ size_t partial_bytes(const GemmPlan& p, int M, int N) {
   return static_cast<size_t>(p.split) * (bm * ceil_div(M, bm)) * (bn * ceil_div(N, bn)) * sizeof(float);
 }
 
+// The consumer of the fused RMSNorm statistics (w4a16_gemm_rmsnorm_stats, M < 32) runs the
+// plain (or SiLU * up) decode plan with fp32 inputs: never staged, at most 8 waves, and a
+// ring that holds two 16-byte loads per activation fragment plus the norm weight's, so fewer
+// groups in flight or fewer tiles per wave; the LDS and staging checks may then split K
+// further.
+GemmPlan plan_norm_stats(int M, int K, int N, bool silu_mul) {
+  GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
+  if (p.regime != W4A16_REGIME_DECODE) return p;
+  const int G = K / w4a16::kGroup;
+  const int MB = (M + 15) / 16;
+  const int T = N / 16;
+  if (p.p1 > 8) p.p1 = 8;
+  while (p.p2 > 1 && !w4a16::decode_config_fits(MB, p.p0, p.p2, false, true)) p.p2 /= 2;
+  const int step = silu_mul ? 2 : 1;
+  while (p.p0 > step && (T % p.p0 != 0 || p.p0 == 5 || !w4a16::decode_config_fits(MB, p.p0, p.p2, false, true)))
+    p.p0 -= step;
+  while ((w4a16::decode_lds_bytes(M, K, p.p0, p.p1, p.p2, p.split, true) > w4a16::kDecodeMaxLds ||
+          !w4a16::decode_stage_fits(M, K, p.p0, p.p1, p.p2, p.split, true)) &&
+         p.split < G)
+    p.split = p.split * 2 > G ? G : p.split * 2;
+  return p;
+}
+
 size_t workspace_for(const GemmPlan& p, int M, int N) {
   if (p.regime == W4A16_REGIME_NONE || p.split <= 1) return 0;
   return kCounterBytes + partial_bytes(p, M, N);
@@ -423,7 +449,7 @@ int check_plan(const GemmPlan& p, int M, int K, int N, const void* workspace, si
 int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const int32_t* qzeros,
              const uint16_t* scales, uint16_t* y, int M, int K, int N, void* workspace, size_t workspace_bytes,
              hipStream_t stream, int up_tiles = 0, const uint16_t* res = nullptr,
-             const w4a16::DecodeNorm* norm = nullptr) {
+             const w4a16::DecodeNorm* norm = nullptr, const w4a16::DecodeRowStats* rs = nullptr) {
   if (p.regime == W4A16_REGIME_NONE) return ok();
   const int c = check_plan(p, M, K, N, workspace, workspace_bytes);
   if (c != W4A16_OK) return c;
@@ -434,7 +460,7 @@ int run_plan(const GemmPlan& p, const uint16_t* x, const int32_t* packed, const 
   const uint32_t* qz = reinterpret_cast<const uint32_t*>(qzeros);
   if (p.regime == W4A16_REGIME_DECODE)
     return check_launch(w4a16::launch_decode_cfg(x, pk, qz, scales, y, res, partials, counters, M, K, N, p.p0,
-                                                 p.p2, p.p1, p.split, up_tiles, norm, stream),
+                                                 p.p2, p.p1, p.split, up_tiles, norm, stream, rs),
                         "decode");
   // The tile kernel addresses the activations through a buffer descriptor (32-bit byte
   // offsets, >= 2^31 meaning "fetch nothing"): rows go in chunks of < 2 GiB of activations,
@@ -728,10 +754,19 @@ int w4a16_pack_int4(const int32_t* values, int32_t* packed, int rows, int cols, 
 
 size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
   if (M <= 0 || K <= 0 || N <= 0 || group_size != w4a16::kGroup || K % w4a16::kGroup || N % 64) return 0;
-  const size_t plain = workspace_for(plan(M, K, N), M, N);
-  if (N % 128) return plain;
-  const size_t fused = workspace_for(plan_silu_mul(M, K, N), M, N);
-  return fused > plain ? fused : plain;
+  // the largest of every entry point's plan at this shape: plain, SiLU * up and, below
+  // M = 32, the fused RMSNorm consumer's variants of both
+  size_t most = workspace_for(plan(M, K, N), M, N);
+  const auto take = [&](const GemmPlan& q) {
+    const size_t b = workspace_for(q, M, N);
+    most = b > most ? b : most;
+  };
+  if (N % 128 == 0) take(plan_silu_mul(M, K, N));
+  if (M < kRowStatsMaxM) {
+    take(plan_norm_stats(M, K, N, false));
+    if (N % 128 == 0) take(plan_norm_stats(M, K, N, true));
+  }
+  return most;
 }
 
 // The maximum runs the planner at every M <= M_max; a model asks for it once per layer with
@@ -772,6 +807,27 @@ int w4a16_split_k(int M, int K, int N) {
   return plan(M, K, N).split;
 }
 
+int w4a16_plan(int M, int K, int N, int entry, int* out) {
+  if (!out) return fail(W4A16_ERR_ARG, "null output pointer");
+  if (M <= 0 || K <= 0 || N <= 0 || K % w4a16::kGroup || N % 64)
+    return fail(W4A16_ERR_SHAPE, "no plan for M=%d K=%d N=%d", M, K, N);
+  if (entry < 0 || entry > 4) return fail(W4A16_ERR_ARG, "entry must be 0..4 (got %d)", entry);
+  if (entry == 4 && M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
+  if (entry & 1 && N % 128) return fail(W4A16_ERR_SHAPE, "the gate|up width N must be divisible by 128 (got %d)", N);
+  if ((entry == 2 || entry == 3) && M >= kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  const GemmPlan p = entry == 0   ? plan(M, K, N)
+                     : entry == 1 ? plan_silu_mul(M, K, N)
+                     : entry == 4 ? plan_decode(M, K, N)
+                                  : plan_norm_stats(M, K, N, entry == 3);
+  out[0] = p.regime;
+  out[1] = p.p0;
+  out[2] = p.p1;
+  out[3] = p.p2;
+  out[4] = p.split;
+  return ok();
+}
+
 int w4a16_gemm(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales, uint16_t* y,
                int M, int K, int N, int group_size, void* workspace, size_t workspace_bytes, void* stream) {
   const int v = validate_gemm(x, packed, qzeros, scales, y, M, K, N, group_size);
@@ -790,6 +846,61 @@ int w4a16_gemm_residual(const uint16_t* x, const int32_t* packed, const int32_t*
   if (!aligned(residual, 16)) return fail(W4A16_ERR_ALIGN, "residual must be 16-byte aligned");
   return run_plan(plan(M, K, N), x, packed, qzeros, scales, y, M, K, N, workspace, workspace_bytes,
                   static_cast<hipStream_t>(stream), 0, residual);
+}
+
+int w4a16_gemm_residual_stats(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                              const uint16_t* residual, float* s_out, uint16_t* residual_out, float* ssq_out, int M,
+                              int K, int N, int group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  const int v = validate_gemm(x, packed, qzeros, scales, residual_out, M, K, N, group_size);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  if (M >= kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  if (!residual || !s_out || !ssq_out) return fail(W4A16_ERR_ARG, "null residual, s_out or ssq_out pointer");
+  if (!aligned(residual, 16) || !aligned(s_out, 16) || !aligned(ssq_out, 16))
+    return fail(W4A16_ERR_ALIGN, "residual, s_out and ssq_out must be 16-byte aligned");
+  const size_t rb = static_cast<size_t>(M) * N * 2, sb = static_cast<size_t>(M) * N * 4;
+  const size_t qb = static_cast<size_t>(M) * (N / 16) * 4, xb = static_cast<size_t>(M) * K * 2;
+  if ((residual_out != residual && overlap(residual_out, rb, residual, rb)) || overlap(s_out, sb, residual, rb) ||
+      overlap(s_out, sb, residual_out, rb) || overlap(ssq_out, qb, s_out, sb) || overlap(ssq_out, qb, residual, rb) ||
+      overlap(ssq_out, qb, residual_out, rb) || overlap(s_out, sb, x, xb) || overlap(residual_out, rb, x, xb) ||
+      overlap(ssq_out, qb, x, xb))
+    return fail(W4A16_ERR_ARG, "s_out, residual_out and ssq_out must not overlap each other or the inputs "
+                               "(residual_out may be residual itself)");
+  const GemmPlan p = plan(M, K, N);  // the decode kernel below M = 32
+  const w4a16::DecodeRowStats rs{s_out, residual_out, ssq_out, nullptr, nullptr, nullptr, 0.f, nullptr};
+  return run_plan(p, x, packed, qzeros, scales, residual_out, M, K, N, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream), 0, residual, nullptr, &rs);
+}
+
+int w4a16_gemm_rmsnorm_stats(const float* s, const float* ssq, const uint16_t* norm_weight, float eps,
+                             uint16_t* x_norm, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,
+                             uint16_t* y, int M, int K, int N, int group_size, int silu_mul, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (silu_mul != 0 && silu_mul != 1) return fail(W4A16_ERR_ARG, "silu_mul must be 0 or 1 (got %d)", silu_mul);
+  // s is checked as the GEMM input (its alignment); its fp32 rows are 4 K bytes
+  const int v = validate_gemm(reinterpret_cast<const uint16_t*>(s), packed, qzeros, scales, y, M, K, N, group_size,
+                              silu_mul != 0);
+  if (v != W4A16_OK) return v;
+  if (M == 0) return ok();
+  if (M >= kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  if (static_cast<size_t>(M) * K * 4 >= kMaxTensorBytes)
+    return fail(W4A16_ERR_SHAPE, "fp32 activations of M=%d K=%d exceed 2 GiB", M, K);
+  if (!ssq || !norm_weight) return fail(W4A16_ERR_ARG, "null ssq or norm_weight pointer");
+  if (!aligned(ssq, 16) || !aligned(norm_weight, 16) || !aligned(x_norm, 16))
+    return fail(W4A16_ERR_ALIGN, "ssq, norm_weight and x_norm must be 16-byte aligned");
+  if (!(eps >= 0.0f) || eps > 1.0f) return fail(W4A16_ERR_ARG, "eps must be in [0, 1] (got %g)", eps);
+  const size_t yb = static_cast<size_t>(M) * (silu_mul ? N / 2 : N) * 2;
+  if (overlap(y, yb, s, static_cast<size_t>(M) * K * 4) || overlap(y, yb, ssq, static_cast<size_t>(M) * (K / 16) * 4) ||
+      overlap(y, yb, x_norm, static_cast<size_t>(M) * K * 2) || overlap(y, yb, norm_weight, static_cast<size_t>(K) * 2))
+    return fail(W4A16_ERR_ARG, "y must not overlap s, ssq, norm_weight or x_norm");
+  const GemmPlan p = plan_norm_stats(M, K, N, silu_mul != 0);
+  const int c = check_plan(p, M, K, N, workspace, workspace_bytes);
+  if (c != W4A16_OK) return c;
+  const w4a16::DecodeRowStats rs{nullptr, nullptr, nullptr, s, ssq, norm_weight, eps, x_norm};
+  return run_plan(p, reinterpret_cast<const uint16_t*>(s), packed, qzeros, scales, y, M, K, N, workspace,
+                  workspace_bytes, static_cast<hipStream_t>(stream), silu_mul ? N / 32 : 0, nullptr, nullptr, &rs);
 }
 
 int w4a16_gemm_silu_mul(const uint16_t* x, const int32_t* packed, const int32_t* qzeros, const uint16_t* scales,

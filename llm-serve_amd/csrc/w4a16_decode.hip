@@ -45,6 +45,7 @@ namespace w4a16 {
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 struct DecodeArgs {
+  DecodeRowStats rs;  // fused RMSNorm across two GEMMs (see DecodeRowStats), or all null
   const uint16_t* x;
   const uint32_t* packed;
   const uint32_t* qzeros;
@@ -134,10 +135,14 @@ __device__ __forceinline__ int decode_tile(int tb, int dt, int tt) {
 // Everything one wave loads from global memory for one 128-row group: one 16-byte weight
 // load per tile and, when the activations are not staged, the MB x 4 activation fragments.
 // Loaded DEPTH groups ahead of use; decoded only when consumed.
-template <int MB, int TN, bool XL>
+// NS: the activations arrive as the fp32 residual sum s of the producer's epilogue and are
+// normalized in registers (see DecodeRowStats): two 16-byte halves per fragment, plus the
+// norm weight's eight values of each step.
+template <int MB, int TN, bool XL, bool NS = false>
 struct DecodeStage {
   u32x4_t w[TN];
-  u32x4_t a[XL ? 1 : MB][4];
+  u32x4_t a[XL ? 1 : MB][NS ? 8 : 4];
+  u32x4_t nw[NS ? 4 : 1];
 };
 
 // Buffer descriptors of the four inputs.  Every global load of the decode kernel is an
@@ -147,10 +152,11 @@ struct DecodeStage {
 // are exact, so the DEPTH groups in flight really overlap.
 struct DecodeSources {
   __amdgpu_buffer_rsrc_t x, w, s, z;
+  __amdgpu_buffer_rsrc_t nw;  // NS: the norm weight (x is then the fp32 residual sum)
 };
 
-template <int MB, int TN, bool XL>
-__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, const DecodeSources& src,
+template <int MB, int TN, bool XL, bool NS = false>
+__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL, NS>& st, const DecodeSources& src,
                                                   const uint32_t (&x_row)[MB], int g, bool valid, int N, int tb,
                                                   int dt, int lane) {
   const int NT = N / kTileCols;
@@ -161,7 +167,21 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, c
     const uint32_t wo = (valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : 0u) | oob;
     st.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
   }
-  if constexpr (!XL) {
+  if constexpr (NS) {
+    // x_row holds fp32 offsets: row * 4K + 32 (lane / 16); a step is 32 values (128 bytes)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t xo = (x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 4u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        st.a[mb][2 * j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 128u * j, 0, 0);
+        st.a[mb][2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 128u * j + 16u, 0, 0);
+      }
+    }
+    const uint32_t wo = (valid ? (static_cast<uint32_t>(kGroup * g) + 8u * static_cast<uint32_t>(lane >> 4)) * 2u : 0u) | oob;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st.nw[j] = __builtin_amdgcn_raw_buffer_load_b128(src.nw, wo + 64u * j, 0, 0);
+  } else if constexpr (!XL) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const uint32_t xo = (x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 2u;
@@ -171,13 +191,29 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, c
   }
 }
 
+// NS: one activation fragment x_norm = bf16(bf16(s * rstd) * w) from its eight fp32 values
+// (two 16-byte halves) and the eight norm-weight values of its columns.
+__device__ __forceinline__ u32x4_t norm_fragment(u32x4_t lo, u32x4_t hi, float rstd, u32x4_t w) {
+  float sv[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    sv[q] = __uint_as_float(lo[q]);
+    sv[4 + q] = __uint_as_float(hi[q]);
+  }
+  const uint4 o = rms_scale_bf16x8(sv, rstd, make_uint4(w[0], w[1], w[2], w[3]));
+  return u32x4_t{o.x, o.y, o.z, o.w};
+}
+
 // Multiply-accumulate one group: the dequant operands (built from the staged scales and
 // zeros, or with PRE read prebuilt) and, with XL, the activation fragments come from the
 // wave's LDS slice `wl`; i is the group's item index within the wave.
-template <int MB, int TN, bool XL, bool PRE>
-__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL>& st,
+// NS: the fragments are normalized here with the lane's row scales `rstd`; the first column
+// block's workgroups (x_out != null) also store them, as the normalized activations.
+template <int MB, int TN, bool XL, bool PRE, bool NS = false>
+__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL, NS>& st,
                                                      const uint8_t* wl, const DecodeLds& lay, int i, int M,
-                                                     const NibbleConsts& nib, int lane) {
+                                                     const NibbleConsts& nib, int lane, const float (&rstd)[MB] = {},
+                                                     uint16_t* x_out = nullptr, int g = 0, int K = 0) {
   const int c = lane & 15;
   TileScale ts[TN];
   if constexpr (PRE) {
@@ -203,6 +239,23 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 #pragma unroll
     for (int js = 0; js < 4; ++js)
       a[0][js] = *reinterpret_cast<const u32x4_t*>(lx + ((((js << 2) | (lane >> 4)) ^ (r & 15)) << 4));
+  } else if constexpr (NS) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int js = 0; js < 4; ++js) a[mb][js] = norm_fragment(st.a[mb][2 * js], st.a[mb][2 * js + 1], rstd[mb], st.nw[js]);
+    if (x_out != nullptr) {  // wave-uniform
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int row = 16 * mb + (lane & 15);
+        if (row < M) {
+#pragma unroll
+          for (int js = 0; js < 4; ++js)
+            *reinterpret_cast<u32x4_t*>(x_out + static_cast<size_t>(row) * K + kGroup * g + 32 * js + 8 * (lane >> 4)) =
+                a[mb][js];
+        }
+      }
+    }
   } else {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -480,7 +533,7 @@ __device__ __forceinline__ void norm_rows(const NormRegs<NR>& nr, uint8_t* wl, c
   }
 }
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR, bool NS>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -488,12 +541,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             uint16_t* y, const uint16_t* res,
                                                             float* __restrict__ partials,
                                                             int* __restrict__ counters, int M, int K, int N,
-                                                            int split, int up_tiles, DecodeGeom geo, DecodeNorm nrm) {
+                                                            int split, int up_tiles, DecodeGeom geo, DecodeNorm nrm,
+                                                            DecodeRowStats rs) {
   constexpr bool NORM = NR > 0;
   static_assert(!NORM || (XL && MB == 1), "the norm prologue works on staged rows (M <= 4)");
+  static_assert(!NS || (!XL && !NORM), "normalized fp32 inputs are not staged");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
   __shared__ float norm_part[NORM ? WAVES : 1][4];
+  __shared__ float row_rstd[NS ? 16 * MB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   constexpr int W = WAVES;
@@ -511,15 +567,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const DecodeLds lay{0u, geo.z_off, geo.x_off, geo.c_off, geo.d_off, geo.wave_bytes, 0u, 0u, 0u};
 
   DecodeSources src;
-  src.x = make_buffer(x, geo.x_bytes);
+  src.x = NS ? make_buffer(rs.s_in, geo.x_bytes * 2u) : make_buffer(x, geo.x_bytes);
   src.w = make_buffer(packed, geo.w_bytes);
   src.s = make_buffer(scales, geo.s_bytes);
   src.z = make_buffer(qzeros, geo.z_bytes);
+  src.nw = make_buffer(NS ? rs.w : nullptr, NS ? static_cast<uint32_t>(K) * 2u : 0u);
   uint32_t x_row[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int row = 16 * mb + (lane & 15);
-    x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * 2u : kOutOfRange;
+    x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * (NS ? 4u : 2u) : kOutOfRange;
   }
 
   f32x4_t acc[MB][TN];
@@ -543,10 +600,37 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   // consumed.  The ring is filled first; then every load is issued whether or not its item
   // exists (out-of-range ones fetch nothing), so no branch encloses a load and the
   // scheduling barriers keep each item's loads together and in order.
-  DecodeStage<MB, TN, XL> ring[DEPTH];
+  DecodeStage<MB, TN, XL, NS> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d)
-    load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
+    load_decode_stage<MB, TN, XL, NS>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
+  // NS: each row's 1 / rms from the producer's per-tile sums of s^2 (K / 16 per row, summed in
+  // a fixed order: lane by lane in 4-value chunks, then across the wave), computed while the
+  // ring's first loads are in flight; wave w takes rows w, w + W, ...
+  float rstd[MB];
+  if constexpr (NS) {
+    const int tiles_k = K / kTileCols;
+    const __amdgpu_buffer_rsrc_t rq = make_buffer(rs.ssq_in, static_cast<uint32_t>(M) * tiles_k * 4u);
+    for (int r = wave; r < M; r += W) {
+      float t = 0.f;
+      for (int c0 = 4 * lane; c0 < tiles_k; c0 += 256) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(r * tiles_k + c0) * 4u, 0, 0);
+        t += (__uint_as_float(v[0]) + __uint_as_float(v[1])) + (__uint_as_float(v[2]) + __uint_as_float(v[3]));
+      }
+      t = wave_sum64(t);
+      if (lane == 0) row_rstd[r] = rsqrt_rn(t / static_cast<float>(K) + rs.eps);
+    }
+    // Only LDS needs ordering: the ring's loads stay in flight.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int row = 16 * mb + (lane & 15);
+      rstd[mb] = row_rstd[row < M ? row : M - 1];
+    }
+  }
+  uint16_t* x_out = NS && blockIdx.x == 0 ? rs.x_out : nullptr;  // the first column block stores x_norm
   // The staged operands go to LDS as soon as they arrive (the ring's loads stay in flight:
   // the compiler waits for each register load individually), then the norm prologue works
   // from its registers and writes the activation slice.
@@ -559,10 +643,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int i = base + d;
-      if (i < n_items) compute_decode_stage<MB, TN, XL, kPre>(acc, ring[d], wl, lay, i, M, nib, lane);
+      if (i < n_items)
+        compute_decode_stage<MB, TN, XL, kPre, NS>(acc, ring[d], wl, lay, i, M, nib, lane, rstd, x_out,
+                                                   g_begin + wave + i * W, K);
       const int in = i + DEPTH;
       __builtin_amdgcn_sched_barrier(0);
-      load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
+      load_decode_stage<MB, TN, XL, NS>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -633,7 +719,36 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   for (int p = 0; p < kPairs; ++p) {
     if (owner(p) != wave) continue;
     const int mb = p / TN, tt = p % TN;
-    if (!act) {
+    if (!act && rs.s_out != nullptr) {
+      // Producer of a fused RMSNorm: s = float(bf16(o)) + float(res) in fp32, the new
+      // residual bf16(s), and per row the sum of s^2 over this 16-column tile (the 16 lanes
+      // of each row quad hold its 16 columns; xor shuffles within them, in a fixed order).
+      const int n = 16 * (tb + tt) + c;
+      float ss[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * mb + 4 * (lane >> 4) + i;
+        ss[i] = 0.f;
+        if (row < M) {
+          const size_t idx = static_cast<size_t>(row) * N + n;
+          const float sv = bf16_bits_to_f32(f32_to_bf16_bits(out[p][i])) + bf16_bits_to_f32(res[idx]);
+          rs.s_out[idx] = sv;
+          rs.res_out[idx] = f32_to_bf16_bits(sv);
+          ss[i] = sv * sv;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 16);
+      if (c == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * mb + 4 * (lane >> 4) + i;
+          if (row < M) rs.ssq_out[static_cast<size_t>(row) * (N / kTileCols) + tb + tt] = ss[i];
+        }
+      }
+    } else if (!act) {
       const int n = 16 * (tb + tt) + c;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -666,17 +781,18 @@ bool decode_stages_x(int M, int K, int split) {
   return M <= 4 && n_gmax * M * 256 <= kDecodeMaxStagedX;
 }
 
-bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split) {
+bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split, bool ns) {
   const int G = K / kGroup;
   const int items = ((G + split - 1) / split + waves - 1) / waves;
   const bool sz = (tn == 1 && decode_prebuilt_scales(waves, depth))
                       ? items * 16 <= 64 * kStageE
                       : items * tn * 8 <= 64 * kStageS && items * tn * 2 <= 64 * kStageZ;
-  return sz && (!decode_stages_x(M, K, split) || items * M * 16 <= 64 * kStageX);
+  return sz && (ns || !decode_stages_x(M, K, split) || items * M * 16 <= 64 * kStageX);
 }
 
-size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split) {
-  return decode_lds_layout(M, K, tn, waves, split, decode_stages_x(M, K, split), decode_prebuilt_scales(waves, depth))
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split, bool ns) {
+  return decode_lds_layout(M, K, tn, waves, split, !ns && decode_stages_x(M, K, split),
+                           decode_prebuilt_scales(waves, depth))
       .total;
 }
 
@@ -689,16 +805,16 @@ size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int spl
 
 constexpr int kMaxDevices = 64;
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0, bool NS = false>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
-  if constexpr (!decode_config_fits(MB, TN, DEPTH, XL)) {
+  if constexpr (!decode_config_fits(MB, TN, DEPTH, XL, NS)) {
     return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
   const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
-  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split))
+  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split, NS))
     return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
@@ -708,22 +824,26 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     if (!raised[dev].load(std::memory_order_acquire)) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR>),
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NS>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                static_cast<int>(kDecodeMaxLds));
       if (e != hipSuccess) return e;
       raised[dev].store(true, std::memory_order_release);
     }
   }
-  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR><<<grid, 64 * WAVES, lds, stream>>>(
+  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NS><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles,
-      geo, a.norm);
+      geo, a.norm, a.rs);
   return hipGetLastError();
   }
 }
 
 template <int MB, int TN, int DEPTH, int WAVES>
 static hipError_t launch_decode_x(const DecodeArgs& a, bool norm, hipStream_t stream) {
+  if (a.rs.s_in != nullptr) {  // normalized fp32 inputs: M < 32, never staged, at most 8 waves
+    if constexpr (MB <= 2 && WAVES <= 8) return launch_decode_t<MB, TN, DEPTH, WAVES, false, 0, true>(a, stream);
+    return hipErrorInvalidValue;  // checked by the API
+  }
   if constexpr (MB == 1) {
     if (decode_stages_x(a.M, a.K, a.split)) {
       if (norm) {
@@ -772,9 +892,9 @@ static hipError_t launch_decode_m(const DecodeArgs& a, int tn, int depth, int wa
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
                              int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
-                             const DecodeNorm* norm, hipStream_t stream) {
-  const DecodeArgs a{x, packed, qzeros, scales, y, res, partials, counters, M, K, N, split, up_tiles,
-                     norm ? *norm : DecodeNorm{}};
+                             const DecodeNorm* norm, hipStream_t stream, const DecodeRowStats* rs) {
+  const DecodeArgs a{rs ? *rs : DecodeRowStats{}, x, packed, qzeros, scales, y, res, partials, counters, M, K, N,
+                     split, up_tiles, norm ? *norm : DecodeNorm{}};
   switch ((M + 15) / 16) {
     case 1: return launch_decode_m<1>(a, tn, depth, waves, norm != nullptr, stream);
     case 2: return launch_decode_m<2>(a, tn, depth, waves, norm != nullptr, stream);

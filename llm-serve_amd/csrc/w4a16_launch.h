@@ -44,22 +44,24 @@ constexpr int kStageS = 3;
 constexpr int kStageZ = 1;
 constexpr int kStageX = 4;
 constexpr int kStageE = 4;
-bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split);
+bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split, bool ns = false);
 // Whether a decode configuration builds its dequant operands once per wave in LDS
 // (8 waves and a ring at least two groups deep) instead of per tile and group.
 constexpr bool decode_prebuilt_scales(int waves, int depth) { return waves >= 8 && depth >= 2; }
 // LDS bytes of a decode workgroup: staged scales, zeros (and activations, and prebuilt
 // dequant operands), or the cross-wave reduction, whichever is larger.
-size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split);
+size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split, bool ns = false);
 
 // Register budget of a decode configuration (16-row activation blocks mb, tiles tn, ring
 // depth, activations staged or not): fp32 accumulators plus the ring of in-flight loads,
 // in 32-bit registers per lane, at most 176.  Configurations beyond it are not compiled.
-constexpr int decode_ring_regs(int mb, int tn, int depth, bool xl) {
-  return 4 * mb * tn + depth * 4 * (tn + (xl ? 0 : 4 * mb));
+// ns: the activations arrive as fp32 sums and are normalized in registers (two 16-byte loads
+// per fragment, plus four of the norm weight per group; see DecodeRowStats).
+constexpr int decode_ring_regs(int mb, int tn, int depth, bool xl, bool ns = false) {
+  return 4 * mb * tn + depth * 4 * (tn + (xl ? 0 : (ns ? 8 : 4) * mb) + (ns ? 4 : 0));
 }
-constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
-  return decode_ring_regs(mb, tn, depth, xl) <= 176;
+constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl, bool ns = false) {
+  return decode_ring_regs(mb, tn, depth, xl, ns) <= 176;
 }
 
 // RMSNorm(+residual) prologue of a decode GEMM whose activations are staged in LDS: the
@@ -75,6 +77,27 @@ struct DecodeNorm {
   float eps;
 };
 
+// An RMSNorm split across two decode GEMMs (M < 32), so that no separate norm launch sits
+// between them.  The producer -- the O or down projection, whose output h feeds the norm --
+// adds the residual in its epilogue as the reference's add_rms_forward does, s =
+// float(bf16(h)) + float(res) in fp32, and writes s (s_out, fp32 [M, N]), the new residual
+// bf16(s) (res_out, [M, N]; may be res itself) and, per row, the sum of s^2 over each
+// 16-column tile (ssq_out, [M, N / 16]).  The consumer -- the QKV or gate|up projection
+// behind the norm -- reads s (s_in, [M, K]) and the tile sums (ssq_in, [M, K / 16]), sums
+// each row's in a fixed order to rstd = 1 / sqrt(mean(s^2) + eps), and multiplies x_norm =
+// bf16(bf16(s * rstd) * w) (w: the norm weight, [K]); the workgroups of its first column
+// block also store x_norm (x_out, [M, K], may be null).
+struct DecodeRowStats {
+  float* s_out;
+  uint16_t* res_out;
+  float* ssq_out;
+  const float* s_in;
+  const float* ssq_in;
+  const uint16_t* w;
+  float eps;
+  uint16_t* x_out;
+};
+
 // LDS bytes of a decode workgroup that also runs the norm prologue (the same layout as
 // without it: the prologue works from registers and writes the activation slice), or 0 if
 // the configuration cannot run it (M > 2, activations not staged, a K split, or more than
@@ -85,10 +108,12 @@ size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int spl
 // gate|up weight (tn even, N % 128 == 0, y is [M, N / 2]).  res: null, or a bf16 [M, N]
 // residual added in the epilogue (plain GEMM only; may be y itself).  norm: null, or the
 // prologue above (requires decode_norm_lds_bytes(...) in (0, kDecodeMaxLds]).
+// rs: null, or the producer half (s_out set: plain GEMM with res) or the consumer half (s_in
+// set: x is then unused, M < 32) of a fused RMSNorm.
 hipError_t launch_decode_cfg(const uint16_t* x, const uint32_t* packed, const uint32_t* qzeros,
                              const uint16_t* scales, uint16_t* y, const uint16_t* res, float* partials,
                              int* counters, int M, int K, int N, int tn, int depth, int waves, int split, int up_tiles,
-                             const DecodeNorm* norm, hipStream_t stream);
+                             const DecodeNorm* norm, hipStream_t stream, const DecodeRowStats* rs = nullptr);
 
 // LDS-tiled MFMA GEMM.  A tile shape code selects the wave grid: wk K slices of nwm waves
 // along M x nwn along N, each wave owning tw 16-column layout tiles and 16 wm rows, so the

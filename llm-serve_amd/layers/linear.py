@@ -118,6 +118,18 @@ class ColumnParallelLinear(LinearBase):
         layer) the new residual is ``x`` itself, as qwen3.py:166-167 sets it."""
         return self._rmsnorm_apply(norm, x, residual, silu_mul=False)
 
+    def forward_rmsnorm_stats(self, norm: nn.Module, inp) -> torch.Tensor:
+        """``self(norm(h, residual))`` where the producer before the norm already added the
+        residual and left its row statistics (``NormInput`` of
+        RowParallelLinear.forward_residual_stats): the norm's scaling and this projection in
+        one decode kernel; the new residual came from the producer."""
+        return self._rmsnorm_stats_apply(norm, inp, silu_mul=False)
+
+    def _rmsnorm_stats_apply(self, norm: nn.Module, inp, silu_mul: bool):
+        if self.quant_method is None or not hasattr(self.quant_method, "apply_rmsnorm_stats"):
+            raise ValueError("the fused RMSNorm statistics are implemented for the AWQ HIP backend only")
+        return self.quant_method.apply_rmsnorm_stats(self, inp, norm.weight, norm.eps, silu_mul=silu_mul)
+
     def _rmsnorm_apply(self, norm: nn.Module, x: torch.Tensor, residual: torch.Tensor | None, silu_mul: bool):
         if self.quant_method is None or not hasattr(self.quant_method, "apply_rmsnorm"):
             raise ValueError("the fused RMSNorm prologue is implemented for the AWQ HIP backend only")
@@ -160,6 +172,13 @@ class MergedColumnParallelLinear(ColumnParallelLinear):
         if len(self.output_sizes) != 2 or self.output_sizes[0] != self.output_sizes[1]:
             raise ValueError("fused SiLU * up needs exactly two equal output shards (gate, up)")
         return self._rmsnorm_apply(norm, x, residual, silu_mul=True)
+
+    def forward_rmsnorm_stats_silu_and_mul(self, norm: nn.Module, inp) -> torch.Tensor:
+        """``SiluAndMul()(self(norm(h, residual)))`` from a producer's ``NormInput`` (see
+        ColumnParallelLinear.forward_rmsnorm_stats)."""
+        if len(self.output_sizes) != 2 or self.output_sizes[0] != self.output_sizes[1]:
+            raise ValueError("fused SiLU * up needs exactly two equal output shards (gate, up)")
+        return self._rmsnorm_stats_apply(norm, inp, silu_mul=True)
 
 
 class QKVParallelLinear(ColumnParallelLinear):
@@ -234,3 +253,15 @@ class RowParallelLinear(LinearBase):
         if self.tp_size > 1:
             raise ValueError("the fused residual add needs a tensor-parallel world size of 1")
         return self.quant_method.apply_residual(self, x, residual, out=out)
+
+    def forward_residual_stats(self, x: torch.Tensor, residual: torch.Tensor,
+                               residual_out: torch.Tensor | None = None):
+        """At decode sizes (packed M <= 31): this projection, the residual add of the next
+        add_rms_forward and that norm's row statistics in the GEMM epilogue, so that the norm
+        needs no launch of its own; returns ``(NormInput, new residual)`` for the next
+        layer's forward_rmsnorm_stats.  ``residual_out`` may be ``residual`` (in place)."""
+        if self.quant_method is None or not hasattr(self.quant_method, "apply_residual_stats"):
+            raise ValueError("the fused RMSNorm statistics are implemented for the AWQ HIP backend only")
+        if self.tp_size > 1:
+            raise ValueError("the fused residual add needs a tensor-parallel world size of 1")
+        return self.quant_method.apply_residual_stats(self, x, residual, residual_out=residual_out)

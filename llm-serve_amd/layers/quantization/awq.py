@@ -19,6 +19,9 @@ Same names, argument meaning and error behaviour as the reference:
 * ``add_rms_norm``: the reference's ``RMSNorm`` forward (layernorm.py:16-50) on the HIP
   kernel; ``awq_linear_rmsnorm`` / ``AWQLinearMethod.apply_rmsnorm``: that norm in front of
   the QKV or gate_up GEMM in one library call (qwen3.py:166-173)
+* ``awq_linear_residual_stats`` / ``awq_linear_rmsnorm_stats`` (``NormInput``): at decode
+  sizes the same norm split between the O / down GEMM before it (residual add and row
+  statistics in its epilogue) and the QKV / gate_up GEMM after it, with no launch between
 
 There is one execution backend, the HIP library (libw4a16.so): every tensor operation
 runs there and raises when the library or a GPU is missing -- nothing falls back to a CPU
@@ -223,6 +226,23 @@ class AWQLinearMethod:
             raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
         return awq_linear_rmsnorm(inputs, residual, norm_weight, eps, layer.awq_qweight, layer.awq_qzeros,
                                   layer.scales, group_size=self.config.group_size, silu_mul=silu_mul)
+
+    def apply_residual_stats(self, layer: nn.Module, inputs: torch.Tensor, residual: torch.Tensor,
+                             residual_out: torch.Tensor | None = None):
+        """The O / down projection with the residual add and the next RMSNorm's row
+        statistics in its epilogue: ``(NormInput, new residual)``."""
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear_residual_stats(inputs, layer.awq_qweight, layer.awq_qzeros, layer.scales, residual,
+                                         group_size=self.config.group_size, residual_out=residual_out)
+
+    def apply_rmsnorm_stats(self, layer: nn.Module, inp: NormInput, norm_weight: torch.Tensor, eps: float,
+                            silu_mul: bool = False) -> torch.Tensor:
+        """``self.apply(layer, RMSNorm(...))`` (or its SiLU(g) * u) from a producer's NormInput."""
+        if not hasattr(layer, "awq_qweight"):
+            raise RuntimeError("AWQ HIP weights must be processed after checkpoint loading")
+        return awq_linear_rmsnorm_stats(inp, norm_weight, eps, layer.awq_qweight, layer.awq_qzeros, layer.scales,
+                                        group_size=self.config.group_size, silu_mul=silu_mul)
 
     def apply(self, layer: nn.Module, inputs: torch.Tensor) -> torch.Tensor:
         if not hasattr(layer, "awq_qweight"):
@@ -532,6 +552,97 @@ def awq_linear_rmsnorm(inputs: torch.Tensor, residual: torch.Tensor | None, norm
                              residual_out.view(m, k) if residual_out is not None else None, packed_qweight,
                              qzeros, scales.contiguous(), y, n, workspace, group_size, silu_mul)
     return y.reshape(*lead, n_out), (residual_out if residual is not None else inputs)
+
+
+# The RMSNorm split across two GEMMs runs in the decode kernel: packed M below this.
+FUSED_NORM_MAX_M = 31
+
+
+@dataclass(frozen=True)
+class NormInput:
+    """The input of an RMSNorm with its residual add done, as the O or down projection's
+    epilogue leaves it (``awq_linear_residual_stats``): ``s`` = float(h) + float(residual) in
+    fp32 [M, K], and ``ssq`` [M, K / 16] the per-row sums of s^2 over each 16-column tile."""
+    s: torch.Tensor
+    ssq: torch.Tensor
+
+
+def awq_linear_residual_stats(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch.Tensor,
+                              scales: torch.Tensor, residual: torch.Tensor, *, group_size: int,
+                              residual_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
+    """The O / down projection followed by the residual add and the row statistics of the
+    next RMSNorm (qwen3.py:170-174, layernorm.py:35-38), so that the norm needs no launch of
+    its own: returns ``(NormInput, residual_out)`` with residual_out = bf16(h + residual)
+    (``residual_out`` may be ``residual`` itself).  The projection's output h is not stored:
+    the next norm reads ``NormInput.s``.  Packed M <= FUSED_NORM_MAX_M (decode sizes)."""
+    x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
+    m = x.shape[0]
+    if m > FUSED_NORM_MAX_M:
+        raise ValueError(f"the fused RMSNorm statistics take M <= {FUSED_NORM_MAX_M} (got {m}): use "
+                         f"awq_linear_residual / awq_linear and add_rms_norm there")
+    if residual.dtype != torch.bfloat16 or residual.device != inputs.device or residual.shape != (*lead, n):
+        raise ValueError("AWQ residual must be a bfloat16 tensor of the layer output shape on the activations' GPU")
+    res = residual.reshape(m, n)
+    if not res.is_contiguous() or not _aligned16(res):
+        raise ValueError("AWQ residual must be contiguous and 16-byte aligned")
+    if residual_out is None:
+        residual_out = torch.empty_like(residual)
+    if (residual_out.shape != residual.shape or residual_out.dtype != torch.bfloat16 or not residual_out.is_contiguous()
+            or not _aligned16(residual_out)):
+        raise ValueError("AWQ residual output must be a contiguous, 16-byte aligned bf16 tensor of the output shape")
+    s_out = torch.empty((m, n), dtype=torch.float32, device=inputs.device)
+    ssq = torch.empty((m, n // 16), dtype=torch.float32, device=inputs.device)
+    if m > 0:
+        library = lib()
+        if workspace is None:
+            workspace = WORKSPACE.get(inputs.device, library.workspace_bytes(m, k, n, group_size))
+        library.gemm_residual_stats(x, packed_qweight, qzeros, scales.contiguous(), res, s_out,
+                                    residual_out.reshape(m, n), ssq, k, n, workspace, group_size)
+    return NormInput(s_out, ssq), residual_out
+
+
+def awq_linear_rmsnorm_stats(inp: NormInput, norm_weight: torch.Tensor, eps: float, packed_qweight: torch.Tensor,
+                             qzeros: torch.Tensor, scales: torch.Tensor, *, group_size: int, silu_mul: bool = False,
+                             x_norm: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The RMSNorm of a ``NormInput`` (the reference's rms scaling of add_rms_forward,
+    layernorm.py:37-40, from the producer's sum s and row statistics) and the QKV GEMM --
+    or, with ``silu_mul``, the gate|up GEMM with SiLU * up -- in one decode kernel:
+    y = x_norm @ W with x_norm = bf16(float(bf16(s * rstd)) * float(norm_weight)).  The new
+    residual came from the producer.  ``x_norm`` (optional, bf16 [M, K]) receives the
+    normalized activations.  Packed M <= FUSED_NORM_MAX_M."""
+    s, ssq = inp.s, inp.ssq
+    if s.dtype != torch.float32 or s.ndim != 2 or ssq.dtype != torch.float32:
+        raise ValueError("NormInput must hold fp32 s [M, K] and ssq [M, K / 16]")
+    m, k = s.shape
+    if ssq.shape != (m, k // 16):
+        raise ValueError("NormInput ssq must be [M, K / 16]")
+    if m > FUSED_NORM_MAX_M:
+        raise ValueError(f"the fused RMSNorm statistics take M <= {FUSED_NORM_MAX_M} (got {m})")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.shape != (k,):
+        raise ValueError(f"RMSNorm weight must be a bfloat16 tensor of shape ({k},)")
+    if len({s.device, ssq.device, norm_weight.device, packed_qweight.device}) != 1 or s.device.type != "cuda":
+        raise ValueError("NormInput, the norm weight and the layer weights must share one GPU")
+    if group_size != 128:
+        raise ValueError("AWQ HIP kernels require group_size=128")
+    n = scales.shape[1]
+    if scales.shape[0] * group_size != k:
+        raise ValueError("RMSNorm width and the layer's input size differ")
+    if silu_mul and n % 128:
+        raise ValueError("AWQ fused SiLU * up requires the gate|up output size to be divisible by 128")
+    for t in (s, ssq, norm_weight):
+        if not t.is_contiguous() or not _aligned16(t):
+            raise ValueError("NormInput tensors and the norm weight must be contiguous and 16-byte aligned")
+    if x_norm is not None and (x_norm.shape != (m, k) or x_norm.dtype != torch.bfloat16 or not x_norm.is_contiguous()
+                               or not _aligned16(x_norm)):
+        raise ValueError("x_norm must be a contiguous, 16-byte aligned bf16 [M, K] tensor")
+    y = torch.empty((m, n // 2 if silu_mul else n), dtype=torch.bfloat16, device=s.device)
+    if m > 0:
+        library = lib()
+        if workspace is None:
+            workspace = WORKSPACE.get(s.device, library.workspace_bytes(m, k, n, group_size))
+        library.gemm_rmsnorm_stats(s, ssq, norm_weight, eps, x_norm, packed_qweight, qzeros, scales.contiguous(), y, n,
+                                   workspace, group_size, silu_mul)
+    return y
 
 
 def awq_regime(m: int, k: int, n: int) -> str:

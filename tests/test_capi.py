@@ -38,7 +38,7 @@ def test_binding_signatures_cover_the_header(pkg):
 
 def test_abi_version_and_empty_error(pkg):
     L = pkg.lib()
-    assert L.dll.w4a16_abi_version() == 4
+    assert L.dll.w4a16_abi_version() == 5
     assert isinstance(L.last_error(), str)
 
 
@@ -239,6 +239,57 @@ def test_rmsnorm_entry_points_validate_without_launching(pkg):
     m, k, n = 32, 4096, 4096
     assert L.split_k(m, k, n) > 1
     assert fused(p, None, p, 1e-6, p, None, p, p, p, y, m, k, n, 128, 0, None, 0, None) == 4
+
+
+def test_norm_stats_entry_points_validate_without_launching(pkg):
+    """The RMSNorm split across two decode GEMMs: every case below fails validation (or is
+    M = 0) before anything is enqueued."""
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (16 - ctypes.addressof(buf) % 16) % 16
+    far = p + (1 << 30)
+    prod = L.dll.w4a16_gemm_residual_stats
+    # (x, packed, qzeros, scales, residual, s_out, residual_out, ssq_out, M, K, N, group, ws, ws_bytes, stream)
+    assert prod(p, p, p, p, p, far, p, far + (1 << 28), 0, 4096, 4096, 128, None, 0, None) == 0
+    assert prod(p, p, p, p, p, far, p, far + (1 << 28), 32, 4096, 4096, 128, None, 0, None) == 2
+    assert "M < 32" in L.last_error()
+    assert prod(p, p, p, p, None, far, p, far + (1 << 28), 8, 4096, 4096, 128, None, 0, None) == 1
+    assert prod(p, p, p, p, p, far, p, far + (1 << 28) + 4, 8, 4096, 4096, 128, None, 0, None) == 3
+    # s_out over the residual, ssq_out inside s_out: rejected
+    assert prod(p, p, p, p, p, p, far, far + (1 << 28), 8, 4096, 4096, 128, None, 0, None) == 1
+    assert "overlap" in L.last_error()
+    assert prod(p, p, p, p, p, far, p, far + 64, 8, 4096, 4096, 128, None, 0, None) == 1
+    cons = L.dll.w4a16_gemm_rmsnorm_stats
+    # (s, ssq, weight, eps, x_norm, packed, qzeros, scales, y, M, K, N, group, silu_mul, ws, ws_bytes, stream)
+    assert cons(p, p, p, 1e-6, None, p, p, p, far, 0, 4096, 4096, 128, 0, None, 0, None) == 0
+    assert cons(p, p, p, 1e-6, None, p, p, p, far, 8, 4096, 4096, 128, 2, None, 0, None) == 1
+    assert cons(p, p, p, 1e-6, None, p, p, p, far, 32, 4096, 4096, 128, 0, None, 0, None) == 2
+    assert cons(p, p, p, 1e-6, None, p, p, p, far, 31, 17318528, 64, 128, 0, None, 0, None) == 2
+    assert "fp32 activations" in L.last_error()
+    assert cons(p, None, p, 1e-6, None, p, p, p, far, 8, 4096, 4096, 128, 0, None, 0, None) == 1
+    assert cons(p, p, p, -1.0, None, p, p, p, far, 8, 4096, 4096, 128, 0, None, 0, None) == 1
+    assert cons(p, p + 4, p, 1e-6, None, p, p, p, far, 8, 4096, 4096, 128, 0, None, 0, None) == 3
+    assert cons(p, p, p, 1e-6, None, p, p, p, p + 4096, 8, 4096, 4096, 128, 0, None, 0, None) == 1
+    assert "overlap" in L.last_error()
+
+
+def test_plan_introspection(pkg):
+    """w4a16_plan reports what the entry points run: the planner's regime and split, the
+    decode kernel's own plan where the tile kernel is chosen, and refuses what no entry does."""
+    L = pkg.lib()
+    for m, k, n in ((1, 4096, 6144), (16, 12288, 4096), (48, 4096, 4096), (2048, 4096, 24576)):
+        r = L.plan(m, k, n)
+        assert r[0] == L.regime(m, k, n) and r[4] == L.split_k(m, k, n)
+    assert L.plan(48, 4096, 4096, 4)[0] == pkg.REGIME_DECODE
+    for m in (1, 8, 31):
+        for entry in (2, 3):
+            assert L.plan(m, 4096, 24576, entry)[0] == pkg.REGIME_DECODE
+    out = (ctypes.c_int * 5)()
+    assert L.dll.w4a16_plan(32, 4096, 4096, 2, out) == 2
+    assert L.dll.w4a16_plan(65, 4096, 4096, 4, out) == 2
+    assert L.dll.w4a16_plan(8, 4096, 4096, 5, out) == 1
+    assert L.dll.w4a16_plan(8, 4096, 4160, 1, out) == 2
+    assert L.dll.w4a16_plan(8, 4096, 4096, 0, None) == 1
 
 
 def test_workspace_bytes_max_covers_every_m(pkg):
