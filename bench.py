@@ -64,7 +64,7 @@ Also reported (not part of `value`):
     input_layernorm + QKV and post_attention_layernorm + gate|up + SiLU * up (the residual
     alternating between two buffers), plain O and down -- 144 GEMM launches per step, plus 72
     norm launches where M > 2 (at M <= 2 the norm runs inside the decode kernel), one graph;
-    `norm_stats` (M < 32): the same step with each norm split across the GEMMs around it
+    `norm_stats` (M <= 8): the same step with each norm split across the GEMMs around it
     (O and down through w4a16_gemm_residual_stats, gate|up and QKV through
     w4a16_gemm_rmsnorm_stats) -- 144 GEMM launches and no norm launch after layer 0's;
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
@@ -432,7 +432,7 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
 
         ms = time_graph(step, stream, reps)
         out[f"M={m}"] = {"step_us": round(ms * 1e3, 1), "us_per_token": round(ms * 1e3 / m, 2)}
-        if m >= 32:
+        if m > 8:
             continue
         # Decode sizes: the norms split across the GEMMs around them.  O and down add the
         # residual in place and leave the fp32 sum s and its tile sums of squares; gate|up and

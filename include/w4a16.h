@@ -211,7 +211,7 @@ int w4a16_gemm_rmsnorm(const uint16_t* x, const uint16_t* residual, const uint16
                        void* stream);
 
 /* The RMSNorm that follows the O or down projection, split across that GEMM and the next
- * one so that no norm launch sits between them (decode sizes, 0 <= M < 32; M >= 32 is
+ * one so that no norm launch sits between them (decode sizes, 0 <= M <= 8; M > 8 is
  * W4A16_ERR_SHAPE: use w4a16_gemm_residual / w4a16_gemm and w4a16_gemm_rmsnorm there).
  * Producer: h = bf16(x[M, K] @ W) is added to residual [M, N] in fp32 in the epilogue, as
  * the reference's add_rms_forward does (layernorm.py:35-36): s_out[M, N] (fp32) =
@@ -228,14 +228,15 @@ int w4a16_gemm_residual_stats(const uint16_t* x, const int32_t* packed, const in
                               void* stream);
 
 /* Consumer of w4a16_gemm_residual_stats: the norm's scaling and the QKV GEMM (silu_mul == 0)
- * or the gate|up GEMM with SiLU * up (silu_mul == 1) in one decode kernel.  s [M, K] and
+ * or the gate|up GEMM with SiLU * up (silu_mul == 1) in one decode kernel, whose workgroups
+ * normalize the M rows of their K range once into LDS.  s [M, K] and
  * ssq [M, K / 16] are the producer's s_out and ssq_out (K its N); per row, rstd =
  * 1 / sqrt(sum(ssq) / K + eps) with the K / 16 tile sums added in a fixed order (rsqrt in
  * fp64, rounded once), then x_norm = bf16(float(bf16(s * rstd)) * float(norm_weight)) and
  * y = x_norm @ W (or SiLU(g) * u of it).  x_norm (may be NULL) receives the normalized
  * activations.  The sum of squares is added in another order than w4a16_add_rmsnorm's, so
  * x_norm can differ from it by one bf16 unit where s * rstd lies next to a rounding
- * boundary.  0 <= M < 32, eps in [0, 1], every pointer 16-byte aligned; y overlaps none of
+ * boundary.  0 <= M <= 8, eps in [0, 1], every pointer 16-byte aligned; y overlaps none of
  * the inputs; workspace as w4a16_gemm (w4a16_workspace_bytes(M, K, N, 128) suffices).
  * Replaces post_attention_layernorm / input_layernorm followed by gate_up_proj / qkv_proj
  * (qwen3.py:166-173 with layernorm.py:28-40). */
@@ -256,7 +257,7 @@ int w4a16_split_k(int M, int K, int N);
 /* The kernel configuration an entry point chooses for (M, K, N), written to out[5] as
  * {regime, p0, p1, p2, split} in w4a16_gemm_config's terms.  entry: 0 = w4a16_gemm (and
  * w4a16_gemm_residual, w4a16_gemm_residual_stats), 1 = w4a16_gemm_silu_mul, 2 and 3 =
- * w4a16_gemm_rmsnorm_stats without and with silu_mul (M < 32), 4 = the decode kernel's own
+ * w4a16_gemm_rmsnorm_stats without and with silu_mul (M <= 8), 4 = the decode kernel's own
  * plan (M <= 64), which w4a16_gemm runs below M = 32.  No reference counterpart: an
  * introspection hook for tuning and benchmarks. */
 int w4a16_plan(int M, int K, int N, int entry, int* out);

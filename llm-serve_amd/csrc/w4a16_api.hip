@@ -46,8 +46,11 @@ bool overlap(const void* a, size_t na, const void* b, size_t nb) {
 
 constexpr int kDecodeMaxM = 64;
 // The fused RMSNorm across two GEMMs (w4a16_gemm_residual_stats, w4a16_gemm_rmsnorm_stats)
-// runs in the decode kernel, below the tile regime.
-constexpr int kRowStatsMaxM = 32;
+// runs in the decode kernel, whose consumer stages its normalized rows in LDS.  Measured on
+// MI355X at the Qwen3-8B shapes, the pair (producer + consumer) beats the residual GEMM
+// plus w4a16_gemm_rmsnorm by 0.3 - 3.4 us per norm for M = 2..8; at M = 16 the consumer's
+// fp32 row reads (every column block reads all of s) cost more than the norm launch saves.
+constexpr int kRowStatsMaxM = 8;
 // Both GEMM kernels address their inputs through buffer descriptors with 32-bit byte
 // offsets and use offsets >= 2^31 as "fetch nothing".
 constexpr size_t kMaxTensorBytes = size_t(1) << 31;
@@ -374,22 +377,16 @@ size_t partial_bytes(const GemmPlan& p, int M, int N) {
   return static_cast<size_t>(p.split) * (bm * ceil_div(M, bm)) * (bn * ceil_div(N, bn)) * sizeof(float);
 }
 
-// The consumer of the fused RMSNorm statistics (w4a16_gemm_rmsnorm_stats, M < 32) runs the
-// plain (or SiLU * up) decode plan with fp32 inputs: never staged, at most 8 waves, and a
-// ring that holds two 16-byte loads per activation fragment plus the norm weight's, so fewer
-// groups in flight or fewer tiles per wave; the LDS and staging checks may then split K
-// further.
+// The consumer of the fused RMSNorm statistics (w4a16_gemm_rmsnorm_stats, M <= 8) runs the
+// plain (or SiLU * up) decode plan with its normalized rows staged in LDS: at most 8 waves
+// and two groups in flight per wave (the compiled consumer kernels), and K split further
+// where the staged rows exceed LDS or a wave would hold more than four groups.
 GemmPlan plan_norm_stats(int M, int K, int N, bool silu_mul) {
   GemmPlan p = silu_mul ? plan_silu_mul(M, K, N) : plan(M, K, N);
   if (p.regime != W4A16_REGIME_DECODE) return p;
   const int G = K / w4a16::kGroup;
-  const int MB = (M + 15) / 16;
-  const int T = N / 16;
   if (p.p1 > 8) p.p1 = 8;
-  while (p.p2 > 1 && !w4a16::decode_config_fits(MB, p.p0, p.p2, false, true)) p.p2 /= 2;
-  const int step = silu_mul ? 2 : 1;
-  while (p.p0 > step && (T % p.p0 != 0 || p.p0 == 5 || !w4a16::decode_config_fits(MB, p.p0, p.p2, false, true)))
-    p.p0 -= step;
+  if (p.p2 > 2) p.p2 = 2;
   while ((w4a16::decode_lds_bytes(M, K, p.p0, p.p1, p.p2, p.split, true) > w4a16::kDecodeMaxLds ||
           !w4a16::decode_stage_fits(M, K, p.p0, p.p1, p.p2, p.split, true)) &&
          p.split < G)
@@ -762,7 +759,7 @@ size_t w4a16_workspace_bytes(int M, int K, int N, int group_size) {
     most = b > most ? b : most;
   };
   if (N % 128 == 0) take(plan_silu_mul(M, K, N));
-  if (M < kRowStatsMaxM) {
+  if (M <= kRowStatsMaxM) {
     take(plan_norm_stats(M, K, N, false));
     if (N % 128 == 0) take(plan_norm_stats(M, K, N, true));
   }
@@ -814,8 +811,8 @@ int w4a16_plan(int M, int K, int N, int entry, int* out) {
   if (entry < 0 || entry > 4) return fail(W4A16_ERR_ARG, "entry must be 0..4 (got %d)", entry);
   if (entry == 4 && M > kDecodeMaxM) return fail(W4A16_ERR_SHAPE, "decode kernel needs M <= 64 (got %d)", M);
   if (entry & 1 && N % 128) return fail(W4A16_ERR_SHAPE, "the gate|up width N must be divisible by 128 (got %d)", N);
-  if ((entry == 2 || entry == 3) && M >= kRowStatsMaxM)
-    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  if ((entry == 2 || entry == 3) && M > kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M <= %d (got %d)", kRowStatsMaxM, M);
   const GemmPlan p = entry == 0   ? plan(M, K, N)
                      : entry == 1 ? plan_silu_mul(M, K, N)
                      : entry == 4 ? plan_decode(M, K, N)
@@ -854,8 +851,8 @@ int w4a16_gemm_residual_stats(const uint16_t* x, const int32_t* packed, const in
   const int v = validate_gemm(x, packed, qzeros, scales, residual_out, M, K, N, group_size);
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
-  if (M >= kRowStatsMaxM)
-    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  if (M > kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M <= %d (got %d)", kRowStatsMaxM, M);
   if (!residual || !s_out || !ssq_out) return fail(W4A16_ERR_ARG, "null residual, s_out or ssq_out pointer");
   if (!aligned(residual, 16) || !aligned(s_out, 16) || !aligned(ssq_out, 16))
     return fail(W4A16_ERR_ALIGN, "residual, s_out and ssq_out must be 16-byte aligned");
@@ -867,7 +864,7 @@ int w4a16_gemm_residual_stats(const uint16_t* x, const int32_t* packed, const in
       overlap(ssq_out, qb, x, xb))
     return fail(W4A16_ERR_ARG, "s_out, residual_out and ssq_out must not overlap each other or the inputs "
                                "(residual_out may be residual itself)");
-  const GemmPlan p = plan(M, K, N);  // the decode kernel below M = 32
+  const GemmPlan p = plan(M, K, N);  // the decode kernel (M <= 8)
   const w4a16::DecodeRowStats rs{s_out, residual_out, ssq_out, nullptr, nullptr, nullptr, 0.f, nullptr};
   return run_plan(p, x, packed, qzeros, scales, residual_out, M, K, N, workspace, workspace_bytes,
                   static_cast<hipStream_t>(stream), 0, residual, nullptr, &rs);
@@ -883,8 +880,8 @@ int w4a16_gemm_rmsnorm_stats(const float* s, const float* ssq, const uint16_t* n
                               silu_mul != 0);
   if (v != W4A16_OK) return v;
   if (M == 0) return ok();
-  if (M >= kRowStatsMaxM)
-    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M < %d (got %d)", kRowStatsMaxM, M);
+  if (M > kRowStatsMaxM)
+    return fail(W4A16_ERR_SHAPE, "the fused RMSNorm statistics take M <= %d (got %d)", kRowStatsMaxM, M);
   if (static_cast<size_t>(M) * K * 4 >= kMaxTensorBytes)
     return fail(W4A16_ERR_SHAPE, "fp32 activations of M=%d K=%d exceed 2 GiB", M, K);
   if (!ssq || !norm_weight) return fail(W4A16_ERR_ARG, "null ssq or norm_weight pointer");

@@ -79,11 +79,35 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float (&f)[8]) {
                     pack_bf16x2(f[6], f[7]));
 }
 
-// Sum over the 64 lanes of a wave (every lane gets the same total).
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// One DPP move of v between the lanes of each row of 16 (every source lane active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each row of 16 lanes, every lane of the row getting the total, by DPP moves in
+// registers (a shuffle through the LDS crossbar costs a round trip per step): neighbours
+// (quad_perm 1,0,3,2), pairs of them (quad_perm 2,3,0,1), quads (mirror within 8 lanes),
+// halves (mirror within 16).  Each step adds the same two partial sums on both lanes, in
+// either order, which fp32 addition ignores, so every lane holds the same bits:
+// (((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7))) + (...).  All 64 lanes must be active.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
   return v;
+}
+
+// Sum over the 64 lanes of a wave, every lane getting the same total: the four row sums,
+// then (row 0 + row 2) + (row 1 + row 3).  All 64 lanes must be active.
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = row_sum16(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r2) + (r1 + r3);
 }
 
 // 1 / sqrt(v) for the RMSNorm row scale, evaluated in fp64 and rounded once to fp32 (within
@@ -95,15 +119,20 @@ __device__ __forceinline__ float rsqrt_rn(float v) {
 // RMSNorm scaling of one chunk of s (fp32, the residual sum): bf16(float(bf16(s * rstd)) *
 // weight), the reference's x.to(orig_dtype).mul_(self.weight); the weight product is exact
 // in fp32 (two 8-bit significands) and rounded once.
-__device__ __forceinline__ uint4 rms_scale_bf16x8(const float (&s)[8], float rstd, uint4 weight) {
-  float t[8], w[8];
+__device__ __forceinline__ uint4 rms_scale_bf16x8(const float (&s)[8], float rstd, const float (&w)[8]) {
+  float t[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) t[i] = s[i] * rstd;
   unpack_bf16x8(pack_bf16x8(t), t);
-  unpack_bf16x8(weight, w);
 #pragma unroll
   for (int i = 0; i < 8; ++i) t[i] *= w[i];
   return pack_bf16x8(t);
+}
+
+__device__ __forceinline__ uint4 rms_scale_bf16x8(const float (&s)[8], float rstd, uint4 weight) {
+  float w[8];
+  unpack_bf16x8(weight, w);
+  return rms_scale_bf16x8(s, rstd, w);
 }
 
 // Residual epilogue: eight bf16 GEMM outputs plus eight bf16 residuals, added in fp32 and

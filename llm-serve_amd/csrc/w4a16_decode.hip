@@ -135,14 +135,10 @@ __device__ __forceinline__ int decode_tile(int tb, int dt, int tt) {
 // Everything one wave loads from global memory for one 128-row group: one 16-byte weight
 // load per tile and, when the activations are not staged, the MB x 4 activation fragments.
 // Loaded DEPTH groups ahead of use; decoded only when consumed.
-// NS: the activations arrive as the fp32 residual sum s of the producer's epilogue and are
-// normalized in registers (see DecodeRowStats): two 16-byte halves per fragment, plus the
-// norm weight's eight values of each step.
-template <int MB, int TN, bool XL, bool NS = false>
+template <int MB, int TN, bool XL>
 struct DecodeStage {
   u32x4_t w[TN];
-  u32x4_t a[XL ? 1 : MB][NS ? 8 : 4];
-  u32x4_t nw[NS ? 4 : 1];
+  u32x4_t a[XL ? 1 : MB][4];
 };
 
 // Buffer descriptors of the four inputs.  Every global load of the decode kernel is an
@@ -152,11 +148,10 @@ struct DecodeStage {
 // are exact, so the DEPTH groups in flight really overlap.
 struct DecodeSources {
   __amdgpu_buffer_rsrc_t x, w, s, z;
-  __amdgpu_buffer_rsrc_t nw;  // NS: the norm weight (x is then the fp32 residual sum)
 };
 
-template <int MB, int TN, bool XL, bool NS = false>
-__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL, NS>& st, const DecodeSources& src,
+template <int MB, int TN, bool XL>
+__device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL>& st, const DecodeSources& src,
                                                   const uint32_t (&x_row)[MB], int g, bool valid, int N, int tb,
                                                   int dt, int lane) {
   const int NT = N / kTileCols;
@@ -167,21 +162,7 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL, NS>& s
     const uint32_t wo = (valid ? static_cast<uint32_t>(tile_word(g, t, NT, lane)) * 4u : 0u) | oob;
     st.w[tt] = __builtin_amdgcn_raw_buffer_load_b128(src.w, wo, 0, 0);
   }
-  if constexpr (NS) {
-    // x_row holds fp32 offsets: row * 4K + 32 (lane / 16); a step is 32 values (128 bytes)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const uint32_t xo = (x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 4u;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        st.a[mb][2 * j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 128u * j, 0, 0);
-        st.a[mb][2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(src.x, xo + 128u * j + 16u, 0, 0);
-      }
-    }
-    const uint32_t wo = (valid ? (static_cast<uint32_t>(kGroup * g) + 8u * static_cast<uint32_t>(lane >> 4)) * 2u : 0u) | oob;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st.nw[j] = __builtin_amdgcn_raw_buffer_load_b128(src.nw, wo + 64u * j, 0, 0);
-  } else if constexpr (!XL) {
+  if constexpr (!XL) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const uint32_t xo = (x_row[mb] | oob) + static_cast<uint32_t>(kGroup * g) * 2u;
@@ -191,29 +172,13 @@ __device__ __forceinline__ void load_decode_stage(DecodeStage<MB, TN, XL, NS>& s
   }
 }
 
-// NS: one activation fragment x_norm = bf16(bf16(s * rstd) * w) from its eight fp32 values
-// (two 16-byte halves) and the eight norm-weight values of its columns.
-__device__ __forceinline__ u32x4_t norm_fragment(u32x4_t lo, u32x4_t hi, float rstd, u32x4_t w) {
-  float sv[8];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    sv[q] = __uint_as_float(lo[q]);
-    sv[4 + q] = __uint_as_float(hi[q]);
-  }
-  const uint4 o = rms_scale_bf16x8(sv, rstd, make_uint4(w[0], w[1], w[2], w[3]));
-  return u32x4_t{o.x, o.y, o.z, o.w};
-}
-
 // Multiply-accumulate one group: the dequant operands (built from the staged scales and
 // zeros, or with PRE read prebuilt) and, with XL, the activation fragments come from the
 // wave's LDS slice `wl`; i is the group's item index within the wave.
-// NS: the fragments are normalized here with the lane's row scales `rstd`; the first column
-// block's workgroups (x_out != null) also store them, as the normalized activations.
-template <int MB, int TN, bool XL, bool PRE, bool NS = false>
-__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL, NS>& st,
+template <int MB, int TN, bool XL, bool PRE>
+__device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], const DecodeStage<MB, TN, XL>& st,
                                                      const uint8_t* wl, const DecodeLds& lay, int i, int M,
-                                                     const NibbleConsts& nib, int lane, const float (&rstd)[MB] = {},
-                                                     uint16_t* x_out = nullptr, int g = 0, int K = 0) {
+                                                     const NibbleConsts& nib, int lane) {
   const int c = lane & 15;
   TileScale ts[TN];
   if constexpr (PRE) {
@@ -239,23 +204,6 @@ __device__ __forceinline__ void compute_decode_stage(f32x4_t (&acc)[MB][TN], con
 #pragma unroll
     for (int js = 0; js < 4; ++js)
       a[0][js] = *reinterpret_cast<const u32x4_t*>(lx + ((((js << 2) | (lane >> 4)) ^ (r & 15)) << 4));
-  } else if constexpr (NS) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int js = 0; js < 4; ++js) a[mb][js] = norm_fragment(st.a[mb][2 * js], st.a[mb][2 * js + 1], rstd[mb], st.nw[js]);
-    if (x_out != nullptr) {  // wave-uniform
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int row = 16 * mb + (lane & 15);
-        if (row < M) {
-#pragma unroll
-          for (int js = 0; js < 4; ++js)
-            *reinterpret_cast<u32x4_t*>(x_out + static_cast<size_t>(row) * K + kGroup * g + 32 * js + 8 * (lane >> 4)) =
-                a[mb][js];
-        }
-      }
-    }
   } else {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -533,7 +481,119 @@ __device__ __forceinline__ void norm_rows(const NormRegs<NR>& nr, uint8_t* wl, c
   }
 }
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR, bool NS>
+// Consumer of the fused RMSNorm statistics (NSR > 0: room for NSR >= M rows, M <= 8, staged
+// activations): the producer GEMM left s = float(h) + float(residual) in fp32 and, per row, the
+// sums of s^2 over each 16-column tile (DecodeRowStats).  Lane l works on item i = l / 16 of
+// its wave and on the group's global chunk p = l % 16 (8 columns) of every row, so it loads the
+// norm weight's chunk once and two 16-byte fp32 halves per row; row r's chunk p goes to staged
+// position p ^ r, the layout the staged-activation loop reads.  Only the M real rows are
+// normalized, once per workgroup and group (the loop's 16-row fragments would redo it for
+// every padded row).
+template <int NSR>
+struct NsRegs {
+  u32x4_t s[NSR][2];
+  u32x4_t w;
+};
+
+template <int W, int NSR>
+__device__ __forceinline__ void load_ns_operands(NsRegs<NSR>& ns, __amdgpu_buffer_rsrc_t rsum,
+                                                 __amdgpu_buffer_rsrc_t rw, int M, int K, int g_first, int n_items,
+                                                 int lane) {
+  const int i = lane >> 4;
+  const bool live = i < n_items;
+  const uint32_t col = static_cast<uint32_t>(g_first + i * W) * kGroup + 8u * static_cast<uint32_t>(lane & 15);
+  ns.w = __builtin_amdgcn_raw_buffer_load_b128(rw, live ? col * 2u : kOutOfRange, 0, 0);
+  // Rows past M issue nothing (a uniform branch): an out-of-range load still occupies the
+  // CU's address unit, shared by all its waves.
+#pragma unroll
+  for (int r = 0; r < NSR; ++r) {
+    if (r < M) {
+      const uint32_t off = (static_cast<uint32_t>(r) * K + col) * 4u;
+      ns.s[r][0] = __builtin_amdgcn_raw_buffer_load_b128(rsum, live ? off : kOutOfRange, 0, 0);
+      ns.s[r][1] = __builtin_amdgcn_raw_buffer_load_b128(rsum, live ? off + 16u : kOutOfRange, 0, 0);
+    }
+  }
+}
+
+// The per-row tile sums of s^2 a wave reduces: rows wave + j W (j < kRows), at most two 16-byte
+// chunks of four tile sums per lane and row (K <= 8192; longer rows load the rest later).
+template <int W>
+struct NsStats {
+  static constexpr int kRows = (8 + W - 1) / W;
+  u32x4_t q[kRows][2];
+};
+
+template <int W>
+__device__ __forceinline__ void load_ns_stats(NsStats<W>& st, __amdgpu_buffer_rsrc_t rq, int M, int tiles_k, int wave,
+                                              int lane) {
+#pragma unroll
+  for (int j = 0; j < NsStats<W>::kRows; ++j) {
+    const int r = wave + j * W;
+    if (r < M) {  // wave-uniform
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c0 = 4 * lane + 256 * h;
+        st.q[j][h] = __builtin_amdgcn_raw_buffer_load_b128(
+            rq, c0 < tiles_k ? static_cast<uint32_t>(r * tiles_k + c0) * 4u : kOutOfRange, 0, 0);
+      }
+    }
+  }
+}
+
+// Row scales into row_rstd[r]: each lane sums its tile sums in chunk order (four at a time),
+// then the wave sums its lanes (xor butterfly) -- the same order in every workgroup, whatever
+// the wave count -- and 1 / rms = rsqrt(sum / K + eps).
+template <int W>
+__device__ __forceinline__ void ns_row_scales(const NsStats<W>& st, __amdgpu_buffer_rsrc_t rq, float* row_rstd, int M,
+                                              int K, int tiles_k, float eps, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < NsStats<W>::kRows; ++j) {
+    const int r = wave + j * W;
+    if (r < M) {  // wave-uniform
+      float t = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4_t v = st.q[j][h];
+        t += (__uint_as_float(v[0]) + __uint_as_float(v[1])) + (__uint_as_float(v[2]) + __uint_as_float(v[3]));
+      }
+      for (int c0 = 4 * lane + 512; c0 < tiles_k; c0 += 256) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(r * tiles_k + c0) * 4u, 0, 0);
+        t += (__uint_as_float(v[0]) + __uint_as_float(v[1])) + (__uint_as_float(v[2]) + __uint_as_float(v[3]));
+      }
+      t = wave_sum64(t);
+      if (lane == 0) row_rstd[r] = rsqrt_rn(t / static_cast<float>(K) + eps);
+    }
+  }
+}
+
+// x_norm = bf16(bf16(s * rstd) * w) of the lane's chunk of every row into the wave's staged
+// activation slice; the writer workgroup also stores it to x_out.
+template <int W, int NSR>
+__device__ __forceinline__ void ns_rows(const NsRegs<NSR>& ns, const float* row_rstd, uint8_t* wl, const DecodeLds& lay,
+                                        int M, int K, int g_first, int n_items, int lane, uint16_t* x_out) {
+  const int i = lane >> 4;
+  const int p = lane & 15;
+  if (i >= n_items) return;
+  float w[8];
+  unpack_bf16x8(as_uint4(ns.w), w);
+  const size_t col = static_cast<size_t>(g_first + i * W) * kGroup + 8 * p;
+#pragma unroll
+  for (int r = 0; r < NSR; ++r) {
+    if (r < M) {
+      float sv[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sv[q] = __uint_as_float(ns.s[r][0][q]);
+        sv[4 + q] = __uint_as_float(ns.s[r][1][q]);
+      }
+      const uint4 out = rms_scale_bf16x8(sv, row_rstd[r], w);
+      *reinterpret_cast<uint4*>(wl + lay.x_off + (i * M + r) * 256 + ((p ^ r) & 15) * 16) = out;
+      if (x_out != nullptr) *reinterpret_cast<uint4*>(x_out + static_cast<size_t>(r) * K + col) = out;
+    }
+  }
+}
+
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR, int NSR>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -544,12 +604,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             int split, int up_tiles, DecodeGeom geo, DecodeNorm nrm,
                                                             DecodeRowStats rs) {
   constexpr bool NORM = NR > 0;
+  constexpr bool NS = NSR > 0;
   static_assert(!NORM || (XL && MB == 1), "the norm prologue works on staged rows (M <= 4)");
-  static_assert(!NS || (!XL && !NORM), "normalized fp32 inputs are not staged");
+  static_assert(!NS || (XL && MB == 1 && !NORM && NSR <= 8), "the fused-norm consumer stages its rows (M <= 8)");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
   __shared__ float norm_part[NORM ? WAVES : 1][4];
-  __shared__ float row_rstd[NS ? 16 * MB : 1];
+  __shared__ float row_rstd[NS ? 8 : 1];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   constexpr int W = WAVES;
@@ -567,16 +628,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const DecodeLds lay{0u, geo.z_off, geo.x_off, geo.c_off, geo.d_off, geo.wave_bytes, 0u, 0u, 0u};
 
   DecodeSources src;
-  src.x = NS ? make_buffer(rs.s_in, geo.x_bytes * 2u) : make_buffer(x, geo.x_bytes);
+  src.x = make_buffer(x, geo.x_bytes);
   src.w = make_buffer(packed, geo.w_bytes);
   src.s = make_buffer(scales, geo.s_bytes);
   src.z = make_buffer(qzeros, geo.z_bytes);
-  src.nw = make_buffer(NS ? rs.w : nullptr, NS ? static_cast<uint32_t>(K) * 2u : 0u);
   uint32_t x_row[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int row = 16 * mb + (lane & 15);
-    x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * (NS ? 4u : 2u) : kOutOfRange;
+    x_row[mb] = row < M ? static_cast<uint32_t>(row * K + 8 * (lane >> 4)) * 2u : kOutOfRange;
   }
 
   f32x4_t acc[MB][TN];
@@ -589,66 +649,79 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   const int n_items = nG > wave ? (nG - wave + W - 1) / W : 0;
   uint8_t* wl = lds + wave * lay.wave_bytes;
   StagedRegs<TN, XL, kPre> staged;
-  load_staged<TN, XL, W, NORM, kPre>(staged, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
+  load_staged<TN, XL, W, NORM || NS, kPre>(staged, src, M, K, N, tb, dt, g_begin + wave, n_items, lane, geo.m_mul);
+  // Residual epilogues: when every wave owns at most one output pair (pair p belongs to wave
+  // p), the wave loads its pair's residual values now, ahead of the ring, so their latency
+  // (the previous kernel wrote them) hides behind the stream instead of ending the kernel.
+  constexpr bool kResPre = MB * TN <= WAVES;
+  uint32_t res_pre[2] = {0u, 0u};  // rows 16 mb + 4 (lane / 16) + i, i < 4, two bf16 per word
+  if (kResPre && res != nullptr && up_tiles == 0 && wave < MB * TN) {
+    const int mb = wave / TN, tt = wave % TN;
+    const size_t n = 16 * static_cast<size_t>(tb + tt) + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * mb + 4 * (lane >> 4) + i;
+      const uint32_t v = row < M ? res[static_cast<size_t>(row) * N + n] : 0u;
+      res_pre[i >> 1] |= v << (16 * (i & 1));
+    }
+  }
+  // The residual of output pair p (owned by this wave), row i of the lane's four, at idx.
+  auto res_bits = [&](int p, int i, size_t idx) -> uint16_t {
+    (void)p;
+    if constexpr (kResPre) return static_cast<uint16_t>(res_pre[i >> 1] >> (16 * (i & 1)));
+    return res[idx];
+  };
   NormRegs<(NR > 0 ? NR : 1)> nr;
   if constexpr (NORM)
     load_norm_operands<W>(nr, src, make_buffer(nrm.res, nrm.res ? geo.x_bytes : 0u),
                           make_buffer(nrm.w, static_cast<uint32_t>(K) * 2u), M, K, g_begin + wave, n_items, lane);
+  // NS: the rows of s (M x K fp32: twice the bf16 activation bytes) and the tile sums of s^2
+  NsRegs<(NSR > 0 ? NSR : 1)> nsr;
+  NsStats<W> nss;
+  const int tiles_k = K / kTileCols;
+  const __amdgpu_buffer_rsrc_t rq = make_buffer(NS ? rs.ssq_in : nullptr, NS ? static_cast<uint32_t>(M) * tiles_k * 4u : 0u);
+  if constexpr (NS) {
+    load_ns_operands<W>(nsr, make_buffer(rs.s_in, geo.x_bytes * 2u), make_buffer(rs.w, static_cast<uint32_t>(K) * 2u),
+                        M, K, g_begin + wave, n_items, lane);
+    load_ns_stats<W>(nss, rq, M, tiles_k, wave, lane);
+  }
   __builtin_amdgcn_sched_barrier(0);  // the staging loads stay ahead of the ring's
 
   // Depth-DEPTH ring over the wave's items: item i is loaded while item i - DEPTH is being
   // consumed.  The ring is filled first; then every load is issued whether or not its item
   // exists (out-of-range ones fetch nothing), so no branch encloses a load and the
   // scheduling barriers keep each item's loads together and in order.
-  DecodeStage<MB, TN, XL, NS> ring[DEPTH];
+  DecodeStage<MB, TN, XL> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d)
-    load_decode_stage<MB, TN, XL, NS>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
-  // NS: each row's 1 / rms from the producer's per-tile sums of s^2 (K / 16 per row, summed in
-  // a fixed order: lane by lane in 4-value chunks, then across the wave), computed while the
-  // ring's first loads are in flight; wave w takes rows w, w + W, ...
-  float rstd[MB];
-  if constexpr (NS) {
-    const int tiles_k = K / kTileCols;
-    const __amdgpu_buffer_rsrc_t rq = make_buffer(rs.ssq_in, static_cast<uint32_t>(M) * tiles_k * 4u);
-    for (int r = wave; r < M; r += W) {
-      float t = 0.f;
-      for (int c0 = 4 * lane; c0 < tiles_k; c0 += 256) {
-        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(r * tiles_k + c0) * 4u, 0, 0);
-        t += (__uint_as_float(v[0]) + __uint_as_float(v[1])) + (__uint_as_float(v[2]) + __uint_as_float(v[3]));
-      }
-      t = wave_sum64(t);
-      if (lane == 0) row_rstd[r] = rsqrt_rn(t / static_cast<float>(K) + rs.eps);
-    }
-    // Only LDS needs ordering: the ring's loads stay in flight.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int row = 16 * mb + (lane & 15);
-      rstd[mb] = row_rstd[row < M ? row : M - 1];
-    }
-  }
-  uint16_t* x_out = NS && blockIdx.x == 0 ? rs.x_out : nullptr;  // the first column block stores x_norm
+    load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + d * W, d < n_items, N, tb, dt, lane);
   // The staged operands go to LDS as soon as they arrive (the ring's loads stay in flight:
   // the compiler waits for each register load individually), then the norm prologue works
   // from its registers and writes the activation slice.
-  store_staged<TN, XL, NORM, kPre>(staged, wl, lay, M, n_items, lane);
+  store_staged<TN, XL, NORM || NS, kPre>(staged, wl, lay, M, n_items, lane);
   if constexpr (NORM)
     norm_rows<W>(nr, wl, lay, norm_part, wave, lane, M, K, g_begin + wave, n_items, blockIdx.x == 0 && sidx == 0, nrm);
+  if constexpr (NS) {
+    // Row scales (wave w takes rows w, w + W, ...), shared through LDS by one barrier that
+    // orders LDS alone (the ring's loads stay in flight); then each wave normalizes its items'
+    // rows into its own slice, which only it reads.  The first column block's workgroups
+    // store x_norm (each its own K range).
+    ns_row_scales<W>(nss, rq, row_rstd, M, K, tiles_k, rs.eps, wave, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    ns_rows<W>(nsr, row_rstd, wl, lay, M, K, g_begin + wave, n_items, lane, blockIdx.x == 0 ? rs.x_out : nullptr);
+  }
 
   const NibbleConsts nib = nibble_consts();
   for (int base = 0; base < n_items; base += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int i = base + d;
-      if (i < n_items)
-        compute_decode_stage<MB, TN, XL, kPre, NS>(acc, ring[d], wl, lay, i, M, nib, lane, rstd, x_out,
-                                                   g_begin + wave + i * W, K);
+      if (i < n_items) compute_decode_stage<MB, TN, XL, kPre>(acc, ring[d], wl, lay, i, M, nib, lane);
       const int in = i + DEPTH;
       __builtin_amdgcn_sched_barrier(0);
-      load_decode_stage<MB, TN, XL, NS>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
+      load_decode_stage<MB, TN, XL>(ring[d], src, x_row, g_begin + wave + in * W, in < n_items, N, tb, dt, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -722,7 +795,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
     if (!act && rs.s_out != nullptr) {
       // Producer of a fused RMSNorm: s = float(bf16(o)) + float(res) in fp32, the new
       // residual bf16(s), and per row the sum of s^2 over this 16-column tile (the 16 lanes
-      // of each row quad hold its 16 columns; xor shuffles within them, in a fixed order).
+      // of each row quad -- one DPP row -- hold its 16 columns).
       const int n = 16 * (tb + tt) + c;
       float ss[4];
 #pragma unroll
@@ -731,16 +804,14 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
         ss[i] = 0.f;
         if (row < M) {
           const size_t idx = static_cast<size_t>(row) * N + n;
-          const float sv = bf16_bits_to_f32(f32_to_bf16_bits(out[p][i])) + bf16_bits_to_f32(res[idx]);
+          const float sv = bf16_bits_to_f32(f32_to_bf16_bits(out[p][i])) + bf16_bits_to_f32(res_bits(p, i, idx));
           rs.s_out[idx] = sv;
           rs.res_out[idx] = f32_to_bf16_bits(sv);
           ss[i] = sv * sv;
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 16);
+      for (int i = 0; i < 4; ++i) ss[i] = row_sum16(ss[i]);
       if (c == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -756,7 +827,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
         if (row < M) {
           const size_t idx = static_cast<size_t>(row) * N + n;
           const uint16_t b = f32_to_bf16_bits(out[p][i]);
-          y[idx] = res ? add_bf16(b, res[idx]) : b;
+          y[idx] = res ? add_bf16(b, res_bits(p, i, idx)) : b;
         }
       }
     } else if constexpr (H > 0) {
@@ -784,6 +855,7 @@ bool decode_stages_x(int M, int K, int split) {
 bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split, bool ns) {
   const int G = K / kGroup;
   const int items = ((G + split - 1) / split + waves - 1) / waves;
+  if (ns && (M > 8 || items > kNormItems)) return false;  // the consumer's lane map: 4 items x 16 chunks
   const bool sz = (tn == 1 && decode_prebuilt_scales(waves, depth))
                       ? items * 16 <= 64 * kStageE
                       : items * tn * 8 <= 64 * kStageS && items * tn * 2 <= 64 * kStageZ;
@@ -791,7 +863,7 @@ bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split, bo
 }
 
 size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split, bool ns) {
-  return decode_lds_layout(M, K, tn, waves, split, !ns && decode_stages_x(M, K, split),
+  return decode_lds_layout(M, K, tn, waves, split, ns || decode_stages_x(M, K, split),
                            decode_prebuilt_scales(waves, depth))
       .total;
 }
@@ -805,16 +877,16 @@ size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int spl
 
 constexpr int kMaxDevices = 64;
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0, bool NS = false>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0, int NSR = 0>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
-  if constexpr (!decode_config_fits(MB, TN, DEPTH, XL, NS)) {
+  if constexpr (!decode_config_fits(MB, TN, DEPTH, XL)) {
     return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
   } else {
   const dim3 grid(a.N / (kTileCols * TN), a.split);
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
   const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
-  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split, NS))
+  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split, NSR > 0) || a.M > (NSR > 0 ? NSR : 64))
     return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
@@ -824,14 +896,14 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     if (!raised[dev].load(std::memory_order_acquire)) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NS>),
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NSR>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                static_cast<int>(kDecodeMaxLds));
       if (e != hipSuccess) return e;
       raised[dev].store(true, std::memory_order_release);
     }
   }
-  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NS><<<grid, 64 * WAVES, lds, stream>>>(
+  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NSR><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles,
       geo, a.norm, a.rs);
   return hipGetLastError();
@@ -840,8 +912,11 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
 
 template <int MB, int TN, int DEPTH, int WAVES>
 static hipError_t launch_decode_x(const DecodeArgs& a, bool norm, hipStream_t stream) {
-  if (a.rs.s_in != nullptr) {  // normalized fp32 inputs: M < 32, never staged, at most 8 waves
-    if constexpr (MB <= 2 && WAVES <= 8) return launch_decode_t<MB, TN, DEPTH, WAVES, false, 0, true>(a, stream);
+  if (a.rs.s_in != nullptr) {  // fused-norm consumer: M <= 8, staged rows, at most 8 waves, 2 groups in flight
+    if constexpr (MB == 1 && WAVES <= 8 && DEPTH <= 2) {
+      if (a.M <= 4) return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 4>(a, stream);
+      return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 8>(a, stream);
+    }
     return hipErrorInvalidValue;  // checked by the API
   }
   if constexpr (MB == 1) {

@@ -44,6 +44,8 @@ constexpr int kStageS = 3;
 constexpr int kStageZ = 1;
 constexpr int kStageX = 4;
 constexpr int kStageE = 4;
+// ns: the fused-norm consumer (DecodeRowStats), which stages its normalized rows (M <= 8, at
+// most 4 groups per wave).
 bool decode_stage_fits(int M, int K, int tn, int waves, int depth, int split, bool ns = false);
 // Whether a decode configuration builds its dequant operands once per wave in LDS
 // (8 waves and a ring at least two groups deep) instead of per tile and group.
@@ -55,13 +57,11 @@ size_t decode_lds_bytes(int M, int K, int tn, int waves, int depth, int split, b
 // Register budget of a decode configuration (16-row activation blocks mb, tiles tn, ring
 // depth, activations staged or not): fp32 accumulators plus the ring of in-flight loads,
 // in 32-bit registers per lane, at most 176.  Configurations beyond it are not compiled.
-// ns: the activations arrive as fp32 sums and are normalized in registers (two 16-byte loads
-// per fragment, plus four of the norm weight per group; see DecodeRowStats).
-constexpr int decode_ring_regs(int mb, int tn, int depth, bool xl, bool ns = false) {
-  return 4 * mb * tn + depth * 4 * (tn + (xl ? 0 : (ns ? 8 : 4) * mb) + (ns ? 4 : 0));
+constexpr int decode_ring_regs(int mb, int tn, int depth, bool xl) {
+  return 4 * mb * tn + depth * 4 * (tn + (xl ? 0 : 4 * mb));
 }
-constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl, bool ns = false) {
-  return decode_ring_regs(mb, tn, depth, xl, ns) <= 176;
+constexpr bool decode_config_fits(int mb, int tn, int depth, bool xl) {
+  return decode_ring_regs(mb, tn, depth, xl) <= 176;
 }
 
 // RMSNorm(+residual) prologue of a decode GEMM whose activations are staged in LDS: the
@@ -77,16 +77,16 @@ struct DecodeNorm {
   float eps;
 };
 
-// An RMSNorm split across two decode GEMMs (M < 32), so that no separate norm launch sits
+// An RMSNorm split across two decode GEMMs (M <= 8), so that no separate norm launch sits
 // between them.  The producer -- the O or down projection, whose output h feeds the norm --
 // adds the residual in its epilogue as the reference's add_rms_forward does, s =
 // float(bf16(h)) + float(res) in fp32, and writes s (s_out, fp32 [M, N]), the new residual
 // bf16(s) (res_out, [M, N]; may be res itself) and, per row, the sum of s^2 over each
 // 16-column tile (ssq_out, [M, N / 16]).  The consumer -- the QKV or gate|up projection
 // behind the norm -- reads s (s_in, [M, K]) and the tile sums (ssq_in, [M, K / 16]), sums
-// each row's in a fixed order to rstd = 1 / sqrt(mean(s^2) + eps), and multiplies x_norm =
-// bf16(bf16(s * rstd) * w) (w: the norm weight, [K]); the workgroups of its first column
-// block also store x_norm (x_out, [M, K], may be null).
+// each row's in a fixed order to rstd = 1 / sqrt(mean(s^2) + eps), and stages x_norm =
+// bf16(bf16(s * rstd) * w) (w: the norm weight, [K]) in LDS as its activations; the
+// workgroups of its first column block also store x_norm (x_out, [M, K], may be null).
 struct DecodeRowStats {
   float* s_out;
   uint16_t* res_out;

@@ -256,7 +256,7 @@ class RowParallelLinear(LinearBase):
 
     def forward_residual_stats(self, x: torch.Tensor, residual: torch.Tensor,
                                residual_out: torch.Tensor | None = None):
-        """At decode sizes (packed M <= 31): this projection, the residual add of the next
+        """At decode sizes (packed M <= 8): this projection, the residual add of the next
         add_rms_forward and that norm's row statistics in the GEMM epilogue, so that the norm
         needs no launch of its own; returns ``(NormInput, new residual)`` for the next
         layer's forward_rmsnorm_stats.  ``residual_out`` may be ``residual`` (in place)."""

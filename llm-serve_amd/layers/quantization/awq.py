@@ -554,8 +554,9 @@ def awq_linear_rmsnorm(inputs: torch.Tensor, residual: torch.Tensor | None, norm
     return y.reshape(*lead, n_out), (residual_out if residual is not None else inputs)
 
 
-# The RMSNorm split across two GEMMs runs in the decode kernel: packed M below this.
-FUSED_NORM_MAX_M = 31
+# The RMSNorm split across two GEMMs runs in the decode kernel with its normalized rows
+# staged in LDS: packed M up to this.
+FUSED_NORM_MAX_M = 8
 
 
 @dataclass(frozen=True)

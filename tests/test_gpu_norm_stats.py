@@ -24,7 +24,7 @@ from oracle import awq_oracle as ora
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
-MS = (1, 2, 5, 16, 17, 31)
+MS = (1, 2, 3, 4, 5, 7, 8)
 
 
 def rand_bits(shape, seed, scale=1.0, offset=0.0):
@@ -111,7 +111,7 @@ def test_rmsnorm_stats_consumer(gpu_lib, shape, silu):
         assert (bits_of(y) == bits_of(plain)).mean() > 0.9, m
         y2 = awq.awq_linear_rmsnorm_stats(inp, w, EPS, packed, qz, s, group_size=128, silu_mul=silu)
         assert torch.equal(y2.view(torch.int16), y.view(torch.int16)), m
-        if not silu and m in (1, 17):
+        if not silu and m in (1, 7):
             # the oracle's fp64 GEMM of the oracle's normalized activations (the CPU GEMM at the
             # full QKV shape takes seconds: two row counts)
             want_y = ora.awq_linear_ref(want_xn, qw.cpu().numpy(), qz.cpu().numpy(), bits_of(s), 128)
@@ -190,6 +190,6 @@ def test_norm_stats_layer_api(gpu_lib):
     assert rel_err(y, qkv(xn).view(6, -1).float()) <= GEMM_REL_TOL
     z = gate_up.forward_rmsnorm_stats_silu_and_mul(norm, inp)
     assert rel_err(z, gate_up.forward_silu_and_mul(xn).view(6, -1).float()) <= GEMM_REL_TOL
-    big = bf16_from_bits(rand_bits((32, k), seed=12))
-    with pytest.raises(ValueError, match="M <= 31"):
+    big = bf16_from_bits(rand_bits((9, k), seed=12))
+    with pytest.raises(ValueError, match="M <= 8"):
         o_proj.forward_residual_stats(big, big)
