@@ -370,7 +370,7 @@ def awq_linear(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzeros: torch
     ``packed_qweight`` comes from ``repack_awq_qweight``; ``qzeros`` [K/128, N/8] and
     ``scales`` [K/128, N] are the AutoAWQ tensors.  Leading dimensions of ``inputs`` are
     flattened into M.  ``workspace`` (uint8, zero-filled when allocated) overrides the
-    per-stream shared one."""
+    per-device shared one."""
     x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
     m = x.shape[0]
     y = torch.empty((m, n), dtype=inputs.dtype, device=inputs.device)
