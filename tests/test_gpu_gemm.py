@@ -164,7 +164,7 @@ def test_scales_and_zeros_at_word_alignment(gpu_lib):
 
 
 def test_shared_workspace_across_shapes_and_m(gpu_lib):
-    """One workspace reused by calls of different M and N (as the per-stream pool does):
+    """One workspace reused by calls of different M and N (as the per-device pool does):
     the counters must always be found re-armed."""
     k = 4096
     ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
@@ -378,7 +378,7 @@ def test_hip_graph_capture_replays_match_eager(gpu_lib):
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        awq.awq_linear(static_x, packed, qz, s, group_size=128)  # warm the per-stream workspace
+        awq.awq_linear(static_x, packed, qz, s, group_size=128)  # warm the per-device workspace
     torch.cuda.current_stream().wait_stream(stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
