@@ -440,7 +440,52 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
     __builtin_amdgcn_s_waitcnt(0);  // the region's reads are done before the next pass writes it
     __builtin_amdgcn_wave_barrier();
   };
-  if (!o.act) {
+  if constexpr ((TW & (TW - 1)) != 0) {
+    // Three tiles per wave (48 columns; the fused product never has an odd count): whole
+    // 96-byte row segments per store, the passes taking row ranges instead of column
+    // ranges.  (A 32-byte piece per pass left every 64-byte block to two partial writes:
+    // 1.7x the output bytes at QKV M=2048.)  Chunks rotate by row, (q + r) % CPR, since CPR
+    // is not a power of two; 10 rows of 6 chunks per store round, lanes 60..63 idle.
+    static_assert(WM % kParts == 0, "row passes of whole 16-row tiles");
+    constexpr int CPR = 2 * TW;
+    constexpr int PITCH = 16 * CPR;
+    constexpr int MP = WM / kParts;  // 16-row tiles per pass
+    constexpr int RP = 16 * MP;      // rows per pass: RP * PITCH == kRegion
+    static_assert(RP * PITCH <= kRegion, "a row pass exceeds the wave's region");
+    constexpr int kRowsPerRound = 64 / CPR;
+#pragma unroll
+    for (int part = 0; part < kParts; ++part) {
+#pragma unroll
+      for (int ml = 0; ml < MP; ++ml)
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * ml + 4 * (lane >> 4) + i;
+            const int c = 16 * t + (lane & 15);
+            const int off = r * PITCH + ((((c >> 3) + r) % CPR) << 4) + ((c & 7) << 1);
+            *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(acc[part * MP + ml][t][i]);
+          }
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+      for (int round = 0; round < (RP + kRowsPerRound - 1) / kRowsPerRound; ++round) {
+        const int r = kRowsPerRound * round + lane / CPR;
+        const int q = lane % CPR;
+        if (lane < kRowsPerRound * CPR && r < RP) {
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + r * PITCH + (((q + r) % CPR) << 4));
+          const int row = o.row_w + RP * part + r;
+          if (row < o.M) {
+            const size_t off = static_cast<size_t>(row) * o.n_out + o.col_w + 8 * q;
+            *reinterpret_cast<uint4*>(o.y + off) =
+                o.res ? add_bf16x8(v, *reinterpret_cast<const uint4*>(o.res + off)) : v;
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // the region's reads are done before the next pass writes it
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else if (!o.act) {
     constexpr int TP0 = TW / kParts;
     constexpr int TP = TP0 & -TP0;  // tiles per pass: a power of two, so that rows are whole lane groups
     constexpr int CPR = 2 * TP;     // 16-byte chunks per row
