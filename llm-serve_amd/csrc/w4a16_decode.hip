@@ -914,6 +914,9 @@ template <int MB, int TN, int DEPTH, int WAVES>
 static hipError_t launch_decode_x(const DecodeArgs& a, bool norm, hipStream_t stream) {
   if (a.rs.s_in != nullptr) {  // fused-norm consumer: M <= 8, staged rows, at most 8 waves, 2 groups in flight
     if constexpr (MB == 1 && WAVES <= 8 && DEPTH <= 2) {
+      // rows held in registers: as few as M allows (the plain kernel's occupancy at M <= 2)
+      if (a.M <= 1) return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 1>(a, stream);
+      if (a.M <= 2) return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 2>(a, stream);
       if (a.M <= 4) return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 4>(a, stream);
       return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, 8>(a, stream);
     }
