@@ -593,7 +593,10 @@ __device__ __forceinline__ void ns_rows(const NsRegs<NSR>& ns, const float* row_
   }
 }
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR, int NSR>
+// FN, the fused RMSNorm split across two GEMMs (DecodeRowStats): 0 none, 1..8 the consumer
+// with room for FN rows, -1 the producer.  A compile-time mode, so that the plain kernels carry
+// none of it (the producer's epilogue behind a run-time test cost the plain decode GEMMs 2 %).
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR, int FN>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ packed,
                                                             const uint32_t* __restrict__ qzeros,
@@ -604,9 +607,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
                                                             int split, int up_tiles, DecodeGeom geo, DecodeNorm nrm,
                                                             DecodeRowStats rs) {
   constexpr bool NORM = NR > 0;
-  constexpr bool NS = NSR > 0;
+  constexpr bool NS = FN > 0;
+  constexpr bool PROD = FN < 0;
+  constexpr int NSR = NS ? FN : 1;
   static_assert(!NORM || (XL && MB == 1), "the norm prologue works on staged rows (M <= 4)");
-  static_assert(!NS || (XL && MB == 1 && !NORM && NSR <= 8), "the fused-norm consumer stages its rows (M <= 8)");
+  static_assert(!NS || (XL && MB == 1 && !NORM && FN <= 8), "the fused-norm consumer stages its rows (M <= 8)");
+  static_assert(!PROD || (MB == 1 && !NORM), "the fused-norm producer runs at M <= 8");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   __shared__ int is_last;
   __shared__ float norm_part[NORM ? WAVES : 1][4];
@@ -676,7 +682,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
     load_norm_operands<W>(nr, src, make_buffer(nrm.res, nrm.res ? geo.x_bytes : 0u),
                           make_buffer(nrm.w, static_cast<uint32_t>(K) * 2u), M, K, g_begin + wave, n_items, lane);
   // NS: the rows of s (M x K fp32: twice the bf16 activation bytes) and the tile sums of s^2
-  NsRegs<(NSR > 0 ? NSR : 1)> nsr;
+  NsRegs<NSR> nsr;
   NsStats<W> nss;
   const int tiles_k = K / kTileCols;
   const __amdgpu_buffer_rsrc_t rq = make_buffer(NS ? rs.ssq_in : nullptr, NS ? static_cast<uint32_t>(M) * tiles_k * 4u : 0u);
@@ -792,7 +798,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
   for (int p = 0; p < kPairs; ++p) {
     if (owner(p) != wave) continue;
     const int mb = p / TN, tt = p % TN;
-    if (!act && rs.s_out != nullptr) {
+    if (PROD) {  // compile-time
       // Producer of a fused RMSNorm: s = float(bf16(o)) + float(res) in fp32, the new
       // residual bf16(s), and per row the sum of s^2 over this 16-column tile (the 16 lanes
       // of each row quad -- one DPP row -- hold its 16 columns).
@@ -877,7 +883,7 @@ size_t decode_norm_lds_bytes(int M, int K, int tn, int waves, int depth, int spl
 
 constexpr int kMaxDevices = 64;
 
-template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0, int NSR = 0>
+template <int MB, int TN, int DEPTH, int WAVES, bool XL, int NR = 0, int FN = 0>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   if constexpr (!decode_config_fits(MB, TN, DEPTH, XL)) {
     return hipErrorInvalidValue;  // rejected by the API before launch; not compiled
@@ -886,7 +892,8 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   constexpr bool kPre = decode_prebuilt_scales(WAVES, DEPTH);
   const size_t lds = decode_lds_layout(a.M, a.K, TN, WAVES, a.split, XL, kPre).total;
   const DecodeGeom geo = decode_geom(a.M, a.K, a.N, TN, WAVES, a.split, XL, kPre);
-  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split, NSR > 0) || a.M > (NSR > 0 ? NSR : 64))
+  if (lds > kDecodeMaxLds || !decode_stage_fits(a.M, a.K, TN, WAVES, DEPTH, a.split, FN > 0) ||
+      a.M > (FN > 0 ? FN : FN < 0 ? 8 : 64))
     return hipErrorInvalidValue;  // checked by the API before launch
   if (lds > 64 * 1024) {
     // Dynamic LDS beyond 64 KiB must be allowed per kernel, once per device (a repeated
@@ -896,14 +903,14 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     if (!raised[dev].load(std::memory_order_acquire)) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NSR>),
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, FN>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                static_cast<int>(kDecodeMaxLds));
       if (e != hipSuccess) return e;
       raised[dev].store(true, std::memory_order_release);
     }
   }
-  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, NSR><<<grid, 64 * WAVES, lds, stream>>>(
+  decode_kernel<MB, TN, DEPTH, WAVES, XL, NR, FN><<<grid, 64 * WAVES, lds, stream>>>(
       a.x, a.packed, a.qzeros, a.scales, a.y, a.res, a.partials, a.counters, a.M, a.K, a.N, a.split, a.up_tiles,
       geo, a.norm, a.rs);
   return hipGetLastError();
@@ -912,6 +919,13 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
 
 template <int MB, int TN, int DEPTH, int WAVES>
 static hipError_t launch_decode_x(const DecodeArgs& a, bool norm, hipStream_t stream) {
+  if (a.rs.s_out != nullptr) {  // fused-norm producer: the plain plan's kernel with its epilogue, M <= 8
+    if constexpr (MB == 1) {
+      if (decode_stages_x(a.M, a.K, a.split)) return launch_decode_t<1, TN, DEPTH, WAVES, true, 0, -1>(a, stream);
+      return launch_decode_t<1, TN, DEPTH, WAVES, false, 0, -1>(a, stream);
+    }
+    return hipErrorInvalidValue;  // checked by the API
+  }
   if (a.rs.s_in != nullptr) {  // fused-norm consumer: M <= 8, staged rows, at most 8 waves, 2 groups in flight
     if constexpr (MB == 1 && WAVES <= 8 && DEPTH <= 2) {
       // rows held in registers: as few as M allows (the plain kernel's occupancy at M <= 2)
