@@ -193,3 +193,46 @@ def test_norm_stats_layer_api(gpu_lib):
     big = bf16_from_bits(rand_bits((9, k), seed=12))
     with pytest.raises(ValueError, match="M <= 8"):
         o_proj.forward_residual_stats(big, big)
+
+
+@pytest.mark.parametrize("shape,m", [("o", 8), ("down", 3), ("down", 8)])
+def test_rmsnorm_stats_consumer_split_and_long_rows(gpu_lib, shape, m):
+    """Consumer plans beyond the QKV / gate_up shapes: a K split across workgroups (the O shape
+    at M = 8: every split's first column block stores its K range of x_norm) and rows longer
+    than 8192 (K = 12288: the tile sums beyond the first two chunks per lane are loaded after
+    the ring), against the oracle's add_rms_forward and the plain GEMM of x_norm."""
+    awq = awq_mod()
+    lib = awq.lib()
+    k, n = QWEN3_SHAPES[shape]
+    print(f"rmsnorm_stats consumer {shape} m={m} plan {lib.plan(m, k, n, 2)}", flush=True)
+    packed, qz, s = layer(shape, seed=86)
+    w_bits = rand_bits((k,), seed=9, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    h_bits = rand_bits((m, k), seed=m + 400, scale=2.0)
+    r_bits = rand_bits((m, k), seed=m + 500, scale=3.0)
+    h, res = bf16_from_bits(h_bits), bf16_from_bits(r_bits)
+    sv = (h.float() + res.float()).contiguous()
+    ssq = (sv.double() ** 2).view(m, -1, 16).sum(-1).float().contiguous()
+    xn = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+    y = awq.awq_linear_rmsnorm_stats(awq.NormInput(sv, ssq), w, EPS, packed, qz, s, group_size=128, x_norm=xn)
+    want_xn, _, _ = ora.add_rms_norm_ref(h_bits, r_bits, w_bits, EPS)
+    d = ulp_diff(bits_of(xn), want_xn)
+    assert d.max() <= 2 and (d == 0).mean() > 0.99, (d.max(), (d == 0).mean())
+    plain = awq.awq_linear(xn, packed, qz, s, group_size=128)
+    assert rel_err(y, plain.float()) <= GEMM_REL_TOL
+    assert (bits_of(y) == bits_of(plain)).mean() > 0.9
+
+
+def test_norm_stats_empty_batch(gpu_lib):
+    """M = 0: both calls return empty results and enqueue nothing."""
+    awq = awq_mod()
+    k, n = QWEN3_SHAPES["o"]
+    packed, qz, s = layer("o", seed=87)
+    x = torch.empty((0, k), dtype=torch.bfloat16, device="cuda")
+    res = torch.empty((0, n), dtype=torch.bfloat16, device="cuda")
+    inp, res_out = awq.awq_linear_residual_stats(x, packed, qz, s, res, group_size=128)
+    assert inp.s.shape == (0, n) and inp.ssq.shape == (0, n // 16) and res_out.shape == (0, n)
+    pq, zq, sq = layer("qkv", seed=88)
+    w = bf16_from_bits(rand_bits((n,), seed=3, scale=0.1, offset=1.0))
+    y = awq.awq_linear_rmsnorm_stats(inp, w, EPS, pq, zq, sq, group_size=128)
+    assert y.shape == (0, QWEN3_SHAPES["qkv"][1])

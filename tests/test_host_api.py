@@ -164,6 +164,36 @@ def test_tensor_functions_have_no_cpu_path(awq):
         awq.awq_linear(x, qw.flatten(), qz, s, group_size=128)
 
 
+def test_fused_norm_functions_validate_and_have_no_cpu_path(awq):
+    """The RMSNorm split across two GEMMs: no CPU path, and the NormInput contract (fp32 s
+    [M, K], ssq [M, K / 16], M <= FUSED_NORM_MAX_M) is checked before any library call."""
+    p = ora.make_problem(seed=2, m=2, k=128, n=64)
+    qw = torch.from_numpy(p["qweight"]).flatten()
+    qz = torch.from_numpy(p["qzeros"])
+    s = torch.from_numpy(p["scales_bits"].view(np.int16)).view(torch.bfloat16)
+    x = torch.from_numpy(p["x_bits"].view(np.int16)).view(torch.bfloat16)
+    res = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        awq.awq_linear_residual_stats(x, qw, qz, s, res, group_size=128)
+    w = torch.ones(128, dtype=torch.bfloat16)
+    k = 128
+    assert awq.FUSED_NORM_MAX_M == 8
+    good = awq.NormInput(torch.zeros((2, k)), torch.zeros((2, k // 16)))
+    with pytest.raises(ValueError, match="share one GPU"):
+        awq.awq_linear_rmsnorm_stats(good, w, 1e-6, qw, qz, s, group_size=128)
+    with pytest.raises(ValueError, match="M <= 8"):
+        awq.awq_linear_rmsnorm_stats(awq.NormInput(torch.zeros((9, k)), torch.zeros((9, k // 16))), w, 1e-6, qw, qz, s,
+                                     group_size=128)
+    with pytest.raises(ValueError, match="ssq must be"):
+        awq.awq_linear_rmsnorm_stats(awq.NormInput(torch.zeros((2, k)), torch.zeros((2, 4))), w, 1e-6, qw, qz, s,
+                                     group_size=128)
+    with pytest.raises(ValueError, match="fp32"):
+        awq.awq_linear_rmsnorm_stats(awq.NormInput(torch.zeros((2, k), dtype=torch.bfloat16), torch.zeros((2, 8))),
+                                     w, 1e-6, qw, qz, s, group_size=128)
+    with pytest.raises(ValueError, match="RMSNorm weight"):
+        awq.awq_linear_rmsnorm_stats(good, w[:64], 1e-6, qw, qz, s, group_size=128)
+
+
 def test_validation_messages_match_reference(awq):
     qw = torch.zeros((4, 1), dtype=torch.int32)
     qz = torch.zeros((2, 1), dtype=torch.int32)
