@@ -45,6 +45,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_
                             : 0;
   const size_t row = static_cast<size_t>(live ? r : 0) * K;
   const int chunks = K >> 3;
+  // The weight chunks are loaded first, so that they arrive during the sum of squares
+  // instead of after it.
+  uint4 wv[kChunks];
+#pragma unroll
+  for (int j = 0; j < kChunks; ++j) {
+    const int c = l + j * LPR;
+    if (live && c < chunks) wv[j] = *reinterpret_cast<const uint4*>(weight + 8 * c);
+  }
   float s[kChunks][8];
   float ss = 0.0f;
 #pragma unroll
@@ -80,8 +88,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_
   for (int j = 0; j < kChunks; ++j) {
     const int c = l + j * LPR;
     if (live && c < chunks) {
-      *reinterpret_cast<uint4*>(x_norm + row + 8 * c) =
-          rms_scale_bf16x8(s[j], rstd, *reinterpret_cast<const uint4*>(weight + 8 * c));
+      *reinterpret_cast<uint4*>(x_norm + row + 8 * c) = rms_scale_bf16x8(s[j], rstd, wv[j]);
     }
   }
 }
