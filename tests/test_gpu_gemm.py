@@ -1,16 +1,17 @@
 """GPU parity of the W4A16 GEMM (decode split-K kernel and MFMA tile kernel).
 
 Small sizes compare against the CPU oracle (fp64-accumulated x @ W over the reference's
-bf16 weights).  Full Qwen3-8B sizes compare against torch fp32 matmul on the GPU over the
-bit-exact dequantized weights (checked separately against the oracle in
-test_gpu_format.py).  Tolerance: max |y - r| / max(|r|, rms(r)) <= 1e-2 (GEMM_REL_TOL),
-plus the reference's own assert_close tolerances where its tests state them."""
+bf16 weights).  Full Qwen3-8B sizes compare against the oracle itself at M = 1, 16, 64 and
+2048, and at the other M against torch fp32 matmul on the GPU over the bit-exact
+dequantized weights (checked separately against the oracle in test_gpu_format.py).
+Tolerance: max |y - r| / max(|r|, rms(r)) <= 1e-2 (GEMM_REL_TOL), plus the reference's own
+assert_close tolerances where its tests state them."""
 import numpy as np
 import pytest
 import torch
 
-from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, decode_config_accepted, golden_cases,
-                         pkg, random_awq_gpu, random_x_gpu, rel_err, to_gpu, assert_gemm_close)
+from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, bf16_from_bits, bits_of, decode_config_accepted,
+                         golden_cases, pkg, random_awq_gpu, random_x_gpu, rel_err, to_gpu, assert_gemm_close)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -204,6 +205,27 @@ def test_full_qwen3_shapes_decode_sweep(gpu_lib, shape):
         x = random_x_gpu(m, k, seed=m)
         y = awq_mod().awq_linear(x, packed, qz, s, group_size=128)
         assert_gemm_close(y, full_reference(x, qw, qz, s), (m))
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
+def test_full_qwen3_shapes_against_the_oracle(gpu_lib, shape):
+    """Full shapes against the CPU oracle itself (its own dequant, fp64 x @ W;
+    awq.py:235-276): one decode launch at M = 1 and 16, a mid-M tile launch at 64 and a
+    prefill chunk of 2048 rows with activation outliers, all rows through one oracle call."""
+    k, n = QWEN3_SHAPES[shape]
+    qw, qz, s = random_awq_gpu(k, n, seed=21)
+    packed = awq_mod().repack_awq_qweight(qw)
+    ms = (1, 16, 64, 2048)
+    xs = [random_x_gpu(m, k, seed=40 + m, outliers=m == 2048) for m in ms]
+    ys = [awq_mod().awq_linear(x, packed, qz, s, group_size=128) for x in xs]
+    torch.cuda.synchronize()
+    want = ora.awq_linear_ref(np.concatenate([bits_of(x) for x in xs]), qw.cpu().numpy(), qz.cpu().numpy(),
+                              bits_of(s), 128)
+    r0 = 0
+    for m, y in zip(ms, ys):
+        print(f"oracle full shape {shape} m={m} regime={pkg().awq_regime(m, k, n)}", flush=True)
+        assert_gemm_close(y, torch.from_numpy(want[r0:r0 + m]).cuda(), (shape, m))
+        r0 += m
 
 
 @pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
