@@ -159,8 +159,9 @@ int w4a16_gemm_residual(const uint16_t* x, const int32_t* packed, const int32_t*
 
 /* y[M, N/2] = SiLU(g) * u with [g | u] = x[M, K] @ W for a gate|up weight W [K, N] whose
  * first N/2 columns are the gate projection and last N/2 the up projection (the layout of
- * MergedColumnParallelLinear's gate_up_proj); g and u stay in fp32 and the product is rounded
- * once to bf16.  Same arguments and limits as w4a16_gemm, plus N % 128 == 0; y is
+ * MergedColumnParallelLinear's gate_up_proj); g and u are rounded to bf16 as that layer
+ * returns them, and SiLU(g) * u is computed in fp32 and rounded once, the reference's two
+ * steps in one kernel.  Same arguments and limits as w4a16_gemm, plus N % 128 == 0; y is
  * [M, N/2], 16-byte aligned; workspace from w4a16_workspace_bytes(M, K, N, 128).
  * Replaces gate_up_proj followed by SiluAndMul (qwen3.py:126-130, activation.py:8-11):
  * the [M, N] gate|up intermediate is never written. */

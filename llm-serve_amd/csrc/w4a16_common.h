@@ -161,6 +161,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
+// The fused gate/up epilogue from the fp32 accumulators, in the reference's two steps: g and
+// u rounded to bf16 first (the gate_up layer's output dtype), then SiLU(g) * u in fp32 and
+// one rounding of the result (its SiluAndMul, a compiled pointwise kernel, keeps the
+// expression in fp32).
+__device__ __forceinline__ float silu_mul_of_bf16(float g, float u) {
+  const uint32_t p = pack_bf16x2(g, u);
+  return silu_mul(bf16_bits_to_f32(p & 0xFFFFu), __uint_as_float(p & 0xFFFF0000u));
+}
+
 // The two constants of the nibble unpack, held in registers: mask 0x000F000F in an SGPR,
 // bias 0x43004300 (the bf16 pair (128, 128)) in a VGPR.  Built once per kernel.  The empty
 // asm statements emit nothing; they only hide the values from constant folding, so that

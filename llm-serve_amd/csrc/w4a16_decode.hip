@@ -843,7 +843,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const uint16_t* __re
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = 16 * mb + 4 * (lane >> 4) + i;
-          if (row < M) y[static_cast<size_t>(row) * (N >> 1) + n] = f32_to_bf16_bits(silu_mul(out[p][i], u[i]));
+          if (row < M)
+            y[static_cast<size_t>(row) * (N >> 1) + n] = f32_to_bf16_bits(silu_mul_of_bf16(out[p][i], u[i]));
         }
       }
     }

@@ -524,7 +524,7 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
             const int c = 16 * t + (lane & 15);
             const int off = r * PITCH + (((c >> 3) ^ (r % CPR)) << 4) + ((c & 7) << 1);
             const int tt = part * TP + t;
-            *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul(acc[mt][tt][i], acc[mt][tt + H][i]));
+            *reinterpret_cast<uint16_t*>(ep + off) = f32_to_bf16_bits(silu_mul_of_bf16(acc[mt][tt][i], acc[mt][tt + H][i]));
           }
       store_rows(std::integral_constant<int, CPR>{}, o.col_w + 16 * TP * part);
     }

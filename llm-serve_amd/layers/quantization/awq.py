@@ -419,7 +419,8 @@ def awq_linear_silu_mul(inputs: torch.Tensor, packed_qweight: torch.Tensor, qzer
     """SiLU(g) * u over [g | u] = inputs @ W for a gate|up weight of width N (first N/2
     columns gate, last N/2 up, as MergedColumnParallelLinear loads them): the reference's
     ``SiluAndMul`` (activation.py:8-11) applied to ``awq_linear``'s output, computed in the
-    GEMM epilogue from the fp32 accumulators and rounded once to bf16.  Returns
+    GEMM epilogue: the fp32 accumulators rounded to bf16 as that output is, then SiLU(g) * u
+    in fp32, rounded once.  Returns
     [..., N/2]; N must be divisible by 128."""
     x, lead, k, n = _prepare_linear(inputs, packed_qweight, qzeros, scales, group_size)
     if n % 128:

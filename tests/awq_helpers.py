@@ -80,6 +80,36 @@ def rel_err_strict(y, r) -> float:
     return rel_err(y, r, floor=STRICT_FLOOR)
 
 
+def assert_silu_two_step(f, x, w, what=None) -> None:
+    """The fused SiLU(g) * u output f [M, N/2] against the reference's two steps over an fp32
+    product [g | u] = x @ w (w: the bf16 dequantized gate|up weight as fp32 [K, N]): the GEMM
+    output rounded to bf16, then SiLU(g) * u in fp32, rounded once.  Two GEMMs that sum in
+    different orders round g or u differently where the value lies next to a bf16 rounding
+    boundary, so: >= 99 % of f equals that two-step result bit for bit, and every element
+    lies within one bf16 last place of the range the two steps take over every g, u within
+    2^-16 (|x| @ |w|) of the fp32 product (summation-order differences are far smaller).
+    The product is monotone in each rounded factor on such a range (SiLU's minimum aside,
+    where it is flat), so the range comes from the four corners."""
+    gu = x.float() @ w
+    delta = (x.float().abs() @ w.abs()) * 2.0 ** -16
+    n2 = gu.shape[1] // 2
+
+    def two(sg, su):
+        g = (gu[:, :n2] + sg * delta[:, :n2]).to(torch.bfloat16).double()
+        u = (gu[:, n2:] + su * delta[:, n2:]).to(torch.bfloat16).double()
+        return torch.nn.functional.silu(g) * u
+
+    want = two(0.0, 0.0).to(torch.bfloat16)
+    corners = torch.stack([two(sg, su) for sg in (-1.0, 1.0) for su in (-1.0, 1.0)])
+    lo, hi = corners.min(0).values, corners.max(0).values
+    fd = f.double()
+    ulp = torch.exp2(torch.floor(torch.log2(fd.abs().clamp_min(2.0 ** -126))) - 7)
+    inside = (fd >= lo - ulp) & (fd <= hi + ulp)
+    same = (f.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+    assert same >= 0.99, (what, same)
+    assert bool(inside.all()), (what, int((~inside).sum()))
+
+
 def assert_gemm_close(y, r, what=None) -> None:
     """A plain GEMM output against an fp32/fp64-accumulated reference over the same bf16
     weights: both floors within GEMM_REL_TOL."""

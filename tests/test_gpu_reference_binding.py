@@ -11,7 +11,8 @@ import pytest
 import torch
 from torch import nn
 
-from awq_helpers import GEMM_REL_TOL, QWEN3_SHAPES, assert_gemm_close, awq_mod, random_awq_gpu, random_x_gpu, rel_err
+from awq_helpers import (QWEN3_SHAPES, assert_gemm_close, assert_silu_two_step, awq_mod, random_awq_gpu,
+                         random_x_gpu)
 
 pytestmark = pytest.mark.gpu
 
@@ -55,9 +56,8 @@ def test_stub_fused_entries(stub, gpu_lib):
     stub.process_weights_after_loading_hip(layer)
     m = 384
     x = random_x_gpu(m, k, seed=3)
-    gu = reference(x, qw, qz, s).double()
-    want = torch.nn.functional.silu(gu[:, : n // 2]) * gu[:, n // 2:]
-    assert rel_err(stub.awq_hip_gate_up_silu_mul(x, layer), want) <= GEMM_REL_TOL
+    assert_silu_two_step(stub.awq_hip_gate_up_silu_mul(x, layer), x,
+                         awq_mod().dequantize_awq_gemm(qw, qz, s, group_size=128).float(), "gate_up silu")
 
     class Norm:  # RMSNorm's weight and eps (layernorm.py:6-14)
         weight = (1 + 0.1 * random_x_gpu(1, k, seed=4)[0].float()).to(torch.bfloat16)

@@ -286,9 +286,8 @@ def test_two_layer_step_from_no_residual_matches_oracle(gpu_lib):
         xn2_bits, want_res2, _ = ora.add_rms_norm_ref(bits_of(a), res_bits, host["norm2"], EPS)
         assert np.array_equal(bits_of(res), want_res2), ("post-attention residual", li)
         gu = host["gate_up"]
-        want_x = ora.awq_gate_up_silu_mul_ref(xn2_bits, gu["qweight"], gu["qzeros"], gu["scales_bits"], 128,
-                                              round_intermediate=False)
-        assert rel_err(x, want_x) <= GEMM_REL_TOL, ("gate_up", li)
+        want_x = ora.awq_gate_up_silu_mul_ref(xn2_bits, gu["qweight"], gu["qzeros"], gu["scales_bits"], 128)
+        assert rel_err(x, want_x) <= 1.2e-2, ("gate_up", li)  # one intermediate ulp + rounding
         h = mods["down"](x)
         assert rel_err(h, gemm_ref(bits_of(x), host["down"])) <= GEMM_REL_TOL, ("down", li)
     assert torch.isfinite(h.float()).all()

@@ -1,29 +1,41 @@
 """GPU parity of the fused gate|up GEMM with SiLU * up in its epilogue (w4a16_gemm_silu_mul):
 the reference computes ``SiluAndMul()(gate_up_proj(x))`` (qwen3.py:126-130,
-activation.py:8-11) as two steps over a bf16 [M, 2 I] intermediate; the fused kernel keeps
-gate and up in fp32 and rounds once.
+activation.py:8-11) as two steps over a bf16 [M, 2 I] intermediate; the fused kernel
+rounds gate and up to bf16 from its fp32 accumulators as that layer output is rounded, and
+computes SiLU(g) * u in fp32 with one rounding of the result, as the reference's compiled
+SiluAndMul does.
 
 Two references, both from the oracle at small sizes (``awq_gate_up_silu_mul_ref``) and from
 torch fp32 on the GPU over the bit-exact dequantized weights at full Qwen3-8B sizes:
 
+* the reference's two steps (GEMM rounded to bf16, then SiLU * up): TWO_STEP_TOL = 1.2e-2
+  with the rms floor (assert_fused_close).  The two results round the same g and u except
+  where the GEMMs' different fp32 summation orders move a bf16 rounding of g or u: one last
+  place, at most 2^-7 of the value, plus the result's own rounding, at most 2^-8 -- 1.17e-2
+  (measured up to 1.04e-2 on such ties, 0.39e-2 elsewhere).  The stricter 1e-3 rms floor is
+  not applied: at a gate far below zero SiLU turns such a difference of g into a relative
+  change about |g| times larger, on outputs that are tiny;
 * the exact composition (fp64 GEMM, no intermediate rounding, fp64 SiLU * up): tolerance
-  max |y - r| / max(|r|, rms(r)) <= 1e-2 (GEMM_REL_TOL), the GEMM's;
-* the reference's two steps (GEMM rounded to bf16, then SiLU * up): tolerance 2e-2
-  (TWO_STEP_TOL).  The reference's own bf16 intermediate moves its result about 0.6-0.8e-2
-  from the exact value in this metric at these sizes (measured on the oracle), so a result
-  within 1e-2 of the exact value can lie up to about 1.8e-2 from the two-step one."""
+  2e-2 (EXACT_TOL).  The reference's own bf16 intermediate moves its result about
+  0.6-0.8e-2 from the exact value in this metric at these sizes (measured on the oracle)."""
 import importlib
 
 import numpy as np
 import pytest
 import torch
 
-from awq_helpers import (GEMM_REL_TOL, QWEN3_SHAPES, awq_mod, decode_config_accepted, random_awq_gpu, random_x_gpu,
-                         rel_err, to_gpu)
+from awq_helpers import (QWEN3_SHAPES, assert_silu_two_step, awq_mod, decode_config_accepted,
+                         random_awq_gpu, random_x_gpu, rel_err, to_gpu)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
-TWO_STEP_TOL = 2e-2
+TWO_STEP_TOL = 1.2e-2
+EXACT_TOL = 2e-2
+
+
+def assert_fused_close(y, r, what=None):
+    err = rel_err(y, r)
+    assert err <= TWO_STEP_TOL, (what, err)
 
 
 def fused(t, packed=None):
@@ -32,7 +44,7 @@ def fused(t, packed=None):
     return awq.awq_linear_silu_mul(t["x"], packed, t["qzeros"], t["scales"], group_size=128)
 
 
-def oracle_fused(p, round_intermediate=False):
+def oracle_fused(p, round_intermediate=True):
     return ora.awq_gate_up_silu_mul_ref(p["x_bits"], p["qweight"], p["qzeros"], p["scales_bits"], 128,
                                         round_intermediate=round_intermediate)
 
@@ -44,8 +56,8 @@ def test_fused_matches_oracle(gpu_lib, m):
     print(f"fused planner m={m} k={k} n={n}", flush=True)
     y = fused(to_gpu(p))
     assert y.shape == (m, n // 2) and y.dtype == torch.bfloat16
-    assert rel_err(y, oracle_fused(p)) <= GEMM_REL_TOL
-    assert rel_err(y, oracle_fused(p, round_intermediate=True)) <= TWO_STEP_TOL
+    assert_fused_close(y, oracle_fused(p), m)
+    assert rel_err(y, oracle_fused(p, round_intermediate=False)) <= EXACT_TOL
 
 
 FUSED_DECODE_CONFIGS = [(tn, w, d, s) for tn in (2, 4, 6) for w in (4, 8) for d in (1, 2, 4) for s in (1, 3, 8)]
@@ -71,8 +83,7 @@ def test_every_fused_decode_configuration(gpu_lib, m):
         y = torch.empty((m, n // 2), dtype=torch.bfloat16, device="cuda")
         gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 1, tn, waves, split, ws, p2=depth,
                             silu_mul=True)
-        err = rel_err(y, want)
-        assert err <= GEMM_REL_TOL, (tn, waves, depth, split, err)
+        assert_fused_close(y, want, (tn, waves, depth, split))
         if ws_bytes:
             assert int(torch.count_nonzero(ws[:65536])) == 0
         ran += 1
@@ -100,8 +111,7 @@ def test_every_fused_tile_configuration(gpu_lib, m, n):
             y = torch.full((m, n // 2), float("nan"), dtype=torch.bfloat16, device="cuda")
             gpu_lib.gemm_config(t["x"], packed, t["qzeros"], t["scales"], y, k, n, 2, wm, occ, split, ws, p2=shape,
                                 silu_mul=True)
-            err = rel_err(y, want)
-            assert err <= GEMM_REL_TOL, (wm, shape, occ, split, err)
+            assert_fused_close(y, want, (wm, shape, occ, split))
             if ws_bytes:
                 assert int(torch.count_nonzero(ws[:65536])) == 0
 
@@ -117,8 +127,8 @@ def torch_fused_reference(x, qw, qz, s):
 
 def test_full_gate_up_fused_matches_two_step_path(gpu_lib):
     """Qwen3-8B gate_up (4096 x 24576 -> 12288) at every decode M, the mixed-batch M and a
-    prefill chunk with outlier channels; also within TWO_STEP_TOL of SiLU * up applied to
-    the plain GEMM's bf16 output (the reference's two steps)."""
+    prefill chunk with outlier channels, against SiLU * up applied to the plain GEMM's bf16
+    output (the reference's two steps) and within EXACT_TOL of the unrounded composition."""
     k, n = QWEN3_SHAPES["gate_up"]
     qw, qz, s = random_awq_gpu(k, n, seed=31)
     awq = awq_mod()
@@ -128,10 +138,10 @@ def test_full_gate_up_fused_matches_two_step_path(gpu_lib):
         x = random_x_gpu(m, k, seed=40 + m, outliers=m >= 512)
         y = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
         assert y.shape == (m, n // 2)
-        assert rel_err(y, torch_fused_reference(x, qw, qz, s)) <= GEMM_REL_TOL, m
-        two_step = awq.awq_linear(x, packed, qz, s, group_size=128).float()
-        two_step = torch.nn.functional.silu(two_step[:, : n // 2]) * two_step[:, n // 2:]
-        assert rel_err(y, two_step) <= TWO_STEP_TOL, m
+        assert rel_err(y, torch_fused_reference(x, qw, qz, s)) <= EXACT_TOL, m
+        assert_silu_two_step(y, x, awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float(), m)
+        two_step = awq.awq_linear(x, packed, qz, s, group_size=128).float()  # over this library's GEMM
+        assert_fused_close(y, torch.nn.functional.silu(two_step[:, : n // 2]) * two_step[:, n // 2:], m)
 
 
 def test_fused_edge_cases(gpu_lib):
@@ -145,7 +155,8 @@ def test_fused_edge_cases(gpu_lib):
     x = random_x_gpu(6, k, seed=3).view(2, 3, k)
     y = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
     assert y.shape == (2, 3, n // 2)
-    assert rel_err(y.reshape(6, -1), torch_fused_reference(x.reshape(6, k), qw, qz, s)) <= GEMM_REL_TOL
+    two_step = awq.awq_linear(x.reshape(6, k), packed, qz, s, group_size=128).float()
+    assert_fused_close(y.reshape(6, -1), torch.nn.functional.silu(two_step[:, : n // 2]) * two_step[:, n // 2:])
     qw2, qz2, s2 = random_awq_gpu(k, 192, seed=4)
     with pytest.raises(ValueError, match="divisible by 128"):
         awq.awq_linear_silu_mul(random_x_gpu(2, k, seed=5), awq.repack_awq_qweight(qw2), qz2, s2, group_size=128)
@@ -173,9 +184,8 @@ def test_merged_layer_forward_silu_and_mul(gpu_lib):
     for m in (3, 100):
         x_bits = ora.f32_to_bf16_bits(np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))
         y = layer.forward_silu_and_mul(torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16).cuda())
-        want = ora.awq_gate_up_silu_mul_ref(x_bits, merged["qweight"], merged["qzeros"], merged["scales_bits"], 128,
-                                            round_intermediate=False)
-        assert rel_err(y, want) <= GEMM_REL_TOL, m
+        want = ora.awq_gate_up_silu_mul_ref(x_bits, merged["qweight"], merged["qzeros"], merged["scales_bits"], 128)
+        assert_fused_close(y, want, m)
     with torch.device("cuda"):
         uneven = linear.MergedColumnParallelLinear(k, [256, 128], quant_config=cfg)
     with pytest.raises(ValueError, match="two equal"):

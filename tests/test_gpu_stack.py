@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 import torch
 
-from awq_helpers import GEMM_REL_TOL, assert_gemm_close, awq_mod, random_awq_gpu, rel_err
+from awq_helpers import assert_gemm_close, assert_silu_two_step, awq_mod, random_awq_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -122,10 +122,7 @@ def test_chained_stack_matches_reference_and_graph_replay(stack, gpu_lib, m):
     for li, (layer, rec) in enumerate(zip(stack, record)):
         assert_gemm_close(rec["qkv"], rec["h0"].float() @ dequant(layer["qkv"]), ("qkv", li, m))
         check_residual(rec["h1"], residual_reference(rec["attn"], layer["o"], rec["h0"]), ("o", li, m))
-        gu = rec["h1"].float() @ dequant(layer["gate_up"])
-        g64, u64 = gu[:, :INTER].double(), gu[:, INTER:].double()
-        want_act = g64 * torch.sigmoid(g64) * u64
-        assert rel_err(rec["act"], want_act) <= GEMM_REL_TOL, ("gate_up+silu", li, m)
+        assert_silu_two_step(rec["act"], rec["h1"], dequant(layer["gate_up"]), ("gate_up+silu", li, m))
         check_residual(rec["h2"], residual_reference(rec["act"], layer["down"], rec["h1"]), ("down", li, m))
     # the magnitude stays in range through the chain
     rms = [float(r["h2"].float().pow(2).mean().sqrt()) for r in record]
