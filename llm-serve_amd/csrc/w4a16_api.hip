@@ -219,6 +219,30 @@ constexpr TileCand kNarrowTiles[] = {{8, 3, 128, 256, 0.955}, {6, 3, 96, 256, 0.
 constexpr TileCand kNarrow384Tiles[] = {{8, 8, 128, 512, 1.0}, {8, 11, 128, 384, 0.93}, {6, 8, 96, 512, 0.91},
                                         {6, 11, 96, 384, 0.89}, {6, 3, 96, 256, 0.87}, {8, 3, 128, 256, 0.86}};
 
+// Wide layers whose width is a multiple of 384 columns, for 256 < M <= 1024: 128 / 96 rows x
+// 512 / 384 / 256 columns, with efficiencies from whole rounds of the gate_up shape relative
+// to a 128 x 512 round (111 us at M = 2048): 128 x 384 0.94 (M = 1536 / 1024 / 512: 260 /
+// 181 / 90 us), 96 x 384 0.855 (M = 768 / 384: 146.5 / 72.8 us), 128 x 256 0.907 (M = 960:
+// 183.7 us), 96 x 256 0.815 (M = 768: 153.4 us).
+constexpr TileCand kWide384Tiles[] = {{8, 8, 128, 512, 1.0},    {8, 11, 128, 384, 0.94}, {6, 8, 96, 512, 0.91},
+                                      {6, 11, 96, 384, 0.855}, {8, 3, 128, 256, 0.907}, {6, 3, 96, 256, 0.815}};
+
+// The candidate that does the most useful work per round of 256 workgroups: its efficiency
+// times the M x N outputs over the rows x columns its rounds compute, so that rows padded
+// past M count against a tile (96-row tiles of a short chunk waste less than 128-row ones).
+// Ties go to the earlier tile.
+template <size_t C>
+GemmPlan most_useful_tile(int M, int N, const TileCand (&cands)[C]) {
+  const TileCand* best = &cands[0];
+  double best_score = 0.0;
+  for (const TileCand& c : cands) {
+    const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+    const double score = c.eff * M * N / (ceil_div(t, 256) * 256.0 * c.bm * c.bn);
+    if (score > best_score + 1e-9) best = &c, best_score = score;
+  }
+  return GemmPlan{W4A16_REGIME_TILE, best->wm, 2, best->shape, 1};
+}
+
 // The candidate whose grid fills its last round of 256 workgroups best, weighted by its
 // efficiency; ties go to the earlier (larger) tile.  Regime NONE when no candidate fills
 // half its last round.
@@ -250,8 +274,8 @@ GemmPlan best_filling_tile(int M, int N, const TileCand (&cands)[C]) {
 // (shape 3) when that grid alone has >= 144 workgroups, else 128 columns (shape 5, 2 K
 // slices), K split in two or more for long K while the grid is below 144 workgroups;
 // short-K narrow layers switch to 64-row tiles of 128 columns instead of splitting K.  From
-// sweeps of every tile configuration at M = 320 ... 1024.  `fused`: no layout with an odd
-// tile count per wave (the fused SiLU * up product pairs a wave's tiles).
+// sweeps of every tile configuration at M = 320 ... 1024.  `fused`: narrow layers leave out
+// the 384-column tiles (their fused form pairs waves; measured on wide layers only).
 GemmPlan plan_large(int M, int K, int N, bool fused) {
   const int G = K / w4a16::kGroup;
   // Plain GEMMs on widths that are multiples of 384 columns: 128 x 384 tiles (shape 11, 8
@@ -259,7 +283,12 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
   // us against 104.0 / 112.6 us), 64 x 384 tiles on QKV-width layers once 128 x 256 tiles
   // would fill a round (QKV M = 768 / 1024: 54.7 / 59.4 us against 60.5 / 61.1 us).
   const bool w384 = !fused && N % 384 == 0;
-  if (w384 && N >= 16384 && ceil_div(M, 128) * (N / 384) <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
+  // Wide layers of such widths, the fused product too (its 384-column waves pair gate and up
+  // waves), by useful work per round (gate_up M = 288 / 384 / 672 / 768 / 864 / 960: 66.5 /
+  // 72.8 / 135.0 / 146.5 / 163.1 / 174.2 us against 79.9 / 81.2 / 145.9 / 153.4 / 175.6 /
+  // 183.7 us by round fill; the fused gate_up M = 384 / 512 / 768 / 1024: 73.0 / 90.0 /
+  // 147.3 / 179.3 against 83.7 / 101.5 / 152.9 / 188.3 us).
+  if (N >= 16384 && N % 384 == 0) return most_useful_tile(M, N, kWide384Tiles);
   if (N >= 16384 && M < 384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   if (N >= 16384) {
     const GemmPlan p = best_filling_tile(M, N, kWideTiles);
@@ -307,7 +336,7 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
     const GemmPlan p = best_filling_tile(M, N, kNarrow384Tiles);
     if (p.regime == W4A16_REGIME_TILE) return p;
   }
-  if (!fused && N % 384 == 0 && N >= 16384 && t11 % 256 == 0 && t11 < 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
+  if (N % 384 == 0 && N >= 16384 && t11 % 256 == 0 && t11 < 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 11, 1};
   const int t9 = ceil_div(M, 128) * ceil_div(N, 512);
   if (N >= 16384 && t9 >= 1024) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 8, 1};
   // Otherwise the best-filling tile (above).  From sweeps at M = 1280 ... 4096: O and down
@@ -334,10 +363,11 @@ GemmPlan plan(int M, int K, int N, bool fused = false) {
 }
 
 // The fused SiLU(gate) * up product of a gate|up weight [K, N] runs the plain GEMM's plan,
-// except that a wave must hold whole gate/up tile pairs: the tile regime leaves out the
-// layouts with an odd tile count per wave, and in the decode regime an odd tile count tn
-// becomes 2 tn (measured best for tn = 3 at M = 3..8), or the largest even count below
-// that divides N / 16 and fits the registers (the LDS check may then split K further).
+// except where the pairing of gate and up values constrains it: narrow layers leave out
+// the 384-column tiles (with three tiles per wave the product pairs gate and up waves, which
+// the wide layers' rules take), and in the decode regime an odd tile count tn becomes 2 tn
+// (measured best for tn = 3 at M = 3..8), or the largest even count below that divides
+// N / 16 and fits the registers (the LDS check may then split K further).
 GemmPlan plan_silu_mul(int M, int K, int N) {
   GemmPlan p = plan(M, K, N, true);
   if (p.regime != W4A16_REGIME_DECODE || p.p0 % 2 == 0) return p;
@@ -944,11 +974,15 @@ int gemm_config_impl(const uint16_t* x, const int32_t* packed, const int32_t* qz
     if (p0 != 2 && p0 != 4 && p0 != 6 && p0 != 8) return fail(W4A16_ERR_ARG, "tile wm must be 2, 4, 6 or 8");
     if (p2 < 0 || p2 > w4a16::kTileShapeMax)
       return fail(W4A16_ERR_ARG, "tile shape code must be 0..%d", w4a16::kTileShapeMax);
-    if (silu_mul && w4a16::tile_shape(p2).tw % 2)
-      return fail(W4A16_ERR_ARG, "the fused SiLU * up product needs a tile wave layout with an even tile count");
+    // The fused product pairs a wave's gate and up tiles (even tile counts) or, with an odd
+    // count, two waves of one K slice along N.
+    const w4a16::TileShape ts = w4a16::tile_shape(p2);
+    const bool paired_waves = silu_mul && ts.tw % 2;
+    if (paired_waves && (ts.nwn % 2 || ts.nwm != 1 || ts.wk != 1))
+      return fail(W4A16_ERR_ARG, "the fused SiLU * up product cannot pair the waves of tile wave layout %d", p2);
     // A wave's output columns must lie wholly inside or wholly past the output width (true for
     // every layout of 32 or 64 columns per wave whenever N % 64 == 0).
-    const int wave_cols = (silu_mul ? 8 : 16) * w4a16::tile_shape(p2).tw;
+    const int wave_cols = (silu_mul && !paired_waves ? 8 : 16) * ts.tw;
     if ((silu_mul ? N / 2 : N) % wave_cols)
       return fail(W4A16_ERR_SHAPE, "tile wave layout %d needs an output width that is a multiple of %d (got %d)", p2,
                   wave_cols, silu_mul ? N / 2 : N);

@@ -133,8 +133,9 @@ __device__ __forceinline__ void issue_sz_stage(const BSources& src, uint8_t* sz,
 
 // LDS byte offsets, within a group's scale/zero stage, of the scale pair word and the zero
 // word holding the lane's column of each of the wave's tiles.  Plain: the wave's columns are
-// [16 TW wn, 16 TW (wn + 1)) of the block; fused: gate columns [8 TW wn, 8 TW (wn + 1)) of
-// range 0 and the same up columns of range 1.
+// [16 TW wn, 16 TW (wn + 1)) of the block; fused, even TW: gate columns [8 TW wn, 8 TW (wn + 1))
+// of range 0 and the same up columns of range 1; fused, odd TW: columns [16 TW v, 16 TW (v + 1))
+// of range 0 for the first half of the waves (v = wn) and of range 1 for the second.
 template <int TW, int BN>
 struct SzOffsets {
   uint32_t s[TW], z[TW];
@@ -143,7 +144,11 @@ struct SzOffsets {
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       int r, u;
-      if (act) {
+      if (act && TW % 2 == 1) {  // waves pair up: wn < NWN / 2 gate, the others up
+        constexpr int kHalfWaves = BN / (32 * TW);
+        r = wn >= kHalfWaves;
+        u = 16 * TW * (wn - r * kHalfWaves) + 16 * tt;
+      } else if (act) {
         r = tt >= TW / 2;
         u = 8 * TW * wn + 16 * (tt - r * (TW / 2));
       } else {
@@ -300,6 +305,81 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
+// The fused SiLU(gate) * up epilogue of wave layouts with an odd tile count (TW = 3): wave
+// v < NWG / 2 holds the gate values and wave v + NWG / 2 the up values of output columns
+// [col_w, col_w + 16 TW).  In row passes every wave rounds its values to bf16 into its own LDS
+// region (rows of 2 TW 16-byte chunks, chunk q of row r at (q + r) % (2 TW)); after a barrier
+// each gate wave reads both operands of a chunk, forms SiLU(g) * u in fp32 (g and u being the
+// bf16 layer outputs, as in the reference's two steps) and stores the rounded chunk.  Every
+// wave of the workgroup passes the barriers, those without columns too.
+template <int WM, int TW, int NWG, int S, int kStage, class StageFn>
+__device__ __forceinline__ void cross_silu_epilogue(const f32x4_t (&acc)[WM][TW], StageFn stage, const TileOut& o,
+                                                    int wave_in, int lane) {
+  constexpr int WR = 16 * WM;
+  constexpr int CPR = 2 * TW;  // 16-byte chunks per row
+  constexpr int PITCH = 16 * CPR;
+  // the fewest row passes (dividing WM) whose NWG regions fit the stages
+  constexpr int kP = [] {
+    for (int p = 1; p <= WM; ++p)
+      if (WM % p == 0 && (kStage / ((WR / p) * PITCH)) * S >= NWG) return p;
+    return 0;
+  }();
+  static_assert(kP > 0, "the paired epilogue's regions exceed the stages");
+  constexpr int MP = WM / kP;  // 16-row tiles per pass
+  constexpr int RP = 16 * MP;  // rows per pass
+  constexpr int kRegion = RP * PITCH;
+  constexpr int kPerStage = kStage / kRegion;
+  constexpr int kHalf = NWG / 2;
+  constexpr int kRowsPerRound = 64 / CPR;
+  // wave v's region, the stage chosen among compile-time addresses
+  auto region = [&](int v) -> uint8_t* {
+    uint8_t* r = stage(0) + (v % kPerStage) * kRegion;
+    static_for<(NWG + kPerStage - 1) / kPerStage>([&](auto i_tag) {
+      constexpr int i = decltype(i_tag)::value;
+      if (i > 0 && v / kPerStage == i) r = stage(i) + (v % kPerStage) * kRegion;
+    });
+    return r;
+  };
+  const bool gate = wave_in < kHalf;
+  uint8_t* own = region(wave_in);
+  uint8_t* partner = region(gate ? wave_in + kHalf : wave_in);
+#pragma unroll
+  for (int part = 0; part < kP; ++part) {
+    if (o.active) {
+#pragma unroll
+      for (int ml = 0; ml < MP; ++ml)
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 16 * ml + 4 * (lane >> 4) + i;
+            const int c = 16 * t + (lane & 15);
+            const int off = r * PITCH + ((((c >> 3) + r) % CPR) << 4) + ((c & 7) << 1);
+            *reinterpret_cast<uint16_t*>(own + off) = f32_to_bf16_bits(acc[part * MP + ml][t][i]);
+          }
+    }
+    __syncthreads();
+    if (gate && o.active) {
+#pragma unroll 4
+      for (int round = 0; round < (RP + kRowsPerRound - 1) / kRowsPerRound; ++round) {
+        const int r = kRowsPerRound * round + lane / CPR;
+        const int q = lane % CPR;
+        const int row = o.row_w + RP * part + r;
+        if (lane < kRowsPerRound * CPR && r < RP && row < o.M) {
+          const int pos = r * PITCH + (((q + r) % CPR) << 4);
+          float g[8], u[8];
+          unpack_bf16x8(*reinterpret_cast<const uint4*>(own + pos), g);
+          unpack_bf16x8(*reinterpret_cast<const uint4*>(partner + pos), u);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) g[k] = silu_mul(g[k], u[k]);
+          *reinterpret_cast<uint4*>(o.y + static_cast<size_t>(row) * o.n_out + o.col_w + 8 * q) = pack_bf16x8(g);
+        }
+      }
+    }
+    __syncthreads();  // the regions are read before the next pass writes them
+  }
+}
+
 // After the K loop: the sum of the workgroup's K slices (WK > 1), the split-K exchange
 // between workgroups (split > 1) and the epilogue.  stage(i), i < S, is LDS region i of
 // kStage bytes; all of them are free here.  Every wave of the workgroup calls this (the
@@ -401,6 +481,12 @@ __device__ __forceinline__ void finish_tile(f32x4_t (&acc)[WM][TW], StageFn stag
     if (threadIdx.x == 0) rearm(&counters[tile]);
   }
 
+  if constexpr (TW % 2 == 1) {
+    if (o.act) {  // uniform: waves paired along N (WK == 1)
+      cross_silu_epilogue<WM, TW, NWG, S, kStage>(acc, stage, o, wave_in, lane);
+      return;
+    }
+  }
   if (!o.active || wk != 0) return;
   // Epilogue (slice 0): bf16 through LDS (row-major 16 WM rows x the wave's output columns:
   // rows of CPR 16-byte chunks swizzled by row), then 16-byte coalesced stores.  The stages

@@ -133,15 +133,22 @@ __global__ __launch_bounds__(64 * NWM * NWN * WK, OCC) void tile_kernel(const ui
   const int g_end = (G * (sidx + 1)) / split;
   const int row0 = mbk * BM;
   // Plain: the wave computes output columns [col_w, col_w + 16 TW) = layout tiles t0 + tt.
-  // Fused SiLU(gate) * up (up_tiles = N / 32): output columns [col_w, col_w + 8 TW) of the
-  // [M, N / 2] result, from gate tiles t0 + tt and up tiles t0 + up_tiles + tt, tt < TW / 2.
-  // The fused product pairs the two halves of a wave's tiles: odd TW runs the plain GEMM only
-  // (the API rejects the fused call for it).
+  // Fused SiLU(gate) * up (up_tiles = N / 32), even TW: output columns [col_w, col_w + 8 TW)
+  // of the [M, N / 2] result, from gate tiles t0 + tt and up tiles t0 + up_tiles + tt,
+  // tt < TW / 2 -- the two halves of the wave's tiles.  Odd TW pairs waves instead: wave
+  // wn < NWN / 2 holds the gate tiles t0 .. t0 + TW - 1 of output columns
+  // [col_w, col_w + 16 TW) and wave wn + NWN / 2 the up tiles of the same columns; the
+  // epilogue meets them in LDS.
+  constexpr bool kCross = TW % 2 == 1;
+  static_assert(!kCross || (NWN % 2 == 0 && NWM == 1 && WK == 1), "waves pair up along N in one slice");
   const bool act = up_tiles != 0;
+  const bool up_wave = kCross && act && wn >= NWN / 2;
+  const int gw = up_wave ? wn - NWN / 2 : wn;
   const int n_out = act ? N / 2 : N;
-  const int col_w = act ? nbk * (BN / 2) + 8 * TW * wn : nbk * BN + 16 * TW * wn;  // first output column
-  const int t0 = col_w / kTileCols;
-  const int dt = act ? up_tiles - TW / 2 : 0;
+  const int col_w = !act ? nbk * BN + 16 * TW * wn
+                  : kCross ? nbk * (BN / 2) + 16 * TW * gw : nbk * (BN / 2) + 8 * TW * wn;  // first output column
+  const int t0 = col_w / kTileCols + (up_wave ? up_tiles : 0);
+  const int dt = act && !kCross ? up_tiles - TW / 2 : 0;
   const bool active = col_w < n_out;  // wave-uniform (n_out % 64 == 0): the last n-block may be partly past it
   // The workgroup's two column ranges of BN / 2 (scale and zero staging).
   const int cs0 = act ? nbk * (BN / 2) : nbk * BN;

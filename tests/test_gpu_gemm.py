@@ -262,7 +262,8 @@ def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
                                      ("o", 31), ("o", 32), ("o", 33), ("qkv", 33), ("down", 31), ("down", 48),
                                      ("down", 33), ("down", 257), ("qkv", 257),
                                      ("gate_up", 160), ("qkv", 160), ("o", 160), ("down", 192), ("o", 640),
-                                     ("down", 640), ("qkv", 704), ("down", 896), ("gate_up", 640), ("down", 4)])
+                                     ("down", 640), ("qkv", 704), ("down", 896), ("gate_up", 640), ("down", 4),
+                                     ("gate_up", 288), ("gate_up", 864)])
 def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
     (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundary
@@ -270,8 +271,9 @@ def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     (M = 257), the mid-range row blocks that follow M (96 x 256 tiles on gate_up, 32-row
     tiles on QKV / O, 64-row tiles split in K on down at M = 160 / 192), the plans above M =
     512 (96 x 256 tiles with K in two on O / down at 640, the best-filling narrow and wide
-    tiles at QKV 704, gate_up 640, down 896 with 128 x 256 tiles and K in two) and the long-K
-    decode split at M = 4, at full shapes."""
+    tiles at QKV 704, gate_up 640, down 896 with 128 x 256 tiles and K in two), the 384-column
+    tiles of 96 and 128 rows the wide layers take by useful work per round (gate_up M = 288,
+    864) and the long-K decode split at M = 4, at full shapes."""
     k, n = QWEN3_SHAPES[shape]
     qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
     packed = awq_mod().repack_awq_qweight(qw)

@@ -92,19 +92,26 @@ def test_every_fused_decode_configuration(gpu_lib, m):
 
 TILE_KERNELS = [(4, 1, 1), (4, 1, 2), (8, 1, 1), (4, 2, 2), (4, 3, 2), (8, 3, 2), (2, 4, 2), (4, 4, 2), (2, 5, 2),
                 (4, 5, 2), (8, 5, 2), (4, 6, 1), (8, 6, 1), (2, 7, 1), (4, 7, 1), (8, 8, 2),
-                (4, 9, 3), (2, 9, 3), (4, 10, 3), (6, 3, 2), (6, 8, 2)]
+                (4, 9, 3), (2, 9, 3), (4, 10, 3), (6, 3, 2), (6, 8, 2), (8, 11, 2), (4, 11, 2), (6, 11, 2)]
+# shape 11 (three tiles per wave) pairs waves along N: the N / 2 outputs must be a multiple of
+# a wave's 48 columns
+PAIRED_WAVE_COLS = {11: 48}
 
 
-@pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 384), (513, 256)])
+@pytest.mark.parametrize("m,n", [(65, 512), (200, 768), (300, 384), (513, 256), (200, 1152)])
 def test_every_fused_tile_configuration(gpu_lib, m, n):
     """Every compiled tile kernel and split in fused mode: partial m-blocks, n-blocks partly
-    past the N / 2 output columns (N = 384: 192 outputs), uneven K splits."""
+    past the N / 2 output columns (N = 384: 192 outputs), uneven K splits; the 384-column
+    layout that pairs gate and up waves at N = 384, 768 and 1152 (one to three column
+    blocks; with N % 128 == 0 its 48-column waves always lie inside the outputs)."""
     k = 1024
     p = ora.make_problem(seed=700 + m, m=m, k=k, n=n)
     t = to_gpu(p)
     packed = awq_mod().repack_awq_qweight(t["qweight"])
     want = oracle_fused(p)
     for wm, shape, occ in TILE_KERNELS:
+        if (n // 2) % PAIRED_WAVE_COLS.get(shape, 1):
+            continue  # rejected by the library
         for split in (1, 2, 3):
             ws_bytes = gpu_lib.workspace_bytes_config(m, n, 2, wm, split)
             ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
