@@ -289,6 +289,24 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
   // 183.7 us by round fill; the fused gate_up M = 384 / 512 / 768 / 1024: 73.0 / 90.0 /
   // 147.3 / 179.3 against 83.7 / 101.5 / 152.9 / 188.3 us).
   if (N >= 16384 && N % 384 == 0) return most_useful_tile(M, N, kWide384Tiles);
+  // Narrow layers just above M = 256: 64-row tiles, five row blocks (320 rows computed
+  // instead of three 128-row blocks' 384), the width chosen for a grid of 192 .. 256: long K
+  // 64 x 192 tiles with K in two (down M = 272 / 320: 46.9 / 47.0 against 51.3 / 51.5 us),
+  // else 64 x 128 (QKV M = 272 / 320: 24.2 / 24.8 against 32.8 / 33.1 us) or 64 x 96 tiles
+  // (O: 20.1 / 20.5 against 23.1 / 23.0 us); QKV-width layers then keep 64 x 192 tiles up to
+  // M = 448 (M = 384 / 448: 30.3 / 32.2 against 33.6 / 33.7 us).
+  if (N < 16384 && M <= 320) {
+    const int mb = ceil_div(M, 64);
+    if (K >= 8192 && mb * ceil_div(N, 192) * 2 <= 256) return GemmPlan{W4A16_REGIME_TILE, 4, 3, 10, 2};
+    if (K < 8192 && N % 128 == 0 && mb * (N / 128) >= 192 && mb * (N / 128) <= 256)
+      return GemmPlan{W4A16_REGIME_TILE, 4, 2, 5, 1};
+    if (K < 8192 && mb * ceil_div(N, 96) >= 192 && mb * ceil_div(N, 96) <= 256)
+      return GemmPlan{W4A16_REGIME_TILE, 4, 3, 9, 1};
+  }
+  if (N < 16384 && K < 8192 && N % 192 == 0) {
+    const int t10 = ceil_div(M, 64) * (N / 192);
+    if (t10 >= 192 && t10 < 256) return GemmPlan{W4A16_REGIME_TILE, 4, 3, 10, 1};
+  }
   if (N >= 16384 && M < 384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   if (N >= 16384) {
     const GemmPlan p = best_filling_tile(M, N, kWideTiles);
