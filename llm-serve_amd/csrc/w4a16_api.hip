@@ -293,8 +293,11 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
   // instead of three 128-row blocks' 384), the width chosen for a grid of 192 .. 256: long K
   // 64 x 192 tiles with K in two (down M = 272 / 320: 46.9 / 47.0 against 51.3 / 51.5 us),
   // else 64 x 128 (QKV M = 272 / 320: 24.2 / 24.8 against 32.8 / 33.1 us) or 64 x 96 tiles
-  // (O: 20.1 / 20.5 against 23.1 / 23.0 us); QKV-width layers then keep 64 x 192 tiles up to
-  // M = 448 (M = 384 / 448: 30.3 / 32.2 against 33.6 / 33.7 us).
+  // (O: 20.1 / 20.5 against 23.1 / 23.0 us).  Above that, for short K, 64 x 192 tiles while
+  // their grid fills 192 .. 255 workgroups of a round (QKV M = 336 .. 448: 30.3 / 32.2 against
+  // 33.6 / 33.7 us at M = 384 / 448; O M = 513 .. 704: 29.5 / 31.3 against 31.3 / 35.0 us at
+  // M = 528 / 704), then 128 x 128 tiles while theirs fills 192 .. 256 (O M = 736 / 768: 33.7 /
+  // 33.8 against 34.7 / 35.2 us).
   if (N < 16384 && M <= 320) {
     const int mb = ceil_div(M, 64);
     if (K >= 8192 && mb * ceil_div(N, 192) * 2 <= 256) return GemmPlan{W4A16_REGIME_TILE, 4, 3, 10, 2};
@@ -303,9 +306,11 @@ GemmPlan plan_large(int M, int K, int N, bool fused) {
     if (K < 8192 && mb * ceil_div(N, 96) >= 192 && mb * ceil_div(N, 96) <= 256)
       return GemmPlan{W4A16_REGIME_TILE, 4, 3, 9, 1};
   }
-  if (N < 16384 && K < 8192 && N % 192 == 0) {
-    const int t10 = ceil_div(M, 64) * (N / 192);
+  if (N < 16384 && K < 8192) {
+    const int t10 = ceil_div(M, 64) * ceil_div(N, 192);
     if (t10 >= 192 && t10 < 256) return GemmPlan{W4A16_REGIME_TILE, 4, 3, 10, 1};
+    const int t5 = ceil_div(M, 128) * ceil_div(N, 128);
+    if (t5 >= 192 && t5 <= 256) return GemmPlan{W4A16_REGIME_TILE, 8, 2, 5, 1};
   }
   if (N >= 16384 && M < 384) return GemmPlan{W4A16_REGIME_TILE, 4, 2, 1, 1};
   if (N >= 16384) {

@@ -264,19 +264,20 @@ def test_full_qwen3_shapes_verify_and_stack_batches(gpu_lib, shape, m):
                                      ("gate_up", 160), ("qkv", 160), ("o", 160), ("down", 192), ("o", 640),
                                      ("down", 640), ("qkv", 704), ("down", 896), ("gate_up", 640), ("down", 4),
                                      ("gate_up", 288), ("gate_up", 864), ("qkv", 288), ("o", 288), ("down", 288),
-                                     ("qkv", 400)])
+                                     ("qkv", 400), ("o", 513), ("o", 705)])
 def test_full_qwen3_shapes_at_planner_boundaries(gpu_lib, shape, m):
     """Chunk sizes where the planner picks 128-row tiles with K split to fill one round
-    (QKV / O / down at M = 768, gate_up at 256, down at 384), the decode / tile boundary
+    (QKV / down at M = 768, gate_up at 256, down at 384), the decode / tile boundary
     (decode below M = 32, the tile kernel's 32- and 64-row plans above), the end of the mid-range plans
     (M = 257), the mid-range row blocks that follow M (96 x 256 tiles on gate_up, 32-row
     tiles on QKV / O, 64-row tiles split in K on down at M = 160 / 192), the plans above M =
-    512 (96 x 256 tiles with K in two on O / down at 640, the best-filling narrow and wide
+    512 (96 x 256 tiles with K in two on down at 640, the best-filling narrow and wide
     tiles at QKV 704, gate_up 640, down 896 with 128 x 256 tiles and K in two), the 384-column
     tiles of 96 and 128 rows the wide layers take by useful work per round (gate_up M = 288,
     864), the 64-row tiles of narrow layers just above M = 256 (QKV 64 x 128, O 64 x 96, down
-    64 x 192 with K in two at M = 288; QKV 64 x 192 at M = 400) and the long-K decode split
-    at M = 4, at full shapes."""
+    64 x 192 with K in two at M = 288; QKV 64 x 192 at M = 400), O's 64 x 192 tiles at M =
+    513 .. 704 (513, 640) and 128 x 128 tiles without a K split at 705 .. 768 (705, 768) and
+    the long-K decode split at M = 4, at full shapes."""
     k, n = QWEN3_SHAPES[shape]
     qw, qz, s = random_awq_gpu(k, n, seed=14 + m)
     packed = awq_mod().repack_awq_qweight(qw)
