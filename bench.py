@@ -68,7 +68,7 @@ Also reported (not part of `value`):
     (O and down through w4a16_gemm_residual_stats, gate|up and QKV through
     w4a16_gemm_rmsnorm_stats) -- 144 GEMM launches and no norm launch after layer 0's;
     `policy_step_us`: the step of the per-M choice (the prologue at M = 1, the split form
-    at M = 2..8, the norm kernel above);
+    at M = 2..4, the norm kernel above);
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
     in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
 
@@ -473,10 +473,10 @@ def layer_stack_normed(lib, dev, stream, reps: int, layers) -> dict:
         ms_s = time_graph(step_stats, stream, reps)
         out[f"M={m}"]["norm_stats"] = {"step_us": round(ms_s * 1e3, 1), "us_per_token": round(ms_s * 1e3 / m, 2)}
     # The per-M choice a model makes (the in-kernel prologue at M = 1, the split form at
-    # M = 2..8, the norm kernel above): the step time of that choice.
+    # M = 2..4, the norm kernel above): the step time of that choice.
     for key, v in out.items():
         m = int(key.split("=")[1])
-        v["policy_step_us"] = v["norm_stats"]["step_us"] if 2 <= m <= 8 and "norm_stats" in v else v["step_us"]
+        v["policy_step_us"] = v["norm_stats"]["step_us"] if 2 <= m <= 4 and "norm_stats" in v else v["step_us"]
     return out
 
 

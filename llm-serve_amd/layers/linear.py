@@ -256,10 +256,11 @@ class RowParallelLinear(LinearBase):
 
     def forward_residual_stats(self, x: torch.Tensor, residual: torch.Tensor,
                                residual_out: torch.Tensor | None = None):
-        """At decode sizes (packed M <= 8): this projection, the residual add of the next
-        add_rms_forward and that norm's row statistics in the GEMM epilogue, so that the norm
-        needs no launch of its own; returns ``(NormInput, new residual)`` for the next
-        layer's forward_rmsnorm_stats.  ``residual_out`` may be ``residual`` (in place)."""
+        """At decode sizes (packed M <= 8; faster than a separate norm launch up to M = 4):
+        this projection, the residual add of the next add_rms_forward and that norm's row
+        statistics in the GEMM epilogue, so that the norm needs no launch of its own; returns
+        ``(NormInput, new residual)`` for the next layer's forward_rmsnorm_stats.
+        ``residual_out`` may be ``residual`` (in place)."""
         if self.quant_method is None or not hasattr(self.quant_method, "apply_residual_stats"):
             raise ValueError("the fused RMSNorm statistics are implemented for the AWQ HIP backend only")
         if self.tp_size > 1:
