@@ -34,8 +34,12 @@ def ulp_diff(a_bits, b_bits):
 
 
 @pytest.mark.parametrize("with_res", [True, False])
-@pytest.mark.parametrize("m,k", [(1, 4096), (5, 4096), (64, 128), (300, 136), (3, 16384), (17, 5120), (2048, 4096)])
+@pytest.mark.parametrize("m,k", [(1, 4096), (5, 4096), (64, 128), (300, 136), (3, 16384), (17, 5120), (2048, 4096),
+                                 (9, 1024), (1, 520), (2, 2056), (4, 8200)])
 def test_add_rmsnorm_matches_oracle(gpu_lib, m, k, with_res):
+    """Short rows (K <= 512: lanes of one wave per row) and whole-workgroup rows of one, two,
+    four and eight 16-byte chunks per lane, full (K = 1024, 4096, 16384) and with the last
+    round of chunks partly past the row (K = 520, 2056, 5120, 8200)."""
     x_bits = rand_bits((m, k), seed=m * 7 + k, scale=2.0)
     r_bits = rand_bits((m, k), seed=m * 11 + k, scale=3.0) if with_res else None
     w_bits = rand_bits((k,), seed=k, scale=0.2, offset=1.0)
@@ -69,9 +73,11 @@ def test_add_rmsnorm_special_rows(gpu_lib):
     assert np.allclose(got[3], 2 * x4 / np.sqrt(x4 * x4 + EPS), rtol=2 ** -8)
 
 
-def test_add_rmsnorm_in_place(gpu_lib):
-    """residual_out may be the residual itself and the normalised output may replace x."""
-    m, k = 33, 4096
+@pytest.mark.parametrize("k", [4096, 136])
+def test_add_rmsnorm_in_place(gpu_lib, k):
+    """residual_out may be the residual itself and the normalised output may replace x
+    (whole-workgroup rows and short rows)."""
+    m = 33
     awq = awq_mod()
     x = bf16_from_bits(rand_bits((m, k), seed=1))
     res = bf16_from_bits(rand_bits((m, k), seed=2))
@@ -224,6 +230,29 @@ def test_head_norms_on_strided_qkv_views(gpu_lib, tokens):
         assert d.max() <= 2 and (d == 0).mean() > 0.99, (d.max(), (d == 0).mean())
         assert torch.equal(out.view(torch.int16), norm(view.contiguous()).view(torch.int16))
     assert np.array_equal(bits_of(qkv), qkv_bits)  # the input is not modified
+
+
+def test_strided_rows_longer_than_512(gpu_lib):
+    """The strided form over rows that take a whole workgroup each: 1024-wide "heads" of a
+    [tokens, 6 * 1024] tensor viewed as [tokens, 4, 1024] (row stride 6 * 1024 between
+    tokens, 1024 within), against the oracle and against a contiguous copy."""
+    layernorm = importlib.import_module("llm-serve_amd.layers.layernorm")
+    tokens, heads, head = 5, 4, 1024
+    buf_bits = rand_bits((tokens, 6 * head), seed=21, scale=2.0)
+    buf = bf16_from_bits(buf_bits)
+    view = buf[:, head: head + heads * head].view(tokens, heads, head)
+    assert not view.is_contiguous()
+    with torch.device("cuda"):
+        norm = layernorm.RMSNorm(head, eps=EPS)
+    w_bits = rand_bits((head,), seed=22, scale=0.2, offset=1.0)
+    norm.weight.copy_(bf16_from_bits(w_bits))
+    out = norm(view)
+    rows = buf_bits[:, head: head + heads * head].reshape(tokens * heads, head)
+    want, _, _ = ora.add_rms_norm_ref(rows, None, w_bits, EPS)
+    d = ulp_diff(bits_of(out).reshape(tokens * heads, head), want)
+    assert d.max() <= 2 and (d == 0).mean() > 0.99, (d.max(), (d == 0).mean())
+    assert torch.equal(out.view(torch.int16), norm(view.contiguous()).view(torch.int16))
+    assert np.array_equal(bits_of(buf), buf_bits)
 
 
 def test_two_layer_step_from_no_residual_matches_oracle(gpu_lib):
