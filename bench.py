@@ -70,7 +70,12 @@ Also reported (not part of `value`):
     `policy_step_us`: the step of the per-M choice (the prologue at M = 1, the split form
     at M = 2..4, the norm kernel above);
   * rmsnorm_prologue: the norm alone, the QKV / gate|up(+SiLU * up) GEMM alone and the two
-    in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048}.
+    in one w4a16_gemm_rmsnorm call at M in {1, 16, 2048};
+  * tp8_shards: one GPU's share of each projection split eight ways (QKV and gate_up
+    column-parallel, O and down row-parallel: 4096x768, 512x4096, 4096x3072, 1536x4096) at
+    M in {1, 16, 64, 2048}, rotating weights as above; `vs_full_over_8` = (the full
+    shape's time in this run / 8) / the shard's time, 1.0 for a GEMM that splits perfectly
+    (the row-parallel all-reduce is not included).
 
 Profiling mode: `--profile-point SHAPE:M` runs one point without graphs (a 256 MiB copy
 for counter calibration, then --steps launches over rotating weights) so that
@@ -98,6 +103,8 @@ SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "dow
 DECODE_M = (1, 4, 8, 16)
 EXTRA_DECODE_M = (32, 64)
 PREFILL_M = 2048
+TP8_SHAPES = {"qkv": (4096, 768), "o": (512, 4096), "gate_up": (4096, 3072), "down": (1536, 4096)}
+TP8_M = (1, 16, 64, 2048)
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 CACHE_BYTES = 256 * 2 ** 20
@@ -695,6 +702,38 @@ def fused_gate_up(lib, dev, stream, reps: int) -> dict:
     return out
 
 
+def tp8_shards(lib, dev, stream, steps: int, full_us: dict) -> dict:
+    """Each projection's one-GPU share under an eight-way tensor-parallel split, timed like
+    the decode points (rotating weight copies beyond the Infinity Cache; two copies at
+    M = 2048), against the full shape's time from the same run divided by eight."""
+    out = {}
+    for si, (name, (k, n)) in enumerate(TP8_SHAPES.items()):
+        copies = max(2, -(-(2 * CACHE_BYTES) // weight_bytes(k, n)))
+        weights = make_weights(k, n, copies, dev, 700 + si)
+        pts = []
+        for m in TP8_M:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(800 + 10 * si + m)
+            x = torch.randn((m, k), device=dev, generator=gen).to(torch.bfloat16)
+            pts.append(Point(lib, name, m, k, n, weights if m < PREFILL_M else weights[:2], x))
+        per_launch, _ = time_points(pts, stream, steps, 1)
+        res = {"K": k, "N": n}
+        for p in pts:
+            ms = per_launch[id(p)]
+            entry = {"us": round(ms * 1e3, 3), "split": p.split}
+            if p.m < PREFILL_M:
+                entry["GB/s"] = round(algorithmic_bytes(p.m, k, n) / (ms * 1e-3) / 1e9, 1)
+            else:
+                entry["TFLOP/s"] = round(2 * p.m * n * k / (ms * 1e-3) / 1e12, 1)
+            full = full_us.get((name, p.m))
+            if full:
+                entry["vs_full_over_8"] = round(full / 8 / (ms * 1e3), 3)
+            res[f"M={p.m}"] = entry
+        out[name] = res
+        del pts, weights
+    return out
+
+
 def quantize_throughput(lib, dev, stream, reps: int) -> dict:
     """w4a16_quantize over a [24576, 4096] bf16 weight (the gate_up projection's float
     weight): bytes = 2 per weight read + 0.5 written + scales and zeros."""
@@ -877,7 +916,7 @@ def main(argv=None):
                 print(f"prefill {p.name:8s} M={p.m} {ms * 1e3:9.2f} us {tf:8.1f} TFLOP/s", file=sys.stderr)
         del pts
 
-    mixed = stack = stack_chained = stack_normed = ceilings = fused = quant = norm = None
+    mixed = stack = stack_chained = stack_normed = ceilings = fused = quant = norm = tp8 = None
     if not args.no_extra:
         mixed = mixed_batch(lib, dev, stream, max(3, args.steps // 4))
         stack, stack_chained, stack_normed = layer_stack(lib, dev, stream, max(2, args.steps // 10))
@@ -885,6 +924,9 @@ def main(argv=None):
         fused = fused_gate_up(lib, dev, stream, max(3, args.steps // 4))
         quant = quantize_throughput(lib, dev, stream, max(3, args.steps // 4))
         norm = norm_prologue(lib, dev, stream, max(3, args.steps // 4))
+        full_us = {(pt["shape"], pt["M"]): pt["us"] for pt in points_out}
+        full_us.update({(name, PREFILL_M): v["us"] for name, v in (prefill or {}).items()})
+        tp8 = tp8_shards(lib, dev, stream, max(3, args.steps // 4), full_us)
         if args.details:
             print(f"mixed M={MIXED_M}: {json.dumps(mixed)}", file=sys.stderr)
             print(f"stack36: {json.dumps(stack)}", file=sys.stderr)
@@ -894,6 +936,7 @@ def main(argv=None):
             print(f"quantize: {json.dumps(quant)}", file=sys.stderr)
             print(f"stack36_normed: {json.dumps(stack_normed)}", file=sys.stderr)
             print(f"rmsnorm_prologue: {json.dumps(norm)}", file=sys.stderr)
+            print(f"tp8_shards: {json.dumps(tp8)}", file=sys.stderr)
 
     by_shape = (ceilings or {}).get("read_per_launch_by_shape", {})
     for pt in points_out:  # each decode point against a plain read of its shape's weight bytes
@@ -931,6 +974,7 @@ def main(argv=None):
         "fused_gate_up": fused,
         "quantize": quant,
         "rmsnorm_prologue": norm,
+        "tp8_shards": tp8,
         "points": points_out,
     }
     print(json.dumps(result))

@@ -89,6 +89,11 @@ int tile_bn(const GemmPlan& p) {
 //    4.96 / 5.37 us with 8 --, one group each in flight at M = 3, 4 -- O M = 3 / 4: 4.97 /
 //    5.05 against 5.13 / 5.19 us with two --, from M = 5 on 4 waves with four groups each in
 //    flight), then 64 columns with K in four;
+//  * narrow layers below the tuned sizes (the tensor-parallel shards of these layers): fewer
+//    than 128 column tiles split K in four from M = 9 on (QKV / 8 = 4096 x 768 at M = 16 /
+//    24: 6.0 / 6.4 us against 6.7 / 7.9 us unsplit), fewer than 16 groups stay unsplit in
+//    one-tile workgroups of 4 waves (O / 8 = 512 x 4096 at M = 24: 3.9 against 7.2 us);
+//    no workgroup has more waves than groups, nor a wave a deeper ring than its groups;
 //  * narrow layers with long K: 16 columns at M = 1 (12 waves, four groups each in flight:
 //    down 8.3 - 8.6 us against 8.7 - 8.9 us with 8), 32 with K in two up to M = 8 (down
 //    M = 4: 9.96 us against 10.27 us with K in four), then 64 columns with K in four.
@@ -110,12 +115,22 @@ GemmPlan plan_decode(int M, int K, int N) {
     if (M <= 4) { tn = 1; waves = 12; if (M > 2) depth = 1; }
     else if (M <= 16) { tn = 1; waves = 4; depth = 4; }
     else { tn = 4; depth = 1; split = 4; }
+    // Narrow layers smaller than the tuned shapes (tensor-parallel shards and the like):
+    // fewer than 128 column tiles split K in four from M = 9 on, so that the grid still
+    // covers the CUs; fewer than 16 groups keep one-tile workgroups of 4 waves unsplit.
+    if (M > 8 && T < 128 && G >= 16) { tn = 1; waves = 4; depth = 2; split = 4; }
+    else if (M > 16 && G < 16) { tn = 1; waves = 4; depth = 2; split = 1; }
   } else {
     if (M <= 1) { tn = 1; depth = 4; waves = 12; }
     else if (M <= 8) { tn = 2; split = 2; }
     else { tn = 4; depth = 1; split = 4; if (M > 32) waves = 4; }
   }
   if (split > G) split = G;
+  // No more waves than a workgroup has groups (at least one per SIMD), and no deeper ring
+  // than a wave has groups.
+  const int per_wg = ceil_div(G, split);
+  while (waves > 4 && waves > per_wg) waves -= 4;
+  while (depth > 1 && depth > ceil_div(per_wg, waves)) depth /= 2;
   const bool xl = w4a16::decode_stages_x(M, K, split);
   // Other shapes: the widest tile count <= tn that divides N / 16 and fits the registers.
   while (depth > 1 && !w4a16::decode_config_fits(MB, tn, depth, xl)) depth /= 2;
@@ -127,6 +142,46 @@ GemmPlan plan_decode(int M, int K, int N) {
          split < G)
     split = split * 2 > G ? G : split * 2;
   return GemmPlan{W4A16_REGIME_DECODE, tn, waves, depth, split};
+}
+
+// Tile plans for layers narrower (N < 4096) or shorter (K < 4096) than the shapes the rules
+// below were tuned on -- tensor-parallel shards and small models -- from a cost model: one
+// round of workgroups takes alpha + beta * K / 1024 us per tile (least-squares fits over
+// sweeps of the Qwen3-8B layers split eight ways, 4096 x 768, 512 x 4096, 4096 x 3072 and
+// 1536 x 4096, at M = 160 .. 2048; every fit within 6 %), and a plan costs its rounds of 256
+// workgroups times that.  Over those sweeps the model's choice is within 1 % of the best
+// configuration at M > 128 (533.9 against 628.8 us in total for the rules below) where its
+// grid has at least 144 workgroups; below that, K split over the same tile fills the grid
+// (QKV / 8 at M = 160 .. 320: 8.7 - 9.4 us, within 1 % of the best configuration).  Used up
+// to M = 2048; longer chunks, which take several rounds of 512-column tiles, keep the rules.
+struct ModelTile {
+  int wm, shape, occ, bm, bn;
+  double alpha, beta;
+};
+constexpr ModelTile kModelTiles[] = {
+    {8, 3, 2, 128, 256, 8.97, 12.05}, {6, 3, 2, 96, 256, 5.67, 10.31}, {4, 3, 2, 64, 256, 5.23, 8.05},
+    {8, 5, 2, 128, 128, 6.10, 6.87},  {4, 10, 3, 64, 192, 5.39, 6.22}, {4, 5, 2, 64, 128, 4.58, 4.68},
+    {4, 9, 3, 64, 96, 5.33, 3.69},    {4, 4, 2, 64, 64, 4.69, 2.80},   {2, 5, 2, 32, 128, 3.87, 3.42},
+    {2, 9, 3, 32, 96, 4.46, 2.58},    {2, 4, 2, 32, 64, 4.00, 1.85}};
+
+bool outside_tuned_shapes(int K, int N) { return N < 4096 || K < 4096; }
+
+// The cheapest modelled tile; when its grid has fewer than 144 workgroups, K split in powers
+// of two (at least 8 groups per split) while the grid stays within one round (QKV / 8 at
+// M = 352: 132 workgroups unsplit 11.1 us, 264 split in two 15.1 us).
+GemmPlan model_tile(int M, int K, int N) {
+  const int G = K / w4a16::kGroup;
+  const ModelTile* best = nullptr;
+  double best_cost = 0.0;
+  int best_grid = 0;
+  for (const ModelTile& c : kModelTiles) {
+    const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn);
+    const double cost = ceil_div(t, 256) * (c.alpha + c.beta * K / 1024.0);
+    if (!best || cost < best_cost - 1e-9) best = &c, best_cost = cost, best_grid = t;
+  }
+  int split = 1;
+  while (best_grid * split < 144 && best_grid * split * 2 <= 256 && G / (2 * split) >= 8) split *= 2;
+  return GemmPlan{W4A16_REGIME_TILE, best->wm, best->occ, best->shape, split};
 }
 
 // Tile regime, chosen from sweeps of every tile configuration on MI355X over the Qwen3-8B
@@ -152,6 +207,9 @@ GemmPlan plan_decode(int M, int K, int N) {
 // tiles of 256 columns used before; QKV M=64: 12.7 vs 16.1 us for the decode kernel).
 GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
+  if (M > 128 && N < 16384 && outside_tuned_shapes(K, N)) {
+    return model_tile(M, K, N);
+  }
   // Layers whose width is a multiple of 96 columns (QKV: 6144) above M = 64: 12-wave
   // workgroups of 96 columns (shape 9: 4 K slices x 3 waves along N, three waves per SIMD),
   // 32-row tiles up to M = 128 and 64-row tiles beyond, when that grid has >= 192
@@ -161,10 +219,16 @@ GemmPlan plan_mid(int M, int K, int N) {
   // (shape 5; QKV M = 160: 19.0 us against 22.9 us for 64 x 96 tiles), of 96 columns on
   // narrow ones (shape 9; O M = 160: 16.4 against 17.9 us for 64 x 64 tiles) -- 64-row tiles
   // would compute 192 rows for 160.
-  if (N < 16384 && K < 8192 && M > 128 && N % 96 == 0 && ceil_div(M, 32) * ceil_div(N, 128) <= 256)
-    return GemmPlan{W4A16_REGIME_TILE, 2, 2, 5, 1};
-  if (N <= 4096 && K < 8192 && M > 128 && ceil_div(M, 32) * ceil_div(N, 96) <= 256)
-    return GemmPlan{W4A16_REGIME_TILE, 2, 3, 9, 1};
+  // Both need a grid of 192 .. 256 workgroups; where both qualify (narrow layers whose width
+  // is a multiple of 96, such as gate_up / 8 = 4096 x 3072) the larger grid wins (M = 256:
+  // 15.0 against 17.5 us).
+  if (N < 16384 && K < 8192 && M > 128) {
+    const int t5 = N % 96 == 0 ? ceil_div(M, 32) * ceil_div(N, 128) : 0;
+    const int t9 = N <= 4096 ? ceil_div(M, 32) * ceil_div(N, 96) : 0;
+    const bool ok5 = t5 >= 192 && t5 <= 256, ok9 = t9 >= 192 && t9 <= 256;
+    if (ok9 && (!ok5 || t9 > t5)) return GemmPlan{W4A16_REGIME_TILE, 2, 3, 9, 1};
+    if (ok5) return GemmPlan{W4A16_REGIME_TILE, 2, 2, 5, 1};
+  }
   if (N < 16384 && K < 8192 && N % 96 == 0 && M > 64) {
     const int wm9 = M <= 128 ? 2 : 4;
     if (ceil_div(M, 16 * wm9) * (N / 96) >= 192) return GemmPlan{W4A16_REGIME_TILE, wm9, 3, 9, 1};
@@ -194,11 +258,21 @@ GemmPlan plan_mid(int M, int K, int N) {
   } else {
     wm = (M <= 64 || (M <= 128 && N <= 4096)) ? 2 : 4;
     shape = (M > 128 && N > 4096) ? 5 : 4;
+    // Layers smaller than the tuned shapes: 32-row tiles when 64-row ones leave fewer than
+    // 144 workgroups (QKV / 8 = 4096 x 768 at M = 256: 9.3 against 10.8 us, K split in two
+    // instead of four).
+    if (wm == 4 && ceil_div(M, 64) * ceil_div(N, 16 * w4a16::tile_shape(shape).tw * w4a16::tile_shape(shape).nwn) < 144)
+      wm = 2;
   }
   const w4a16::TileShape ts = w4a16::tile_shape(shape);
-  const int tiles = ceil_div(M, 16 * wm * ts.nwm) * ceil_div(N, 16 * ts.tw * ts.nwn);
+  int tiles = ceil_div(M, 16 * wm * ts.nwm) * ceil_div(N, 16 * ts.tw * ts.nwn);
   if (N < 16384)
     while (tiles * split < 144 && G / (2 * split) >= 8) split *= 2;
+  // Still fewer than 144 workgroups (few columns, or K too short to split): 32-column
+  // workgroups of four K slices, four waves (shape 7) double the grid (O / 8 = 512 x 4096
+  // at M = 32 / 64: 4.4 against 4.9 us; down / 8 = 1536 x 4096: 6.2 against 7.1 / 6.9 us;
+  // QKV / 8 at M = 32 / 64: 7.6 / 7.9 against 8.0 / 8.1 us with K in four).
+  if (K < 8192 && N < 16384 && shape == 4 && tiles * split < 144) return GemmPlan{W4A16_REGIME_TILE, wm, 1, 7, split};
   return GemmPlan{W4A16_REGIME_TILE, wm, 2, shape, split};
 }
 
@@ -278,6 +352,9 @@ GemmPlan best_filling_tile(int M, int N, const TileCand (&cands)[C]) {
 // the 384-column tiles (their fused form pairs waves; measured on wide layers only).
 GemmPlan plan_large(int M, int K, int N, bool fused) {
   const int G = K / w4a16::kGroup;
+  if (N < 16384 && outside_tuned_shapes(K, N)) {
+    return model_tile(M, K, N);
+  }
   // Plain GEMMs on widths that are multiples of 384 columns: 128 x 384 tiles (shape 11, 8
   // waves of 48) where they fill one round on wide layers (gate_up M = 384 / 512: 86.6 / 96.1
   // us against 104.0 / 112.6 us), 64 x 384 tiles on QKV-width layers once 128 x 256 tiles
@@ -348,6 +425,9 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N, fused);
   const int G = K / w4a16::kGroup;
+  if (M <= 2048 && N < 16384 && outside_tuned_shapes(K, N)) {
+    return model_tile(M, K, N);
+  }
   // Plain GEMMs on widths that are multiples of 384 columns: on narrow layers the best-filling
   // of the 384-, 512- and 256-column tiles of 96 or 128 rows (QKV M = 1536 / 2048 / 3072 on
   // 384-column tiles: 76.8 / 95.4 / 151.0 us against 85.9 / 110.6 / 171.9 us; M = 5120 /
