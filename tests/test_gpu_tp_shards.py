@@ -9,12 +9,16 @@ The chunk sizes reach every plan these shapes take: the decode kernel's small-sh
 mid-range tiles of 32 columns and four K slices, and the modelled tile choice beyond
 M = 128.  Plain GEMMs are checked against the CPU oracle itself (awq.py:235-276, fp64
 x @ W over its own dequant), the fused SiLU * up on the gate_up shard against the
-reference's two steps."""
+reference's two steps.  The norm in front of the QKV and gate_up shards takes the same
+paths as at the full shapes (the decode kernel's prologue at M <= 2, the norm kernel before
+the GEMM above that, and the norm split across a producer GEMM and the shard's GEMM at
+M <= 8), with the same bars (test_gpu_rmsnorm.py, test_gpu_norm_stats.py)."""
 import numpy as np
 import pytest
 import torch
 
-from awq_helpers import assert_gemm_close, assert_silu_two_step, awq_mod, bits_of, pkg, random_awq_gpu, random_x_gpu
+from awq_helpers import (GEMM_REL_TOL, assert_gemm_close, assert_silu_two_step, awq_mod, bf16_from_bits, bits_of, pkg,
+                         random_awq_gpu, random_x_gpu, rel_err)
 from oracle import awq_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -54,3 +58,80 @@ def test_tp8_gate_up_shard_fused_silu_mul(gpu_lib, m):
     y = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
     assert y.shape == (m, n // 2)
     assert_silu_two_step(y, x, awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float(), ("gate_up/8", m))
+
+
+EPS = 1e-6
+
+
+def rand_bits(shape, seed, scale=1.0, offset=0.0):
+    rng = np.random.default_rng(seed)
+    return ora.f32_to_bf16_bits((offset + scale * rng.standard_normal(shape)).astype(np.float32))
+
+
+def ulp_diff(a_bits, b_bits):
+    return np.abs(a_bits.view(np.int16).astype(np.int32) - b_bits.view(np.int16).astype(np.int32))
+
+
+@pytest.mark.parametrize("shape,silu", [("qkv", False), ("gate_up", True)])
+def test_tp8_fused_norm_gemm_equals_norm_then_gemm(gpu_lib, shape, silu):
+    """w4a16_gemm_rmsnorm on the shard: x_norm within two ulps of the oracle (> 99 % exact),
+    the new residual bit-exact, the GEMM output bit-identical to the plain GEMM of x_norm."""
+    k, n = TP8_SHAPES[shape]
+    awq = awq_mod()
+    lib = awq.lib()
+    qw, qz, s = random_awq_gpu(k, n, seed=33)
+    packed = awq.repack_awq_qweight(qw)
+    w_bits = rand_bits((k,), seed=34, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    for m in (1, 2, 3, 16, 300):
+        print(f"tp8 gemm_rmsnorm {shape} silu={silu} m={m} plan={lib.plan(m, k, n, 1 if silu else 0)}", flush=True)
+        x_bits, r_bits = rand_bits((m, k), seed=m + 35), rand_bits((m, k), seed=m + 36, scale=4.0)
+        x, res = bf16_from_bits(x_bits), bf16_from_bits(r_bits)
+        want_xn, want_res, _ = ora.add_rms_norm_ref(x_bits, r_bits, w_bits, EPS)
+        ws = torch.zeros(max(lib.workspace_bytes(m, k, n), 256), dtype=torch.uint8, device="cuda")
+        xn, res_out = torch.empty_like(x), torch.empty_like(res)
+        y = torch.empty((m, n // 2 if silu else n), dtype=torch.bfloat16, device="cuda")
+        lib.gemm_rmsnorm(x, res, w, EPS, xn, res_out, packed, qz, s, y, n, ws, silu_mul=silu)
+        assert np.array_equal(bits_of(res_out), want_res), m
+        d = ulp_diff(bits_of(xn), want_xn)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99, (m, d.max(), (d == 0).mean())
+        plain = (awq.awq_linear_silu_mul if silu else awq.awq_linear)(xn, packed, qz, s, group_size=128)
+        assert torch.equal(y.view(torch.int16), plain.view(torch.int16)), m
+
+
+@pytest.mark.parametrize("shape,silu", [("qkv", False), ("gate_up", True)])
+def test_tp8_norm_split_across_shard_gemms(gpu_lib, shape, silu):
+    """The split norm at M <= 8 with the down shard (1536 -> 4096) as the producer and the
+    QKV or gate_up shard as the consumer: s and the new residual bit-exact with the plain and
+    residual-epilogue GEMMs of the producer, x_norm within two ulps of the oracle's
+    add_rms_forward, y within the GEMM tolerance of the plain GEMM of x_norm (> 90 %
+    bit-equal) and deterministic."""
+    awq = awq_mod()
+    k, n = TP8_SHAPES[shape]
+    kd, nd = TP8_SHAPES["down"]
+    qw, qz, s = random_awq_gpu(k, n, seed=37)
+    packed = awq.repack_awq_qweight(qw)
+    qwd, qzd, sd = random_awq_gpu(kd, nd, seed=38)
+    pd = awq.repack_awq_qweight(qwd)
+    w_bits = rand_bits((k,), seed=39, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    for m in (1, 2, 3, 5, 8):
+        print(f"tp8 norm split {shape} silu={silu} m={m}", flush=True)
+        x = bf16_from_bits(rand_bits((m, kd), seed=m + 40))
+        res = bf16_from_bits(rand_bits((m, nd), seed=m + 41, scale=4.0))
+        inp, res_out = awq.awq_linear_residual_stats(x, pd, qzd, sd, res, group_size=128)
+        h = awq.awq_linear(x, pd, qzd, sd, group_size=128)
+        assert torch.equal(inp.s.view(torch.int32), (h.float() + res.float()).view(torch.int32)), m
+        want_res_epi = awq.awq_linear_residual(x, pd, qzd, sd, res, group_size=128)
+        assert torch.equal(res_out.view(torch.int16), want_res_epi.view(torch.int16)), m
+        want_xn, want_res, _ = ora.add_rms_norm_ref(bits_of(h), bits_of(res), w_bits, EPS)
+        assert np.array_equal(bits_of(res_out), want_res), m
+        xn = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+        y = awq.awq_linear_rmsnorm_stats(inp, w, EPS, packed, qz, s, group_size=128, silu_mul=silu, x_norm=xn)
+        d = ulp_diff(bits_of(xn), want_xn)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99, (m, d.max(), (d == 0).mean())
+        plain = (awq.awq_linear_silu_mul if silu else awq.awq_linear)(xn, packed, qz, s, group_size=128)
+        assert rel_err(y, plain.float()) <= GEMM_REL_TOL, m
+        assert (bits_of(y) == bits_of(plain)).mean() > 0.9, m
+        y2 = awq.awq_linear_rmsnorm_stats(inp, w, EPS, packed, qz, s, group_size=128, silu_mul=silu)
+        assert torch.equal(y2.view(torch.int16), y.view(torch.int16)), m
