@@ -73,6 +73,16 @@ int tile_bn(const GemmPlan& p) {
   return 16 * t.tw * t.nwn;
 }
 
+// The four Qwen3-8B projections (K x N) the rule sets below were tuned on.
+bool tuned_shape(int K, int N) {
+  return (K == 4096 && (N == 6144 || N == 4096 || N == 24576)) || (K == 12288 && N == 4096);
+}
+
+// Layers at least as large as the tuned ones in both dimensions, other than those four:
+// their own rules (decode) and cost model (mid range), from sweeps of the Qwen3-14B and
+// Qwen3-32B projections.
+bool larger_shape(int K, int N) { return K >= 4096 && N >= 4096 && !tuned_shape(K, N); }
+
 // Decode regime, chosen from a sweep of every configuration on MI355X over the Qwen3-8B
 // projection shapes (tn 16-column tiles per workgroup, waves, depth = groups in flight per
 // wave, split = K splits).  The activation traffic per weight byte falls as tn grows (each
@@ -102,7 +112,41 @@ GemmPlan plan_decode(int M, int K, int N) {
   const int MB = (M + 15) / 16;
   const int T = N / 16;
   int tn = 2, waves = 8, depth = 2, split = 1;
-  if (N >= 16384) {
+  if (larger_shape(K, N)) {
+    // K split s0 so that a workgroup covers more than 4096 of K (K = 8192 unsplit, 17408 and
+    // 25600 in four).  Very wide (>= 1024 column tiles) or long-K (s0 >= 4) layers: 32
+    // columns and one group in flight up to M = 8, then 64 columns (K split twice as often
+    // for long K; 4 waves above M = 16 on wide ones).  Others: 32 columns at M = 1, then 64
+    // where that still gives >= 160 workgroups (else 32), 4 waves for 32 columns at
+    // 8 < M <= 16 (64 columns with K in two for K >= 8192), and 64 columns with one group
+    // in flight beyond.  Sweeps of the Qwen3-14B and -32B projections (QKV 5120 x 7168 /
+    // 10240, O 5120 x 5120 / 8192 x 5120, gate_up 5120 x 34816 / 51200, down 17408 / 25600
+    // x 5120) at M = 1, 4, 8, 16, 24: within 0.9 % / 1.6 % of the best configurations in
+    // total (331.0 / 414.0 against 377.5 / 437.8 us for the rules of the tuned shapes).
+    int s0 = 1;
+    while (K / (2 * s0) > 4096) s0 *= 2;
+    const bool wide = T >= 1024, longk = s0 >= 4;
+    const int tn_m = T / 4 >= 160 ? 4 : 2;
+    split = s0;
+    if (wide || longk) {
+      depth = 1;
+      if (M <= 8) tn = 2;
+      else if (M > 16 && wide) { tn = 4; waves = 4; split = 2 * s0; }
+      else { tn = 4; split = wide ? s0 : 2 * s0; }
+    } else if (M <= 1) {
+      tn = 2;
+    } else if (M <= 8) {
+      tn = tn_m;
+    } else if (M <= 16) {
+      tn = tn_m;
+      if (tn_m == 2 && K >= 8192) { tn = 4; split = 2 * s0; }  // O 8192 x 5120: 11.4 against 14.0 us
+      else if (tn_m == 2) waves = 4;
+    } else {
+      tn = 4;
+      depth = 1;
+      if (tn_m == 2) split = 2 * s0;
+    }
+  } else if (N >= 16384) {
     if (M <= 2) tn = 2;
     else if (M <= 8) tn = 3;
     else if (M <= 24) tn = 6;
@@ -184,6 +228,32 @@ GemmPlan model_tile(int M, int K, int N) {
   return GemmPlan{W4A16_REGIME_TILE, best->wm, best->occ, best->shape, split};
 }
 
+// Mid-range (M <= 256) plans for layers larger than the tuned ones: every modelled tile with
+// K split s in {1, 2, 3, 4, 6, 8} (at least 4 groups per split), costed as its rounds of 256
+// workgroups times alpha + beta * K / s / 1024, plus for s > 1 the exchange of partials,
+// (-0.31 + 0.59 A + 0.19 (s - 1) A) us per round for A = the tile's area / 4096 (least
+// squares over every split configuration of the Qwen3-14B and tensor-parallel sweeps).  On
+// the Qwen3-14B sweep at M = 32 .. 256 it comes within 3.6 % of the best configuration in
+// total (740.7 against 715.2 us), where the tuned rules took 897.0 us.
+GemmPlan model_tile_split(int M, int K, int N) {
+  const int G = K / w4a16::kGroup;
+  const ModelTile* best = nullptr;
+  int best_split = 1;
+  double best_cost = 0.0;
+  for (const ModelTile& c : kModelTiles) {
+    for (int sp : {1, 2, 3, 4, 6, 8}) {
+      if (G / sp < 4) continue;
+      const int t = ceil_div(M, c.bm) * ceil_div(N, c.bn) * sp;
+      const double rounds = ceil_div(t, 256);
+      const double area = c.bm * c.bn / 4096.0;
+      double cost = rounds * (c.alpha + c.beta * K / (1024.0 * sp));
+      if (sp > 1) cost += rounds * (-0.31 + 0.59 * area + 0.19 * (sp - 1) * area);
+      if (!best || cost < best_cost - 1e-9) best = &c, best_split = sp, best_cost = cost;
+    }
+  }
+  return GemmPlan{W4A16_REGIME_TILE, best->wm, best->occ, best->shape, best_split};
+}
+
 // Tile regime, chosen from sweeps of every tile configuration on MI355X over the Qwen3-8B
 // shapes at M = 32 .. 2048.  Wave layouts (w4a16::tile_shape): shape 3 = 8 waves side by side
 // along N (32 columns each), one workgroup per CU; shape 1 = 4 waves (64 columns each), two
@@ -207,6 +277,7 @@ GemmPlan model_tile(int M, int K, int N) {
 // tiles of 256 columns used before; QKV M=64: 12.7 vs 16.1 us for the decode kernel).
 GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
+  if (larger_shape(K, N)) return model_tile_split(M, K, N);
   if (M > 128 && N < 16384 && outside_tuned_shapes(K, N)) {
     return model_tile(M, K, N);
   }

@@ -135,3 +135,46 @@ def test_tp8_norm_split_across_shard_gemms(gpu_lib, shape, silu):
         assert (bits_of(y) == bits_of(plain)).mean() > 0.9, m
         y2 = awq.awq_linear_rmsnorm_stats(inp, w, EPS, packed, qz, s, group_size=128, silu_mul=silu)
         assert torch.equal(y2.view(torch.int16), y.view(torch.int16)), m
+
+
+# Layers larger than the tuned Qwen3-8B ones take their own decode rules and a mid-range
+# cost model: the Qwen3-14B projections, every plan branch up to M = 512, against an fp32
+# GEMM over the library's dequant (bit-exact with the oracle's, test_gpu_format.py) with the
+# oracle itself at two row counts of the narrower layers.
+Q14_SHAPES = {"qkv": (5120, 7168), "o": (5120, 5120), "gate_up": (5120, 34816), "down": (17408, 5120)}
+
+
+@pytest.mark.parametrize("shape", sorted(Q14_SHAPES))
+def test_larger_model_shapes(gpu_lib, shape):
+    k, n = Q14_SHAPES[shape]
+    awq = awq_mod()
+    qw, qz, s = random_awq_gpu(k, n, seed=41)
+    packed = awq.repack_awq_qweight(qw)
+    w = awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
+    for m in (1, 8, 16, 24, 32, 64, 128, 256, 512):
+        print(f"larger shape {shape} {k}x{n} m={m} plan={pkg().lib().plan(m, k, n)}", flush=True)
+        x = random_x_gpu(m, k, seed=70 + m, outliers=m >= 256)
+        y = awq.awq_linear(x, packed, qz, s, group_size=128)
+        assert_gemm_close(y, x.float() @ w, (shape, m))
+        if shape != "gate_up" and m in (16, 64):
+            want = ora.awq_linear_ref(bits_of(x), qw.cpu().numpy(), qz.cpu().numpy(), bits_of(s), 128)
+            assert_gemm_close(y, torch.from_numpy(want).cuda(), (shape, m, "oracle"))
+
+
+Q32_SHAPES = {"qkv": (5120, 10240), "o": (8192, 5120), "gate_up": (5120, 51200), "down": (25600, 5120)}
+
+
+@pytest.mark.parametrize("shape", sorted(Q32_SHAPES))
+def test_larger_model_shapes_32b(gpu_lib, shape):
+    """The Qwen3-32B projections through the same larger-layer rules (decode M = 1 .. 24,
+    the mid-range model at 64 and 256), against an fp32 GEMM over the library's dequant."""
+    k, n = Q32_SHAPES[shape]
+    awq = awq_mod()
+    qw, qz, s = random_awq_gpu(k, n, seed=42)
+    packed = awq.repack_awq_qweight(qw)
+    w = awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
+    for m in (1, 4, 16, 24, 64, 256):
+        print(f"larger shape {shape} {k}x{n} m={m} plan={pkg().lib().plan(m, k, n)}", flush=True)
+        x = random_x_gpu(m, k, seed=90 + m)
+        y = awq.awq_linear(x, packed, qz, s, group_size=128)
+        assert_gemm_close(y, x.float() @ w, (shape, m))
