@@ -1,6 +1,8 @@
-"""Parity at the per-GPU shapes of the Qwen3-8B projections split eight ways: QKV and
-gate_up column-parallel on N, O and down row-parallel on K (linear.py:14-21, 136-146,
-178-196, 217-226), i.e. QKV 4096 x 768, O 512 x 4096, gate_up 4096 x 3072 and down
+"""Parity at shapes other than the four Qwen3-8B projections the planner was tuned on.
+
+Tensor-parallel shards -- the per-GPU shapes of the Qwen3-8B projections split eight ways,
+QKV and gate_up column-parallel on N, O and down row-parallel on K (linear.py:14-21,
+136-146, 178-196, 217-226): QKV 4096 x 768, O 512 x 4096, gate_up 4096 x 3072 and down
 1536 x 4096.  One GPU shows the kernels on its share at its real shape; the all-reduce of
 the row-parallel outputs lies outside this library.
 
@@ -12,7 +14,10 @@ x @ W over its own dequant), the fused SiLU * up on the gate_up shard against th
 reference's two steps.  The norm in front of the QKV and gate_up shards takes the same
 paths as at the full shapes (the decode kernel's prologue at M <= 2, the norm kernel before
 the GEMM above that, and the norm split across a producer GEMM and the shard's GEMM at
-M <= 8), with the same bars (test_gpu_rmsnorm.py, test_gpu_norm_stats.py)."""
+M <= 8), with the same bars (test_gpu_rmsnorm.py, test_gpu_norm_stats.py).
+
+Larger models -- the Qwen3-14B and -32B projections, which take the larger-layer decode
+rules and the mid-range cost model (below)."""
 import numpy as np
 import pytest
 import torch
@@ -178,3 +183,56 @@ def test_larger_model_shapes_32b(gpu_lib, shape):
         x = random_x_gpu(m, k, seed=90 + m)
         y = awq.awq_linear(x, packed, qz, s, group_size=128)
         assert_gemm_close(y, x.float() @ w, (shape, m))
+
+
+@pytest.mark.parametrize("m", [1, 16, 24, 64, 256])
+def test_larger_gate_up_fused_silu_mul(gpu_lib, m):
+    """The fused SiLU * up on the Qwen3-14B gate_up (5120 x 34816) through the larger-layer
+    plans, against the reference's two steps."""
+    k, n = Q14_SHAPES["gate_up"]
+    awq = awq_mod()
+    qw, qz, s = random_awq_gpu(k, n, seed=43)
+    packed = awq.repack_awq_qweight(qw)
+    x = random_x_gpu(m, k, seed=95 + m)
+    print(f"larger fused gate_up m={m} plan={pkg().lib().plan(m, k, n, 1)}", flush=True)
+    y = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
+    assert_silu_two_step(y, x, awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float(), ("gate_up 14B", m))
+
+
+def test_larger_qkv_norm_paths(gpu_lib):
+    """w4a16_gemm_rmsnorm (prologue at M <= 2, norm kernel + GEMM above) and the split norm
+    (O 5120 x 5120 as producer) in front of the Qwen3-14B QKV (5120 x 7168)."""
+    awq = awq_mod()
+    lib = awq.lib()
+    k, n = Q14_SHAPES["qkv"]
+    qw, qz, s = random_awq_gpu(k, n, seed=44)
+    packed = awq.repack_awq_qweight(qw)
+    ko, no = Q14_SHAPES["o"]
+    qwo, qzo, so = random_awq_gpu(ko, no, seed=45)
+    po = awq.repack_awq_qweight(qwo)
+    w_bits = rand_bits((k,), seed=46, scale=0.1, offset=1.0)
+    w = bf16_from_bits(w_bits)
+    for m in (1, 2, 3, 8, 16, 64):
+        print(f"larger qkv norm m={m}", flush=True)
+        x_bits, r_bits = rand_bits((m, k), seed=m + 47), rand_bits((m, k), seed=m + 48, scale=4.0)
+        x, res = bf16_from_bits(x_bits), bf16_from_bits(r_bits)
+        want_xn, want_res, _ = ora.add_rms_norm_ref(x_bits, r_bits, w_bits, EPS)
+        ws = torch.zeros(max(lib.workspace_bytes(m, k, n), 256), dtype=torch.uint8, device="cuda")
+        xn, res_out = torch.empty_like(x), torch.empty_like(res)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        lib.gemm_rmsnorm(x, res, w, EPS, xn, res_out, packed, qz, s, y, n, ws, silu_mul=False)
+        assert np.array_equal(bits_of(res_out), want_res), m
+        d = ulp_diff(bits_of(xn), want_xn)
+        assert d.max() <= 2 and (d == 0).mean() > 0.99, (m, d.max(), (d == 0).mean())
+        assert torch.equal(y.view(torch.int16), awq.awq_linear(xn, packed, qz, s, group_size=128).view(torch.int16)), m
+        if m <= 8:
+            xo = bf16_from_bits(rand_bits((m, ko), seed=m + 49))
+            inp, _ = awq.awq_linear_residual_stats(xo, po, qzo, so, res, group_size=128)
+            h = awq.awq_linear(xo, po, qzo, so, group_size=128)
+            want_xn2, _, _ = ora.add_rms_norm_ref(bits_of(h), r_bits, w_bits, EPS)
+            xn2 = torch.empty((m, k), dtype=torch.bfloat16, device="cuda")
+            y2 = awq.awq_linear_rmsnorm_stats(inp, w, EPS, packed, qz, s, group_size=128, x_norm=xn2)
+            d2 = ulp_diff(bits_of(xn2), want_xn2)
+            assert d2.max() <= 2 and (d2 == 0).mean() > 0.99, (m, d2.max(), (d2 == 0).mean())
+            plain = awq.awq_linear(xn2, packed, qz, s, group_size=128)
+            assert rel_err(y2, plain.float()) <= GEMM_REL_TOL and (bits_of(y2) == bits_of(plain)).mean() > 0.9, m
