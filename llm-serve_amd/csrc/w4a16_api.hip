@@ -83,6 +83,13 @@ bool tuned_shape(int K, int N) {
 // Qwen3-32B projections.
 bool larger_shape(int K, int N) { return K >= 4096 && N >= 4096 && !tuned_shape(K, N); }
 
+// Untuned layers that are very wide (N >= 16384) or long (K >= 8192) also take the larger
+// layers' mid-range cost model, and the very wide ones their decode rules (Qwen3-4B gate_up
+// 2560 x 19456 and down 9728 x 2560 at M = 32 .. 256: 81.2 / 64.6 us, the best
+// configurations, against 89.7 / 76.5 us by the tuned rules; gate_up decode at M = 8 / 16:
+// 10.8 / 12.1 against 12.0 / 14.5 us).
+bool wide_or_long_shape(int K, int N) { return !tuned_shape(K, N) && (N >= 16384 || K >= 8192); }
+
 // Decode regime, chosen from a sweep of every configuration on MI355X over the Qwen3-8B
 // projection shapes (tn 16-column tiles per workgroup, waves, depth = groups in flight per
 // wave, split = K splits).  The activation traffic per weight byte falls as tn grows (each
@@ -112,7 +119,7 @@ GemmPlan plan_decode(int M, int K, int N) {
   const int MB = (M + 15) / 16;
   const int T = N / 16;
   int tn = 2, waves = 8, depth = 2, split = 1;
-  if (larger_shape(K, N)) {
+  if (larger_shape(K, N) || (N >= 16384 && wide_or_long_shape(K, N))) {
     // K split s0 so that a workgroup covers more than 4096 of K (K = 8192 unsplit, 17408 and
     // 25600 in four).  Very wide (>= 1024 column tiles) or long-K (s0 >= 4) layers: 32
     // columns and one group in flight up to M = 8, then 64 columns (K split twice as often
@@ -131,7 +138,7 @@ GemmPlan plan_decode(int M, int K, int N) {
     if (wide || longk) {
       depth = 1;
       if (M <= 8) tn = 2;
-      else if (M > 16 && wide) { tn = 4; waves = 4; split = 2 * s0; }
+      else if (M > 16 && wide) { tn = 4; waves = 4; split = (G >= 32 ? 2 : 1) * s0; }  // 4B gate_up M = 24: 16.8 / 18.7 us
       else { tn = 4; split = wide ? s0 : 2 * s0; }
     } else if (M <= 1) {
       tn = 2;
@@ -197,7 +204,9 @@ GemmPlan plan_decode(int M, int K, int N) {
 // configuration at M > 128 (533.9 against 628.8 us in total for the rules below) where its
 // grid has at least 144 workgroups; below that, K split over the same tile fills the grid
 // (QKV / 8 at M = 160 .. 320: 8.7 - 9.4 us, within 1 % of the best configuration).  Used up
-// to M = 2048; longer chunks, which take several rounds of 512-column tiles, keep the rules.
+// to M = 2048 (beyond M = 1024 for widths below 4096 only: wider layers fill rounds with the
+// rules' 384- and 512-column tiles, which the model leaves out -- Qwen3-4B QKV 2560 x 6144
+// at M = 2048: 58.8 us on 128 x 384 tiles against 69.6 us on the model's 64 x 96).
 struct ModelTile {
   int wm, shape, occ, bm, bn;
   double alpha, beta;
@@ -277,7 +286,7 @@ GemmPlan model_tile_split(int M, int K, int N) {
 // tiles of 256 columns used before; QKV M=64: 12.7 vs 16.1 us for the decode kernel).
 GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
-  if (larger_shape(K, N)) return model_tile_split(M, K, N);
+  if (larger_shape(K, N) || wide_or_long_shape(K, N)) return model_tile_split(M, K, N);
   if (M > 128 && N < 16384 && outside_tuned_shapes(K, N)) {
     return model_tile(M, K, N);
   }
@@ -496,7 +505,7 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N, fused);
   const int G = K / w4a16::kGroup;
-  if (M <= 2048 && N < 16384 && outside_tuned_shapes(K, N)) {
+  if (M <= 2048 && N < 4096 && outside_tuned_shapes(K, N)) {
     return model_tile(M, K, N);
   }
   // Plain GEMMs on widths that are multiples of 384 columns: on narrow layers the best-filling
