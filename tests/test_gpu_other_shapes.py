@@ -236,3 +236,23 @@ def test_larger_qkv_norm_paths(gpu_lib):
             assert d2.max() <= 2 and (d2 == 0).mean() > 0.99, (m, d2.max(), (d2 == 0).mean())
             plain = awq.awq_linear(xn2, packed, qz, s, group_size=128)
             assert rel_err(y2, plain.float()) <= GEMM_REL_TOL and (bits_of(y2) == bits_of(plain)).mean() > 0.9, m
+
+
+Q4_SHAPES = {"qkv": (2560, 6144), "o": (4096, 2560), "gate_up": (2560, 19456), "down": (9728, 2560)}
+
+
+@pytest.mark.parametrize("shape", sorted(Q4_SHAPES))
+def test_smaller_model_shapes_4b(gpu_lib, shape):
+    """The Qwen3-4B projections: the 8B rules (QKV, O), the very wide / long-K rules and
+    mid-range model (gate_up, down), and the one-round model beyond M = 1024 for the narrow
+    ones, against an fp32 GEMM over the library's dequant."""
+    k, n = Q4_SHAPES[shape]
+    awq = awq_mod()
+    qw, qz, s = random_awq_gpu(k, n, seed=46)
+    packed = awq.repack_awq_qweight(qw)
+    w = awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
+    for m in (1, 8, 16, 24, 32, 64, 256, 2048):
+        print(f"smaller shape {shape} {k}x{n} m={m} plan={pkg().lib().plan(m, k, n)}", flush=True)
+        x = random_x_gpu(m, k, seed=110 + m, outliers=m == 2048)
+        y = awq.awq_linear(x, packed, qz, s, group_size=128)
+        assert_gemm_close(y, x.float() @ w, (shape, m))
