@@ -345,3 +345,45 @@ def test_noalloc_scratch_covers_every_planned_workspace(pkg):
     L = pkg.lib()
     for k, n in ((4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096)):
         assert L.workspace_bytes_max(16384, k, n) <= 48 << 20, (k, n)
+
+
+def test_every_plan_passes_the_configuration_checks(pkg):
+    """Every plan the planner emits -- plain and fused SiLU * up, decode and tile regimes --
+    for the Qwen3-8B projections, their eight-way tensor-parallel shards, the Qwen3-4B, -14B
+    and -32B projections and seeded random layer shapes, at chunk sizes across every
+    planner boundary, passes the library's own configuration checks (shape, tiles, waves,
+    depth, LDS, registers), and its workspace is covered by w4a16_workspace_bytes (plain) or
+    w4a16_workspace_bytes_max (both).  Without a GPU a valid configuration stops at the
+    launch (W4A16_ERR_LAUNCH); any other status is a planner or workspace-query bug.  The
+    pointers are dummies, so on a machine with a GPU the test is skipped."""
+    import random
+
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("dummy pointers: the configuration calls would launch on a real GPU")
+    L = pkg.lib()
+    buf = (ctypes.c_uint8 * 1024)()
+    p = ctypes.addressof(buf) + (256 - ctypes.addressof(buf) % 256) % 256  # the workspace is 256-byte aligned
+    shapes = [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096),
+              (4096, 768), (512, 4096), (4096, 3072), (1536, 4096),
+              (2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560),
+              (5120, 7168), (5120, 5120), (5120, 34816), (17408, 5120),
+              (5120, 10240), (8192, 5120), (5120, 51200), (25600, 5120)]
+    rng = random.Random(5)
+    shapes += [(128 * rng.randint(2, 200), 128 * rng.randint(2, 400)) for _ in range(12)]
+    ms = list(range(1, 34)) + [40, 48, 49, 64, 65, 96, 128, 129, 160, 192, 256, 257, 288, 320, 321, 384, 448, 512,
+                               513, 640, 704, 705, 768, 769, 1024, 1025, 1152, 1536, 2048, 2049, 3072, 4096]
+    bad = []
+    for k, n in shapes:
+        ws_max = L.workspace_bytes_max(max(ms), k, n)
+        for m in ms:
+            for entry, fn in ((0, L.dll.w4a16_gemm_config), (1, L.dll.w4a16_gemm_silu_mul_config)):
+                if entry == 1 and n % 128:
+                    continue
+                plan = L.plan(m, k, n, entry)
+                ws = L.workspace_bytes(m, k, n) if entry == 0 else ws_max
+                rc = fn(p, p, p, p, p, m, k, n, 128, *plan, p if ws else None, ws, None)
+                if rc != 5:
+                    bad.append((k, n, m, entry, plan, rc, L.last_error()[:80]))
+    assert not bad, bad[:10]
