@@ -154,11 +154,18 @@ __device__ __forceinline__ uint16_t add_bf16(uint16_t v, uint16_t r) {
 
 // SiLU(g) * u = g / (1 + e^-g) * u in fp32 for the fused gate/up epilogue, e^-g as
 // 2^(-g log2 e) on the hardware exp2 and the quotient by the hardware reciprocal (about
-// 1 ulp each, far below the bf16 rounding of the result).  g -> -inf gives -0 (e^-g = inf,
-// reciprocal 0), g -> +inf gives g u; NaN propagates.
+// 1 ulp each, far below the bf16 rounding of the result).  Below g = -44 the reciprocal of
+// 1 + e^-g approaches the subnormal range, where it flushes to zero, and below g = -88.7
+// e^-g itself overflows, although g u / (1 + e^-g) is still a normal float down to about
+// g = -95 (g = -88, u = 15: -8.1e-36): there the quotient is formed as
+// g / (2^-64 + 2^(-g log2 e - 64)) * u * 2^-64.  Results below the smallest normal float
+// flush to zero.  g -> -inf gives -0, g -> +inf gives g u; NaN propagates.
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
-  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+  const float t = -g * 1.44269504088896341f;
+  const bool low = t > 64.0f;
+  const float e = __builtin_amdgcn_exp2f(low ? t - 64.0f : t);
+  const float sc = low ? 0x1p-64f : 1.0f;
+  return g * __builtin_amdgcn_rcpf(sc + e) * u * sc;
 }
 
 // The fused gate/up epilogue from the fp32 accumulators, in the reference's two steps: g and

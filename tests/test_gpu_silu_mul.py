@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 import torch
 
-from awq_helpers import (QWEN3_SHAPES, assert_silu_two_step, awq_mod, decode_config_accepted,
+from awq_helpers import (QWEN3_SHAPES, assert_silu_two_step, awq_mod, bf16_from_bits, bits_of, decode_config_accepted,
                          random_awq_gpu, random_x_gpu, rel_err, to_gpu)
 from oracle import awq_oracle as ora
 
@@ -224,3 +224,57 @@ def test_fused_graph_capture_replays_match_eager(gpu_lib):
         assert torch.equal(static_y.view(torch.int16), eager.view(torch.int16)), i
         _ = awq.awq_linear_silu_mul(random_x_gpu(m, k, seed=60 + i), packed, qz, s, group_size=128)
         torch.cuda.synchronize()
+
+
+def test_fused_silu_mul_deep_negative_gate(gpu_lib):
+    """Gate values far into SiLU's negative tail, where 1 / (1 + e^-g) is subnormal in fp32
+    but the result g u / (1 + e^-g) is a normal float (g = -88, u = -176: 7.1e-35), through
+    every fused epilogue (decode configurations, every tile kernel including the paired-wave
+    384-column layout): one group of K = 128 with weights q - z = 1 on the gate columns and 2
+    on the up columns at scale 1, so that row r of x = (v_r, 0, ..., 0) gives g = v_r and
+    u = 2 v_r exactly.  Against the reference's two steps in fp64 (SiLU(g) * u rounded
+    once), within one bf16 last place, and nonzero wherever the reference is a normal
+    float; results below the smallest normal float (g <= -100 here) may flush to zero."""
+    k, n = 128, 768
+    vals = [-30.0, -44.0, -45.0, -60.0, -80.0, -87.0, -88.0, -90.0, -95.0, -100.0, -104.0, -120.0, 3.0, 88.0]
+    m = 64
+    rows = np.zeros((m, k), np.float32)
+    for r in range(m):
+        rows[r, 0] = vals[r % len(vals)]
+    x_bits = ora.f32_to_bf16_bits(rows)
+    q = np.full((k, n), 9, np.int64)
+    q[:, n // 2:] = 10
+    qweight = ora.pack_awq_int4(q)
+    qzeros = ora.pack_awq_int4(np.full((1, n), 8, np.int64))
+    scales_bits = ora.f32_to_bf16_bits(np.ones((1, n), np.float32))
+    g = rows[:, :1].astype(np.float64).repeat(n // 2, axis=1)
+    want = ora.f32_to_bf16_bits(ora.silu_and_mul_ref(np.concatenate([g, 2 * g], axis=1)).astype(np.float32))
+    qw = torch.from_numpy(qweight).cuda()
+    packed = awq_mod().repack_awq_qweight(qw)
+    qz, s, x = torch.from_numpy(qzeros).cuda(), bf16_from_bits(scales_bits), bf16_from_bits(x_bits)
+
+    def check(y, what):
+        got, ref = bits_of(y), want[: y.shape[0]]
+        subnormal = (ref & 0x7F80) == 0  # zero or subnormal reference
+        d = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+        ok_flush = subnormal & ((got & 0x7FFF) == 0)
+        assert d[~ok_flush].max() <= 1, (what, d[~ok_flush].max())
+        assert not (((got & 0x7FFF) == 0) & ~subnormal).any(), what
+        assert (~subnormal).sum() > (subnormal.sum() * 3), what  # most rows are normal results
+
+    for mm in (14, 64):  # a decode plan, then the tile regime
+        check(awq_mod().awq_linear_silu_mul(x[:mm], packed, qz, s, group_size=128), mm)
+    for tn, waves, depth, split in FUSED_DECODE_CONFIGS:
+        if split > 1 or not decode_config_accepted(14, k, tn, depth, waves, split):
+            continue
+        y = torch.empty((14, n // 2), dtype=torch.bfloat16, device="cuda")
+        ws = torch.zeros(1, dtype=torch.uint8, device="cuda")
+        gpu_lib.gemm_config(x[:14], packed, qz, s, y, k, n, 1, tn, waves, split, ws, p2=depth, silu_mul=True)
+        check(y, (tn, waves, depth))
+    for wm, shape, occ in TILE_KERNELS:
+        if (n // 2) % PAIRED_WAVE_COLS.get(shape, 1):
+            continue
+        y = torch.empty((m, n // 2), dtype=torch.bfloat16, device="cuda")
+        ws = torch.zeros(1, dtype=torch.uint8, device="cuda")
+        gpu_lib.gemm_config(x, packed, qz, s, y, k, n, 2, wm, occ, 1, ws, p2=shape, silu_mul=True)
+        check(y, (wm, shape, occ))
