@@ -83,6 +83,10 @@ bool tuned_shape(int K, int N) {
 // Qwen3-32B projections.
 bool larger_shape(int K, int N) { return K >= 4096 && N >= 4096 && !tuned_shape(K, N); }
 
+// Layers narrower or shorter than the tuned ones (tensor-parallel shards, small models):
+// their own small-grid rules, and a one-round tile cost model above M = 128.
+bool smaller_shape(int K, int N) { return N < 4096 || K < 4096; }
+
 // Untuned layers that are very wide (N >= 16384) or long (K >= 8192) also take the larger
 // layers' mid-range cost model, and the very wide ones their decode rules (Qwen3-4B gate_up
 // 2560 x 19456 and down 9728 x 2560 at M = 32 .. 256: 81.2 / 64.6 us, the best
@@ -217,7 +221,6 @@ constexpr ModelTile kModelTiles[] = {
     {4, 9, 3, 64, 96, 5.33, 3.69},    {4, 4, 2, 64, 64, 4.69, 2.80},   {2, 5, 2, 32, 128, 3.87, 3.42},
     {2, 9, 3, 32, 96, 4.46, 2.58},    {2, 4, 2, 32, 64, 4.00, 1.85}};
 
-bool outside_tuned_shapes(int K, int N) { return N < 4096 || K < 4096; }
 
 // The cheapest modelled tile; when its grid has fewer than 144 workgroups, K split in powers
 // of two (at least 8 groups per split) while the grid stays within one round (QKV / 8 at
@@ -287,7 +290,7 @@ GemmPlan model_tile_split(int M, int K, int N) {
 GemmPlan plan_mid(int M, int K, int N) {
   const int G = K / w4a16::kGroup;
   if (larger_shape(K, N) || wide_or_long_shape(K, N)) return model_tile_split(M, K, N);
-  if (M > 128 && N < 16384 && outside_tuned_shapes(K, N)) {
+  if (M > 128 && N < 16384 && smaller_shape(K, N)) {
     return model_tile(M, K, N);
   }
   // Layers whose width is a multiple of 96 columns (QKV: 6144) above M = 64: 12-wave
@@ -432,7 +435,7 @@ GemmPlan best_filling_tile(int M, int N, const TileCand (&cands)[C]) {
 // the 384-column tiles (their fused form pairs waves; measured on wide layers only).
 GemmPlan plan_large(int M, int K, int N, bool fused) {
   const int G = K / w4a16::kGroup;
-  if (N < 16384 && outside_tuned_shapes(K, N)) {
+  if (N < 16384 && smaller_shape(K, N)) {
     return model_tile(M, K, N);
   }
   // Plain GEMMs on widths that are multiples of 384 columns: 128 x 384 tiles (shape 11, 8
@@ -505,7 +508,7 @@ GemmPlan plan_tile(int M, int K, int N, bool fused) {
   if (M <= 256) return plan_mid(M, K, N);
   if (M <= 1024) return plan_large(M, K, N, fused);
   const int G = K / w4a16::kGroup;
-  if (M <= 2048 && N < 4096 && outside_tuned_shapes(K, N)) {
+  if (M <= 2048 && N < 4096 && smaller_shape(K, N)) {
     return model_tile(M, K, N);
   }
   // Plain GEMMs on widths that are multiples of 384 columns: on narrow layers the best-filling
