@@ -3,7 +3,10 @@ split and tile configuration that the planner reaches for M in 1..3000, K in 128
 and N in 64..8192 (multiples of 128 and 64), against the fp32 product of the reference's
 bf16 weights (same metric and tolerance as every GEMM test); where N % 128 == 0 also the
 fused SiLU(gate) * up product of the same weight read as a gate|up pair, against SiLU * up
-over that fp32 product rounded to bf16 (the reference's two steps)."""
+over that fp32 product rounded to bf16 (the reference's two steps).  Larger layers (K up to
+28672, N up to 57344) the same way against an fp64 product; and the residual epilogue and
+the norm + GEMM call at random shapes against their definitions in terms of the plain
+GEMM, bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -76,3 +79,35 @@ def test_random_large_shapes_match_reference(gpu_lib, seed):
             f = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128)
             assert_silu_two_step(f, x, wb.float(), ("silu_mul", m, k, n))
         del wb
+
+
+@pytest.mark.parametrize("seed", [0, 10])
+def test_random_shapes_residual_and_norm_calls(gpu_lib, seed):
+    """The same random shapes (seed 0: small layers, seed 10: large ones) through the
+    residual epilogue and the norm + GEMM call, each against its own definition in terms of
+    the plain GEMM: bf16(bf16(x W) + residual) bit for bit, and for w4a16_gemm_rmsnorm (the
+    layer's K as hidden size, K <= 16384) the plain GEMM of the returned x_norm bit for bit,
+    with the new residual bf16(x + residual) bit-exact."""
+    awq = awq_mod()
+    lib = awq.lib()
+    cases = shapes(seed, 8) if seed < 10 else large_shapes(seed, 6)
+    for i, (m, k, n) in enumerate(cases):
+        print(f"random residual/norm seed={seed} i={i} M={m} K={k} N={n}", flush=True)
+        qw, qz, s = random_awq_gpu(k, n, seed=2000 * seed + i)
+        packed = awq.repack_awq_qweight(qw)
+        x = random_x_gpu(m, k, seed=50 + i)
+        res = random_x_gpu(m, n, seed=60 + i)
+        plain = awq.awq_linear(x, packed, qz, s, group_size=128)
+        want = (plain.float() + res.float()).to(torch.bfloat16)
+        got = awq.awq_linear_residual(x, packed, qz, s, res, group_size=128)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (m, k, n)
+        if k > 16384:
+            continue
+        res_k = random_x_gpu(m, k, seed=70 + i)
+        w = (1 + 0.1 * random_x_gpu(1, k, seed=80 + i).float()).to(torch.bfloat16).view(k)
+        xn, res_out = torch.empty_like(x), torch.empty_like(x)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        ws = torch.zeros(max(lib.workspace_bytes(m, k, n), 256), dtype=torch.uint8, device="cuda")
+        lib.gemm_rmsnorm(x, res_k, w, 1e-6, xn, res_out, packed, qz, s, y, n, ws, silu_mul=False)
+        assert torch.equal(res_out.view(torch.int16), (x.float() + res_k.float()).to(torch.bfloat16).view(torch.int16))
+        assert torch.equal(y.view(torch.int16), awq.awq_linear(xn, packed, qz, s, group_size=128).view(torch.int16)), (m, k, n)
