@@ -111,3 +111,33 @@ def test_random_shapes_residual_and_norm_calls(gpu_lib, seed):
         lib.gemm_rmsnorm(x, res_k, w, 1e-6, xn, res_out, packed, qz, s, y, n, ws, silu_mul=False)
         assert torch.equal(res_out.view(torch.int16), (x.float() + res_k.float()).to(torch.bfloat16).view(torch.int16))
         assert torch.equal(y.view(torch.int16), awq.awq_linear(xn, packed, qz, s, group_size=128).view(torch.int16)), (m, k, n)
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 4096, 6144), (16, 12288, 4096), (64, 4096, 4096), (600, 4096, 3072)])
+def test_special_activation_values_propagate_as_in_the_reference(gpu_lib, m, k, n):
+    """Rows of x holding +inf, -inf or NaN in one position (and one row of 1e30) go through
+    the decode kernel, K splits and the tile kernel: the positions of NaN, +inf and -inf in
+    y, and in the fused SiLU * up output, are those of the fp32 reference."""
+    awq = awq_mod()
+    qw, qz, s = random_awq_gpu(k, n, seed=77)
+    packed = awq.repack_awq_qweight(qw)
+    x = random_x_gpu(m, k, seed=78).float()
+    x[0, 5] = float("inf")
+    x[1, 100] = float("nan")
+    x[2, k - 1] = float("-inf")
+    if m > 3:
+        x[3] *= 1e30
+    x = x.to(torch.bfloat16)
+    w = awq.dequantize_awq_gemm(qw, qz, s, group_size=128).float()
+    ref = x.float() @ w
+    y = awq.awq_linear(x, packed, qz, s, group_size=128).float()
+    print(f"special values m={m} k={k} n={n} plan={gpu_lib.plan(m, k, n)}", flush=True)
+    for f in (torch.isnan, torch.isposinf, torch.isneginf):
+        assert torch.equal(f(y), f(ref)), (f.__name__, int((f(y) != f(ref)).sum()))
+    finite = torch.isfinite(ref) & (ref.abs() < 1e30)
+    assert_gemm_close(y[4:][finite[4:]].view(1, -1), ref[4:][finite[4:]].view(1, -1), (m, k, n))
+    f2 = awq.awq_linear_silu_mul(x, packed, qz, s, group_size=128).float()
+    gb, ub = ref[:, : n // 2].to(torch.bfloat16).float(), ref[:, n // 2:].to(torch.bfloat16).float()
+    ref2 = torch.nn.functional.silu(gb) * ub
+    for f in (torch.isnan, torch.isposinf, torch.isneginf):
+        assert torch.equal(f(f2), f(ref2)), ("silu", f.__name__, int((f(f2) != f(ref2)).sum()))
