@@ -115,3 +115,37 @@ def test_pack_int4_matches_oracle_and_reference_errors(cal):
         cal.pack_int4(torch.full((1, 8), 16, dtype=torch.int32, device="cuda"))
     with pytest.raises(TypeError, match="integer"):
         cal.pack_int4(torch.zeros((1, 8), device="cuda"))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("kind", ["constant", "huge_tiny", "signed_zeros", "dtype_extremes", "coarse_grid", "outlier"])
+def test_adversarial_groups_bit_exact(cal, dtype, kind):
+    """Groups built to stress the min / max / scale / round steps (awq_calibration.py:35-62):
+    constant groups (max - min = 0), rows scaled by 1e4 and 1e-6, signed zeros, values at the
+    dtype's largest magnitude beside subnormals, values on a coarse grid (exact ratios and
+    rounding ties), one outlier per row -- bit for bit against the oracle."""
+    gs, out_f, in_f = 128, 48, 384
+    w = np.random.default_rng(len(kind)).standard_normal((out_f, in_f)).astype(np.float32) * 0.05
+    if kind == "constant":
+        w[:, :gs] = 0.3
+    elif kind == "huge_tiny":
+        w[0] *= 1e4
+        w[1] *= 1e-6
+    elif kind == "signed_zeros":
+        w[2, ::2] = -0.0
+        w[2, 1::2] = 0.0
+    elif kind == "dtype_extremes":
+        big = 60000.0 if dtype == torch.float16 else 3e38
+        w[0, 0], w[0, 1] = big, -big
+        w[1] = 1e-7 if dtype == torch.float16 else 1e-40
+    elif kind == "coarse_grid":
+        w[3] = np.round(w[3] * 64) / 64
+    else:
+        w[:, 0] = 1000.0
+    wt = torch.from_numpy(w).to(dtype)
+    print(f"quantize adversarial {kind} {dtype}", flush=True)
+    p = cal.quantize_awq_weight(wt.cuda(), group_size=gs)
+    qw, qz, sc = ora.quantize_awq_weight(wt.float().numpy(), group_size=gs, out_dtype=ORACLE_DTYPE[dtype])
+    np.testing.assert_array_equal(p.qweight.cpu().numpy(), qw)
+    np.testing.assert_array_equal(p.qzeros.cpu().numpy(), qz)
+    np.testing.assert_array_equal(scale_array(p.scales), sc)
