@@ -145,7 +145,8 @@ def test_adversarial_groups_bit_exact(cal, dtype, kind):
     wt = torch.from_numpy(w).to(dtype)
     print(f"quantize adversarial {kind} {dtype}", flush=True)
     p = cal.quantize_awq_weight(wt.cuda(), group_size=gs)
-    qw, qz, sc = ora.quantize_awq_weight(wt.float().numpy(), group_size=gs, out_dtype=ORACLE_DTYPE[dtype])
+    with np.errstate(over="ignore"):  # max - min overflows to inf for the +-3e38 group
+        qw, qz, sc = ora.quantize_awq_weight(wt.float().numpy(), group_size=gs, out_dtype=ORACLE_DTYPE[dtype])
     np.testing.assert_array_equal(p.qweight.cpu().numpy(), qw)
     np.testing.assert_array_equal(p.qzeros.cpu().numpy(), qz)
     np.testing.assert_array_equal(scale_array(p.scales), sc)
