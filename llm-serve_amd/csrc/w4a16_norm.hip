@@ -160,16 +160,16 @@ hipError_t launch_rows(const uint16_t* x, const uint16_t* residual, const uint16
                                stride_inner, eps, stream);
   static_assert(kNormMaxK == 8 * 8 * kNormThreads, "whole-workgroup rows hold at most 8 chunks per lane");
   if (chunks <= kNormThreads)
-    return launch_whole<RES, 1>(x, residual, weight, x_norm, residual_out, M, K, rows_inner,
-                                            stride_outer, stride_inner, eps, stream);
+    return launch_whole<RES, 1>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                                 stride_inner, eps, stream);
   if (chunks <= 2 * kNormThreads)
-    return launch_whole<RES, 2>(x, residual, weight, x_norm, residual_out, M, K, rows_inner,
-                                            stride_outer, stride_inner, eps, stream);
+    return launch_whole<RES, 2>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                                 stride_inner, eps, stream);
   if (chunks <= 4 * kNormThreads)
-    return launch_whole<RES, 4>(x, residual, weight, x_norm, residual_out, M, K, rows_inner,
-                                            stride_outer, stride_inner, eps, stream);
+    return launch_whole<RES, 4>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
+                                 stride_inner, eps, stream);
   return launch_whole<RES, 8>(x, residual, weight, x_norm, residual_out, M, K, rows_inner, stride_outer,
-                                          stride_inner, eps, stream);
+                               stride_inner, eps, stream);
 }
 
 }  // namespace
